@@ -1,0 +1,268 @@
+"""Benchmark of the paged KV hot path on one MI355X.
+
+A step is one decode step of the hot path over one batch: append one new K/V row
+per sequence into its page (ivakv_append), then paged GQA decode attention over
+the whole context (ivakv_decode_attn: the paged walk + the split-K merge).
+Workload C2: 32 sequences, 32 query / 8 KV heads, head_dim 128, fp16, block 16,
+context lengths ~ U[512, 4096] (seed 0), values N(0, 1)/sqrt(128).
+
+Inputs are resident in HBM before timing.  To keep the 256 MiB MALL from
+serving repeated reads, steps rotate over --pools independent page pools
+(>= 1 GiB in total by default).  Each pool's step is captured once as a HIP
+graph (launch overhead of the three kernels is then the graph's, as in a
+production decode loop) and the graphs are replayed --steps times between two
+synchronisations.
+
+Output: one JSON line.  `value` is algorithmic GB/s of the whole step (append
+bytes + attention bytes, formulas in DESIGN.md) / step time.  `roofline` is for
+the dominant kernel (the paged walk, decode_partial_kernel): its algorithmic
+bytes / its average duration measured here with HIP events over a graph of
+back-to-back launches on the launch stream.  `cpu_baseline` times the CPU
+restatement of the reference's torch path (contiguous cache + torch.cat append +
+AttentionTorch math, fp32) on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged decode-attn + KV append GB/s and % HBM peak; decode tokens/s at 1 GPU"
+PROFILE_TRAFFIC = ROOT / "profiles" / "decode_attn_c2_traffic.json"
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--pools", type=int, default=4, help="independent KV pools rotated per step")
+    p.add_argument("--partition-pages", type=int, default=0, help="0 = library default")
+    p.add_argument("--kernel-launches", type=int, default=200,
+                   help="launches of the paged walk timed for the roofline figure")
+    p.add_argument("--cpu-reps", type=int, default=10, help="timed CPU-baseline reps (0 = skip)")
+    p.add_argument("--eager", action="store_true", help="time eager launches instead of graphs")
+    return p.parse_args()
+
+
+def algorithmic_bytes(lengths, hq, hkv, d, esize, bs=16):
+    """Per-step algorithmic bytes: append of one row per sequence, decode attention."""
+    b = len(lengths)
+    append = 2 * b * hkv * d * esize + 4 * b
+    attn = (sum(2 * n * hkv * d * esize for n in lengths)   # K + V of attended rows
+            + 2 * b * hq * d * esize                          # q in, out
+            + sum(4 * math.ceil(n / bs) for n in lengths)     # block-table entries
+            + 4 * b)                                          # context lengths
+    return append, attn
+
+
+def cpu_baseline(lengths, hq, hkv, d, reps, seed=0):
+    """Times the CPU restatement of the reference torch path on a padded fp32 batch."""
+    import torch
+    from oracle import reference_path as rp
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(seed)
+    b, lmax = len(lengths), max(lengths)
+    lens = torch.tensor(lengths)
+    sc = 1 / math.sqrt(d)
+    ck = torch.randn(b, hkv, lmax - 1, d, generator=g) * sc
+    cv = torch.randn(b, hkv, lmax - 1, d, generator=g) * sc
+    valid = torch.arange(lmax - 1)[None] < (lens[:, None] - 1)
+    q = torch.randn(b, hq, 1, d, generator=g) * sc
+    kn = torch.randn(b, hkv, 1, d, generator=g) * sc
+    vn = torch.randn(b, hkv, 1, d, generator=g) * sc
+    for _ in range(3):
+        rp.reference_decode_step(ck, cv, valid, lens, q, kn, vn, sc)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        rp.reference_decode_step(ck, cv, valid, lens, q, kn, vn, sc)
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), threads
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                          "(the multi-GPU sharding of the path is described in DESIGN.md)"}))
+        sys.exit(2)
+
+    import torch
+    import __graft_entry__
+
+    iva = __graft_entry__.load_package()
+    iva._abi.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = iva.workloads
+
+    hq, hkv, d, dtype, esize = 32, 8, 128, torch.float16, 2
+    lengths = wl.c2_lengths(seed=0)
+    batch = len(lengths)
+    sc = 1 / math.sqrt(d)
+    sets = []
+    for i in range(args.pools):
+        dd = wl.decode_batch(lengths, hq, hkv, d, dtype, seed=100 + i, device=dev, scale=sc)
+        lay = dd["layout"]
+        bt = lay.block_tables.to(dev)
+        ctx = lay.context_lens.to(dev)
+        pos = torch.tensor([n - 1 for n in lengths])
+        slots = torch.stack([lay.slots(b, pos[b]) for b in range(batch)]).to(dev)
+        gen = torch.Generator(device=dev).manual_seed(500 + i)
+        k_new = (torch.randn(batch, hkv, d, generator=gen, device=dev) * sc).to(dtype)
+        v_new = (torch.randn(batch, hkv, d, generator=gen, device=dev) * sc).to(dtype)
+        sets.append(dict(q=dd["q"], k_pool=dd["k_pool"], v_pool=dd["v_pool"], bt=bt, ctx=ctx,
+                         slots=slots, k_new=k_new, v_new=v_new, out=torch.empty_like(dd["q"])))
+    pool_bytes = sum(s["k_pool"].numel() * esize * 2 for s in sets)
+    max_blocks = sets[0]["bt"].shape[1]
+    ws_bytes = iva.decode_workspace_bytes(batch, hq, hkv, d, 16, max_blocks,
+                                          partition_pages=args.partition_pages)
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    pp = args.partition_pages or None
+
+    def step(s):
+        iva.kv_append(s["k_new"], s["v_new"], s["k_pool"], s["v_pool"], s["slots"])
+        iva.paged_decode_attention(s["q"], s["k_pool"], s["v_pool"], s["bt"], s["ctx"],
+                                   partition_pages=pp, out=s["out"], workspace=workspace)
+
+    def walk(s):
+        iva.paged_decode_attention_partial(s["q"], s["k_pool"], s["v_pool"], s["bt"], s["ctx"],
+                                           partition_pages=pp, out=s["out"], workspace=workspace)
+
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        for s in sets:  # warm every code path before capture
+            step(s)
+            walk(s)
+        torch.cuda.synchronize(dev)
+
+        def make_graph(fn, reps):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for r in range(reps):
+                    fn(sets[r % len(sets)])
+            return g
+
+        step_graph = None if args.eager else make_graph(step, len(sets))
+        per_graph = len(sets) * max(1, 20 // len(sets))
+        walk_graph = None if args.eager else make_graph(walk, per_graph)
+
+        def run_steps(n):
+            if step_graph is None:
+                for i in range(n):
+                    step(sets[i % len(sets)])
+            else:
+                for _ in range(n // len(sets)):
+                    step_graph.replay()
+                for i in range(n % len(sets)):
+                    step(sets[i])
+
+        run_steps(args.warmup)
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        run_steps(args.steps)
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        step_ms = e0.elapsed_time(e1) / args.steps
+
+        # dominant kernel alone: back-to-back launches of the paged walk
+        launches = 0
+        k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        if walk_graph is not None:
+            walk_graph.replay()
+            torch.cuda.synchronize(dev)
+            reps = max(1, args.kernel_launches // per_graph)
+            k0.record(stream)
+            for _ in range(reps):
+                walk_graph.replay()
+            k1.record(stream)
+            launches = reps * per_graph
+        else:
+            k0.record(stream)
+            for i in range(args.kernel_launches):
+                walk(sets[i % len(sets)])
+            k1.record(stream)
+            launches = args.kernel_launches
+        torch.cuda.synchronize(dev)
+        walk_us = k0.elapsed_time(k1) * 1e3 / launches
+
+    append_b, attn_b = algorithmic_bytes(lengths, hq, hkv, d, esize)
+    step_s = step_ms * 1e-3
+    value = (append_b + attn_b) / step_s / 1e9
+    achieved = attn_b / (walk_us * 1e-6) / 1e9
+
+    traffic = None
+    if PROFILE_TRAFFIC.exists():
+        try:
+            traffic = json.loads(PROFILE_TRAFFIC.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    cpu = None
+    if args.cpu_reps > 0:
+        t_cpu, threads = cpu_baseline(lengths, hq, hkv, d, args.cpu_reps)
+        cpu = {"value": round((append_b + attn_b) / t_cpu / 1e9, 3), "unit": "GB/s",
+               "cores": threads, "kind": "port",
+               "sample": (f"full C2 batch ({batch} seqs), one decode step of the reference torch "
+                          f"path restated on CPU in fp32 (torch.cat append + AttentionTorch math), "
+                          f"median of {args.cpu_reps} reps after 3 warm-ups, "
+                          f"{t_cpu * 1e3:.1f} ms/step, {cpu_model()}"),
+               "ms_per_step": round(t_cpu * 1e3, 2)}
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "C2 paged decode attention + 1-row KV append per sequence",
+                   "batch": batch, "num_q_heads": hq, "num_kv_heads": hkv, "head_dim": d,
+                   "block_size": 16, "context": "U[512,4096] seed 0",
+                   "mean_context": round(sum(lengths) / batch, 1), "pools_rotated": args.pools,
+                   "pool_bytes_total": pool_bytes, "launch": "eager" if args.eager else "hip graph",
+                   "partition_pages": args.partition_pages or 16},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "kernel": "decode_partial_kernel<f16,128>",
+                     "kernel_us": round(walk_us, 3), "algorithmic_bytes": attn_b},
+        "cpu_baseline": cpu,
+        "tokens_per_s": round(batch / step_s, 1),
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "step_bytes": {"append": append_b, "attention": attn_b},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

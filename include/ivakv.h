@@ -1,0 +1,186 @@
+/*
+ * ivakv.h -- C ABI of libivakv.so, the MI355X (gfx950) paged KV-cache library.
+ *
+ * Scope: the paged KV-cache hot path of IVA1.0 -- appending new K/V rows into
+ * block-table pages, gathering pages back to contiguous K/V, and paged
+ * single-query (decode) attention with grouped-query heads, sliding window and
+ * attention sinks -- plus the reference's index gather/scatter op.
+ *
+ * Conventions
+ *   - Every entry point returns IVAKV_OK (0) or a negative IVAKV_E_* code and
+ *     never throws across the ABI.  On error, ivakv_last_error() returns a
+ *     thread-local message describing it.
+ *   - All pointers except `stream` and host scalars are DEVICE pointers owned by
+ *     the caller (the library never allocates or frees device memory).
+ *   - Work is enqueued asynchronously on `stream` (NULL = the default stream).
+ *     Argument checks run on the host before any launch.
+ *   - Integer indices read from device memory (slot ids, page ids, context
+ *     lengths, positions) are bounds-checked inside the kernels: an out-of-range
+ *     slot is skipped by append/scatter, an out-of-range page reads as empty.
+ *
+ * Paged pool layout (esize = bytes per element, X = 16 / esize, BS = block_size):
+ *   k_pool = [num_pages][Hkv][D / X][BS][X]   K(page,h,t,d) at ((d/X)*BS + t)*X + d%X
+ *   v_pool = [num_pages][Hkv][D][BS]          V(page,h,t,d) at d*BS + t
+ * Both pools are dense.  A slot s names page s / BS, in-page row s % BS.
+ * A 16-row page of one KV head is 16*D*esize contiguous bytes for K and for V
+ * (4 KiB each at D=128 fp16): one page is a handful of fully-coalesced 1 KiB
+ * wavefront loads, already in the operand order of the 16x16 MFMA tiles.
+ *
+ * Reference interfaces replaced (paths relative to the IVA1.0 source tree):
+ *   src/core/rope_kv.py:71-137        KVCache (contiguous [B,H,S,D] cache)
+ *   src/core/attention.py:61-102      AttentionTorch.forward cache append + math
+ *   src/kernels_t/kv_ops_triton.py:18-156  kv_gather/kv_scatter kernels, kv_ops_triton
+ */
+#ifndef IVAKV_H
+#define IVAKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IVAKV_ABI_VERSION 1
+
+/* status codes */
+#define IVAKV_OK            0
+#define IVAKV_E_ARG        -1  /* null pointer, negative size, bad stride */
+#define IVAKV_E_DTYPE      -2  /* unknown dtype code */
+#define IVAKV_E_SHAPE      -3  /* geometry the kernels do not support */
+#define IVAKV_E_LAUNCH     -4  /* HIP reported an error at launch */
+#define IVAKV_E_WORKSPACE  -5  /* workspace missing or too small */
+
+/* dtype codes (element type of K, V, Q and outputs) */
+#define IVAKV_F32   0
+#define IVAKV_F16   1
+#define IVAKV_BF16  2
+
+/* ABI version compiled into the library (== IVAKV_ABI_VERSION). */
+int ivakv_abi_version(void);
+
+/* Thread-local description of the last error returned on this thread. */
+const char* ivakv_last_error(void);
+
+/*
+ * Append: scatter n_tok new K/V rows into their slots.
+ *   k_new(t, h, d) = k_new[t*k_tok_stride + h*k_head_stride + d]   (elements)
+ *   slot_mapping[t] = slot of token t; -1 (or any id outside
+ *   [0, num_pages*block_size)) leaves the pools untouched for that token.
+ * Bit-exact data movement.  Duplicate slots in one call: one of the writers
+ * wins (unspecified which), as for the reference scatter.
+ * Replaces: KVCache.update slice-assign (src/core/rope_kv.py:98-110), the
+ * torch.cat append (src/core/attention.py:61-63) and the scatter branch of
+ * KVOpsTriton (src/kernels_t/kv_ops_triton.py:43-65,125-140).
+ */
+int ivakv_append(const void* k_new, const void* v_new,
+                 int64_t k_tok_stride, int64_t k_head_stride,
+                 int64_t v_tok_stride, int64_t v_head_stride,
+                 void* k_pool, void* v_pool, const int32_t* slot_mapping,
+                 int n_tok, int num_kv_heads, int head_dim, int block_size,
+                 int num_pages, int dtype, hipStream_t stream);
+
+/*
+ * Gather: pages -> contiguous k_out/v_out = [batch][Hkv][out_len][D] (dense).
+ * Row p < min(context_lens[b], out_len) of sequence b comes from slot
+ * block_tables[b*max_blocks + p/BS]*BS + p%BS; all other rows are zero.
+ * Output keeps the pool dtype.  Bit-exact data movement.
+ * Replaces: KVCache.get_slice / .k / .v (src/core/rope_kv.py:136-137) and the
+ * gather branch of KVOpsTriton (src/kernels_t/kv_ops_triton.py:18-40,111-123).
+ */
+int ivakv_gather(const void* k_pool, const void* v_pool,
+                 const int32_t* block_tables, const int32_t* context_lens,
+                 int batch, int max_blocks, int num_kv_heads, int head_dim,
+                 int block_size, int num_pages, int out_len,
+                 void* k_out, void* v_out, int dtype, hipStream_t stream);
+
+/*
+ * Bytes of device workspace ivakv_decode_attn needs for this geometry
+ * (fp32 partial accumulators + per-partition max/sum).  partition_pages <= 0
+ * selects the library default.
+ */
+int ivakv_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
+                                int head_dim, int block_size, int max_blocks,
+                                int window, int n_sink, int partition_pages,
+                                size_t* bytes);
+
+/*
+ * Paged decode attention (one query row per sequence):
+ *   out[b, hq, :] = softmax_j(scale * q[b,hq,:] . K_b[j,:]) V_b[j,:]
+ * over the visible positions j of sequence b, with L = context_lens[b]:
+ *   j < L  and  (window <= 0  or  j >= L - window  or  j < n_sink).
+ * KV head of query head hq is hq / (num_q_heads / num_kv_heads).
+ * q, out = [batch][num_q_heads][D] dense.  L == 0 gives a zero row.
+ * fp32 accumulation; the context is split into partitions of
+ * partition_pages pages that are merged with a log-sum-exp reduction.
+ * Supported: block_size 16, head_dim 64/128/256, num_q_heads/num_kv_heads
+ * in {1,2,4,8,16}.
+ * Replaces: the cache branch of AttentionTorch.forward -- scores, causal /
+ * sliding-window / sink masks, softmax, PV (src/core/attention.py:77-102,
+ * 115-148) -- on the paged cache.
+ */
+int ivakv_decode_attn(const void* q, const void* k_pool, const void* v_pool,
+                      const int32_t* block_tables, const int32_t* context_lens,
+                      void* out, void* workspace, size_t workspace_bytes,
+                      int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                      int block_size, int max_blocks, int num_pages, float scale,
+                      int window, int n_sink, int partition_pages, int dtype,
+                      hipStream_t stream);
+
+/*
+ * The two halves of ivakv_decode_attn, same arguments.  _partial runs the
+ * paged walk (and writes `out` directly for sequences that fit in one
+ * partition); _merge folds the per-partition (max, sum, acc) triples into
+ * `out`.  Exposed so a caller can time the walk alone or merge partials that
+ * come from several devices (context-parallel sharding of one sequence).
+ * Replaces: same reference code as ivakv_decode_attn.
+ */
+int ivakv_decode_attn_partial(const void* q, const void* k_pool, const void* v_pool,
+                              const int32_t* block_tables, const int32_t* context_lens,
+                              void* out, void* workspace, size_t workspace_bytes,
+                              int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                              int block_size, int max_blocks, int num_pages, float scale,
+                              int window, int n_sink, int partition_pages, int dtype,
+                              hipStream_t stream);
+int ivakv_decode_attn_merge(const void* q, const void* k_pool, const void* v_pool,
+                            const int32_t* block_tables, const int32_t* context_lens,
+                            void* out, void* workspace, size_t workspace_bytes,
+                            int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                            int block_size, int max_blocks, int num_pages, float scale,
+                            int window, int n_sink, int partition_pages, int dtype,
+                            hipStream_t stream);
+
+/*
+ * Index gather on a contiguous-layout cache kv = [batch][n_heads][seq_len][D]
+ * with element strides (s_b, s_h, s_s, s_d):
+ *   out[b, h, j, :] = kv[b, h, indices[j], :]      out = [B][H][n_idx][D] dense
+ * indices are int64 on the device, shared by every (b, h).  An index outside
+ * [0, seq_len) yields a zero row.
+ * Replaces: kv_gather_kernel + the gather branch of KVOpsTriton
+ * (src/kernels_t/kv_ops_triton.py:18-40,111-123).
+ */
+int ivakv_index_gather(const void* kv, int64_t s_b, int64_t s_h, int64_t s_s, int64_t s_d,
+                       const int64_t* indices, int n_idx,
+                       int batch, int n_heads, int seq_len, int head_dim,
+                       void* out, int dtype, hipStream_t stream);
+
+/*
+ * Index scatter, in place: kv[b, h, indices[j], :] = values[b, h, j, :] with
+ * values strides (v_b, v_h, v_s, v_d).  Indices outside [0, seq_len) are
+ * skipped; duplicate indices leave one of the written rows (unspecified which).
+ * Replaces: kv_scatter_kernel + the scatter branch of KVOpsTriton
+ * (src/kernels_t/kv_ops_triton.py:43-65,125-140); the functional (clone, then
+ * scatter) form is kept by the Python op.
+ */
+int ivakv_index_scatter(void* kv, int64_t s_b, int64_t s_h, int64_t s_s, int64_t s_d,
+                        const int64_t* indices, int n_idx,
+                        const void* values, int64_t v_b, int64_t v_h, int64_t v_s, int64_t v_d,
+                        int batch, int n_heads, int seq_len, int head_dim,
+                        int dtype, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IVAKV_H */

@@ -1,0 +1,37 @@
+"""MI355X-native paged KV-cache hot path of IVA1.0.
+
+Host side in Python on PyTorch-ROCm (tensors, streams, the page allocator);
+compute in hand-written gfx950 HIP kernels behind the C ABI of
+include/ivakv.h (libivakv.so, bound with ctypes in ``_abi``).
+
+The directory name is not a Python identifier; load it with
+``__graft_entry__.load_package()``, which registers it as ``iva_amd``.
+"""
+from . import _abi, workloads
+from .ops import (
+    chunk_elems,
+    decode_workspace_bytes,
+    dtype_code,
+    kv_append,
+    kv_gather,
+    kv_ops,
+    paged_decode_attention,
+    paged_decode_attention_merge,
+    paged_decode_attention_partial,
+    pool_geometry,
+    pool_shapes,
+)
+
+__all__ = [
+    "chunk_elems",
+    "decode_workspace_bytes",
+    "dtype_code",
+    "kv_append",
+    "kv_gather",
+    "kv_ops",
+    "paged_decode_attention",
+    "paged_decode_attention_merge",
+    "paged_decode_attention_partial",
+    "pool_geometry",
+    "pool_shapes",
+]

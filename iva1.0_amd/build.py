@@ -1,0 +1,72 @@
+"""Builds libivakv.so (the gfx950 HIP kernels behind the C ABI in include/ivakv.h).
+
+One hipcc invocation compiles every ``csrc/*.hip`` translation unit for gfx950
+and links them into ``libivakv.so`` next to this file.  The library is written
+to a temporary name first and renamed, so a concurrent reader never maps a
+half-written file.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO_ROOT = PKG_DIR.parent
+CSRC = PKG_DIR / "csrc"
+INCLUDE = REPO_ROOT / "include"
+LIB_NAME = "libivakv.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+OFFLOAD_ARCH = "gfx950"
+
+# Packed-FP32 VALU ops (v_pk_fma_f32 and friends) are disabled for device code;
+# the host pass prints a harmless "not a recognized feature" warning for it.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def hipcc_path() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: set HIPCC or install ROCm")
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def build(verbose: bool = False) -> Path:
+    """Compiles all HIP sources into ``libivakv.so``; returns its path."""
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    tmp = LIB_PATH.with_name(LIB_NAME + f".tmp{os.getpid()}")
+    cmd = [
+        hipcc_path(),
+        f"--offload-arch={OFFLOAD_ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-Wall",
+        "-Wno-unused-command-line-argument",
+        f"-I{INCLUDE}",
+        f"-I{CSRC}",
+        *DEVICE_FLAGS,
+        "-o",
+        str(tmp),
+        *[str(s) for s in srcs],
+    ]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        tmp.unlink(missing_ok=True)
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,317 @@
+// Bit-exact KV data movement on gfx950: paged append (scatter into slots), paged
+// gather (pages -> contiguous rows) and the index gather/scatter of a contiguous
+// [B, H, S, D] cache.  Elements are moved as raw 16/32-bit words, so every
+// kernel here is exact for any dtype of that size.
+//
+// All kernels are HBM-bound copies: each thread moves one 16-byte chunk
+// (8 half / 4 float elements) per row, so a wavefront reads or writes 1 KiB
+// per instruction in the layout-favoured direction.
+#include "ivakv_internal.h"
+
+namespace ivakv {
+namespace {
+
+struct alignas(16) Chunk16 {
+  uint32_t w[4];
+};
+
+// ---------------------------------------------------------------------------
+// append: new rows [n_tok][Hkv][D] (strided) -> k_pool / v_pool slots
+// ---------------------------------------------------------------------------
+struct AppendArgs {
+  const void* k_new;
+  const void* v_new;
+  int64_t kts, khs, vts, vhs;  // element strides (token, head)
+  void* k_pool;
+  void* v_pool;
+  const int32_t* slots;
+  int n_tok, Hkv, D, bs;
+  int64_t n_slots;  // num_pages * bs
+};
+
+// One thread per (token, head, 16-byte chunk of the row); chunk index varies
+// fastest so a wavefront reads consecutive bytes of the new rows.
+template <typename E, bool VEC>
+__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
+  constexpr int X = 16 / sizeof(E);
+  const int nch = a.D / X;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)a.n_tok * a.Hkv * nch;
+  if (gid >= total) return;
+  const int c = (int)(gid % nch);
+  const int64_t th = gid / nch;
+  const int h = (int)(th % a.Hkv);
+  const int64_t t = th / a.Hkv;
+  const int64_t slot = a.slots[t];
+  if (slot < 0 || slot >= a.n_slots) return;
+  const int64_t page = slot / a.bs;
+  const int off = (int)(slot - page * a.bs);
+  const int64_t head_base = page * a.Hkv + h;
+
+  const E* ks = static_cast<const E*>(a.k_new) + t * a.kts + h * a.khs + (int64_t)c * X;
+  const E* vs = static_cast<const E*>(a.v_new) + t * a.vts + h * a.vhs + (int64_t)c * X;
+  E* kd = static_cast<E*>(a.k_pool) + ((head_base * nch + c) * a.bs + off) * X;
+  E* vd = static_cast<E*>(a.v_pool) + head_base * a.D * a.bs + (int64_t)c * X * a.bs + off;
+
+  if constexpr (VEC) {
+    *reinterpret_cast<Chunk16*>(kd) = *reinterpret_cast<const Chunk16*>(ks);
+    union {
+      Chunk16 c16;
+      E e[X];
+    } v;
+    v.c16 = *reinterpret_cast<const Chunk16*>(vs);
+#pragma unroll
+    for (int i = 0; i < X; ++i) vd[(int64_t)i * a.bs] = v.e[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < X; ++i) kd[i] = ks[i];
+#pragma unroll
+    for (int i = 0; i < X; ++i) vd[(int64_t)i * a.bs] = vs[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gather: pages -> k_out / v_out = [B][Hkv][out_len][D]
+// ---------------------------------------------------------------------------
+struct GatherArgs {
+  const void* k_pool;
+  const void* v_pool;
+  const int32_t* bt;
+  const int32_t* ctx;
+  int max_blocks, Hkv, D, bs, num_pages, out_len;
+  void* k_out;
+  void* v_out;
+};
+
+// Grid (logical page, kv head, sequence).  Thread index = chunk * bs + row, so
+// the K page (stored [D/X][bs][X]) is read as one contiguous run and each
+// 16-byte V chunk is assembled from X row-adjacent elements of the [D][bs]
+// page (consecutive lanes read consecutive rows).
+template <typename E>
+__global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
+  constexpr int X = 16 / sizeof(E);
+  const int j = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int nch = a.D / X;
+  int L = a.ctx[b];
+  L = L < 0 ? 0 : L;
+  const int lim = L < a.out_len ? L : a.out_len;
+  int64_t phys = -1;
+  if (j < a.max_blocks && (int64_t)j * a.bs < lim) {
+    const int64_t p = a.bt[(int64_t)b * a.max_blocks + j];
+    if (p >= 0 && p < a.num_pages) phys = p;
+  }
+  const int rows = nch * a.bs;
+  for (int idx = threadIdx.x; idx < rows; idx += blockDim.x) {
+    const int t = idx % a.bs;
+    const int c = idx / a.bs;
+    const int64_t pos = (int64_t)j * a.bs + t;
+    if (pos >= a.out_len) continue;
+    const int64_t orow = (((int64_t)b * a.Hkv + h) * a.out_len + pos) * a.D + (int64_t)c * X;
+    union {
+      Chunk16 c16;
+      E e[X];
+    } kv, vv;
+    kv.c16 = Chunk16{{0u, 0u, 0u, 0u}};
+    vv.c16 = Chunk16{{0u, 0u, 0u, 0u}};
+    if (phys >= 0 && pos < lim) {
+      const int64_t head_base = phys * a.Hkv + h;
+      kv.c16 = *reinterpret_cast<const Chunk16*>(static_cast<const E*>(a.k_pool) +
+                                                  ((head_base * nch + c) * a.bs + t) * X);
+      const E* vb = static_cast<const E*>(a.v_pool) + head_base * a.D * a.bs + (int64_t)c * X * a.bs + t;
+#pragma unroll
+      for (int i = 0; i < X; ++i) vv.e[i] = vb[(int64_t)i * a.bs];
+    }
+    *reinterpret_cast<Chunk16*>(static_cast<E*>(a.k_out) + orow) = kv.c16;
+    *reinterpret_cast<Chunk16*>(static_cast<E*>(a.v_out) + orow) = vv.c16;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// index gather / scatter on a contiguous-layout [B][H][S][D] cache
+// ---------------------------------------------------------------------------
+struct IndexArgs {
+  const void* src;
+  void* dst;
+  int64_t s_b, s_h, s_s, s_d;  // strides of the indexed cache
+  int64_t o_b, o_h, o_s, o_d;  // strides of the dense side (gather out / scatter values)
+  const int64_t* idx;
+  int n_idx, H, S, D;
+  int64_t total;
+};
+
+// One thread per (b, h, j, chunk).  GATHER: out[b,h,j] = kv[b,h,idx[j]] (zero
+// row for an out-of-range index).  SCATTER: kv[b,h,idx[j]] = values[b,h,j]
+// (out-of-range index skipped).
+template <typename E, bool VEC, bool GATHER>
+__global__ __launch_bounds__(256) void index_copy_kernel(IndexArgs a) {
+  constexpr int X = VEC ? 16 / (int)sizeof(E) : 1;
+  const int per_row = a.D / X;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= a.total) return;
+  const int e = (int)(gid % per_row);
+  int64_t r = gid / per_row;
+  const int j = (int)(r % a.n_idx);
+  r /= a.n_idx;
+  const int h = (int)(r % a.H);
+  const int64_t b = r / a.H;
+  const int64_t ix = a.idx[j];
+  const bool ok = ix >= 0 && ix < a.S;
+  const int64_t cache_row = b * a.s_b + h * a.s_h + ix * a.s_s + (int64_t)e * X * a.s_d;
+  const int64_t dense_row = b * a.o_b + h * a.o_h + (int64_t)j * a.o_s + (int64_t)e * X * a.o_d;
+  if constexpr (GATHER) {
+    E* o = static_cast<E*>(a.dst) + dense_row;
+    if constexpr (VEC) {
+      Chunk16 v{{0u, 0u, 0u, 0u}};
+      if (ok) v = *reinterpret_cast<const Chunk16*>(static_cast<const E*>(a.src) + cache_row);
+      *reinterpret_cast<Chunk16*>(o) = v;
+    } else {
+      *o = ok ? static_cast<const E*>(a.src)[cache_row] : E(0);
+    }
+  } else {
+    if (!ok) return;
+    E* o = static_cast<E*>(a.dst) + cache_row;
+    const E* s = static_cast<const E*>(a.src) + dense_row;
+    if constexpr (VEC) {
+      *reinterpret_cast<Chunk16*>(o) = *reinterpret_cast<const Chunk16*>(s);
+    } else {
+      *o = *s;
+    }
+  }
+}
+
+inline unsigned blocks_for(int64_t total, int per_block) {
+  return (unsigned)((total + per_block - 1) / per_block);
+}
+
+constexpr int64_t kMaxGrid = 2147483647LL;
+
+}  // namespace
+}  // namespace ivakv
+
+using namespace ivakv;
+
+extern "C" int ivakv_append(const void* k_new, const void* v_new, int64_t k_tok_stride,
+                            int64_t k_head_stride, int64_t v_tok_stride, int64_t v_head_stride,
+                            void* k_pool, void* v_pool, const int32_t* slot_mapping, int n_tok,
+                            int num_kv_heads, int head_dim, int block_size, int num_pages,
+                            int dtype, hipStream_t stream) {
+  const int es = dtype_size(dtype);
+  if (es == 0) return fail(IVAKV_E_DTYPE, "ivakv_append: unknown dtype code %d", dtype);
+  if (n_tok < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_pages < 0)
+    return fail(IVAKV_E_ARG,
+                "ivakv_append: bad sizes n_tok=%d Hkv=%d D=%d block_size=%d num_pages=%d", n_tok,
+                num_kv_heads, head_dim, block_size, num_pages);
+  const int X = 16 / es;
+  if (head_dim % X != 0)
+    return fail(IVAKV_E_SHAPE, "ivakv_append: head_dim %d must be a multiple of %d", head_dim, X);
+  if (n_tok == 0) return IVAKV_OK;
+  if (!k_new || !v_new || !k_pool || !v_pool || !slot_mapping)
+    return fail(IVAKV_E_ARG, "ivakv_append: null pointer argument");
+  if (k_tok_stride < 0 || k_head_stride < 0 || v_tok_stride < 0 || v_head_stride < 0)
+    return fail(IVAKV_E_ARG, "ivakv_append: negative stride");
+  AppendArgs a{k_new, v_new, k_tok_stride, k_head_stride, v_tok_stride, v_head_stride,
+               k_pool, v_pool, slot_mapping, n_tok, num_kv_heads, head_dim, block_size,
+               (int64_t)num_pages * block_size};
+  const bool vec = aligned16(k_new) && aligned16(v_new) && aligned16(k_pool) && aligned16(v_pool) &&
+                   (k_tok_stride % X == 0) && (k_head_stride % X == 0) &&
+                   (v_tok_stride % X == 0) && (v_head_stride % X == 0);
+  const int64_t total = (int64_t)n_tok * num_kv_heads * (head_dim / X);
+  const unsigned grid = blocks_for(total, 256);
+  if ((int64_t)grid > kMaxGrid) return fail(IVAKV_E_SHAPE, "ivakv_append: too many rows");
+  if (es == 4) {
+    if (vec) append_kernel<uint32_t, true><<<grid, 256, 0, stream>>>(a);
+    else append_kernel<uint32_t, false><<<grid, 256, 0, stream>>>(a);
+  } else {
+    if (vec) append_kernel<uint16_t, true><<<grid, 256, 0, stream>>>(a);
+    else append_kernel<uint16_t, false><<<grid, 256, 0, stream>>>(a);
+  }
+  return launch_status("ivakv_append");
+}
+
+extern "C" int ivakv_gather(const void* k_pool, const void* v_pool, const int32_t* block_tables,
+                            const int32_t* context_lens, int batch, int max_blocks,
+                            int num_kv_heads, int head_dim, int block_size, int num_pages,
+                            int out_len, void* k_out, void* v_out, int dtype,
+                            hipStream_t stream) {
+  const int es = dtype_size(dtype);
+  if (es == 0) return fail(IVAKV_E_DTYPE, "ivakv_gather: unknown dtype code %d", dtype);
+  if (batch < 0 || max_blocks < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
+      num_pages < 0 || out_len < 0)
+    return fail(IVAKV_E_ARG,
+                "ivakv_gather: bad sizes B=%d max_blocks=%d Hkv=%d D=%d block_size=%d "
+                "num_pages=%d out_len=%d",
+                batch, max_blocks, num_kv_heads, head_dim, block_size, num_pages, out_len);
+  const int X = 16 / es;
+  if (head_dim % X != 0)
+    return fail(IVAKV_E_SHAPE, "ivakv_gather: head_dim %d must be a multiple of %d", head_dim, X);
+  if (batch == 0 || out_len == 0) return IVAKV_OK;
+  if (!k_pool || !v_pool || !context_lens || !k_out || !v_out || (max_blocks > 0 && !block_tables))
+    return fail(IVAKV_E_ARG, "ivakv_gather: null pointer argument");
+  if (!aligned16(k_pool) || !aligned16(v_pool) || !aligned16(k_out) || !aligned16(v_out))
+    return fail(IVAKV_E_ARG, "ivakv_gather: pools and outputs must be 16-byte aligned");
+  if (batch > 65535 || num_kv_heads > 65535)
+    return fail(IVAKV_E_SHAPE, "ivakv_gather: batch and num_kv_heads must be <= 65535");
+  GatherArgs a{k_pool, v_pool, block_tables, context_lens, max_blocks, num_kv_heads, head_dim,
+               block_size, num_pages, out_len, k_out, v_out};
+  dim3 grid((unsigned)cdiv(out_len, block_size), (unsigned)num_kv_heads, (unsigned)batch);
+  if (es == 4) gather_kernel<uint32_t><<<grid, 256, 0, stream>>>(a);
+  else gather_kernel<uint16_t><<<grid, 256, 0, stream>>>(a);
+  return launch_status("ivakv_gather");
+}
+
+namespace {
+
+int index_copy(bool gather, const char* name, const void* src, void* dst, int64_t s_b, int64_t s_h,
+               int64_t s_s, int64_t s_d, int64_t o_b, int64_t o_h, int64_t o_s, int64_t o_d,
+               const int64_t* indices, int n_idx, int batch, int n_heads, int seq_len,
+               int head_dim, int dtype, hipStream_t stream) {
+  const int es = dtype_size(dtype);
+  if (es == 0) return fail(IVAKV_E_DTYPE, "%s: unknown dtype code %d", name, dtype);
+  if (n_idx < 0 || batch < 0 || n_heads < 0 || seq_len < 0 || head_dim < 0)
+    return fail(IVAKV_E_ARG, "%s: negative size", name);
+  const int64_t rows = (int64_t)batch * n_heads * n_idx;
+  if (rows == 0 || head_dim == 0) return IVAKV_OK;
+  if (!src || !dst || !indices) return fail(IVAKV_E_ARG, "%s: null pointer argument", name);
+  const int X = 16 / es;
+  const bool vec = s_d == 1 && o_d == 1 && head_dim % X == 0 && aligned16(src) && aligned16(dst) &&
+                   s_b % X == 0 && s_h % X == 0 && s_s % X == 0 && o_b % X == 0 &&
+                   o_h % X == 0 && o_s % X == 0;
+  IndexArgs a{src, dst, s_b, s_h, s_s, s_d, o_b, o_h, o_s, o_d, indices, n_idx, n_heads, seq_len,
+              head_dim, rows * (vec ? head_dim / X : head_dim)};
+  const unsigned grid = blocks_for(a.total, 256);
+  if ((int64_t)grid > kMaxGrid) return fail(IVAKV_E_SHAPE, "%s: too many rows", name);
+#define IVAKV_IDX_LAUNCH(E)                                                              \
+  do {                                                                                   \
+    if (gather) {                                                                        \
+      if (vec) index_copy_kernel<E, true, true><<<grid, 256, 0, stream>>>(a);            \
+      else index_copy_kernel<E, false, true><<<grid, 256, 0, stream>>>(a);               \
+    } else {                                                                             \
+      if (vec) index_copy_kernel<E, true, false><<<grid, 256, 0, stream>>>(a);           \
+      else index_copy_kernel<E, false, false><<<grid, 256, 0, stream>>>(a);              \
+    }                                                                                    \
+  } while (0)
+  if (es == 4) IVAKV_IDX_LAUNCH(uint32_t);
+  else IVAKV_IDX_LAUNCH(uint16_t);
+#undef IVAKV_IDX_LAUNCH
+  return launch_status(name);
+}
+
+}  // namespace
+
+extern "C" int ivakv_index_gather(const void* kv, int64_t s_b, int64_t s_h, int64_t s_s,
+                                  int64_t s_d, const int64_t* indices, int n_idx, int batch,
+                                  int n_heads, int seq_len, int head_dim, void* out, int dtype,
+                                  hipStream_t stream) {
+  const int64_t o_s = head_dim, o_h = (int64_t)n_idx * head_dim, o_b = (int64_t)n_heads * o_h;
+  return index_copy(true, "ivakv_index_gather", kv, out, s_b, s_h, s_s, s_d, o_b, o_h, o_s, 1,
+                    indices, n_idx, batch, n_heads, seq_len, head_dim, dtype, stream);
+}
+
+extern "C" int ivakv_index_scatter(void* kv, int64_t s_b, int64_t s_h, int64_t s_s, int64_t s_d,
+                                   const int64_t* indices, int n_idx, const void* values,
+                                   int64_t v_b, int64_t v_h, int64_t v_s, int64_t v_d, int batch,
+                                   int n_heads, int seq_len, int head_dim, int dtype,
+                                   hipStream_t stream) {
+  return index_copy(false, "ivakv_index_scatter", values, kv, s_b, s_h, s_s, s_d, v_b, v_h, v_s,
+                    v_d, indices, n_idx, batch, n_heads, seq_len, head_dim, dtype, stream);
+}

@@ -1,0 +1,68 @@
+// Internal helpers shared by the libivakv translation units (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "ivakv.h"
+
+namespace ivakv {
+
+// Records a printf-style message as this thread's last error and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Maps the state after a launch to a status: IVAKV_E_LAUNCH with HIP's message
+// when the launch failed, IVAKV_OK otherwise.
+int launch_status(const char* what);
+
+inline int dtype_size(int dtype) {
+  switch (dtype) {
+    case IVAKV_F32: return 4;
+    case IVAKV_F16: return 2;
+    case IVAKV_BF16: return 2;
+    default: return 0;
+  }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Ceil division for non-negative ints.
+__host__ __device__ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// Visible-page walk of one sequence for decode attention.  The visible key
+// positions of a sequence of length L are
+//   { j < L : window <= 0 or j >= L - window or j < n_sink }
+// i.e. the attention-sink prefix [0, n_sink) united with the window [L-window, L).
+// They are covered by "effective" pages 0..n_eff-1: effective page v < sink_pages
+// is logical page v, and v >= sink_pages is logical page win_first + v - sink_pages.
+struct PageWalk {
+  int L;           // context length
+  int win_start;   // first window position (0 when there is no window)
+  int sink_pages;  // pages holding sink positions that lie before the window
+  int win_first;   // first logical page of the window range
+  int n_eff;       // number of effective pages
+};
+
+__host__ __device__ inline PageWalk make_walk(int L, int window, int n_sink, int bs) {
+  PageWalk w;
+  w.L = L < 0 ? 0 : L;
+  w.win_start = (window > 0 && w.L > window) ? w.L - window : 0;
+  int sink_len = (n_sink > 0) ? (n_sink < w.win_start ? n_sink : w.win_start) : 0;
+  w.sink_pages = cdiv(sink_len, bs);
+  int wf = w.win_start / bs;
+  w.win_first = wf > w.sink_pages ? wf : w.sink_pages;
+  int n_log = cdiv(w.L, bs);
+  w.n_eff = w.sink_pages + (n_log > w.win_first ? n_log - w.win_first : 0);
+  return w;
+}
+
+// Largest n_eff any sequence can have for a block table of max_blocks columns.
+inline int max_effective_pages(int max_blocks, int window, int n_sink, int bs) {
+  if (window <= 0) return max_blocks;
+  int bound = cdiv(n_sink > 0 ? n_sink : 0, bs) + cdiv(window, bs) + 1;
+  return bound < max_blocks ? bound : max_blocks;
+}
+
+}  // namespace ivakv

@@ -1,0 +1,289 @@
+"""Tensor-level paged KV ops on the HIP library (the operator API of this package).
+
+Every function here validates shapes on the host, then enqueues libivakv
+kernels on the current HIP stream of the tensors' device.  Nothing falls back
+to another implementation: a CPU tensor, an unsupported dtype or a missing
+library raises.
+
+Pool layout (X = 16 bytes / element size, e.g. 8 for fp16, 4 for fp32):
+    k_pool: [num_pages, Hkv, D // X, block_size, X]
+    v_pool: [num_pages, Hkv, D, block_size]
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from . import _abi
+
+_DTYPE_CODES = {torch.float32: _abi.F32, torch.float16: _abi.F16, torch.bfloat16: _abi.BF16}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported KV dtype {dtype}; expected float32, float16 or bfloat16") from None
+
+
+def chunk_elems(dtype: torch.dtype) -> int:
+    """Elements per 16-byte chunk (the innermost K-page dimension)."""
+    return 16 // torch.empty((), dtype=dtype).element_size()
+
+
+def pool_shapes(num_pages: int, num_kv_heads: int, head_dim: int, block_size: int,
+                dtype: torch.dtype) -> Tuple[Tuple[int, ...], Tuple[int, ...]]:
+    """Shapes of (k_pool, v_pool) for one layer."""
+    x = chunk_elems(dtype)
+    if head_dim % x:
+        raise ValueError(f"head_dim {head_dim} must be a multiple of {x} for {dtype}")
+    return ((num_pages, num_kv_heads, head_dim // x, block_size, x),
+            (num_pages, num_kv_heads, head_dim, block_size))
+
+
+def pool_geometry(k_pool: torch.Tensor, v_pool: torch.Tensor) -> Tuple[int, int, int, int]:
+    """(num_pages, Hkv, head_dim, block_size) of a pool pair; checks the layout."""
+    if k_pool.dim() != 5 or v_pool.dim() != 4:
+        raise ValueError("k_pool must be [P, Hkv, D/X, bs, X] and v_pool [P, Hkv, D, bs]")
+    num_pages, hkv, nch, bs, x = k_pool.shape
+    if x != chunk_elems(k_pool.dtype):
+        raise ValueError(f"k_pool innermost dim {x} != 16-byte chunk {chunk_elems(k_pool.dtype)}")
+    head_dim = nch * x
+    if tuple(v_pool.shape) != (num_pages, hkv, head_dim, bs):
+        raise ValueError(f"v_pool shape {tuple(v_pool.shape)} != {(num_pages, hkv, head_dim, bs)}")
+    if k_pool.dtype != v_pool.dtype:
+        raise TypeError("k_pool and v_pool dtypes differ")
+    if not (k_pool.is_contiguous() and v_pool.is_contiguous()):
+        raise ValueError("pools must be contiguous")
+    return num_pages, hkv, head_dim, bs
+
+
+def _require_gpu(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise RuntimeError(f"paged KV ops run on the GPU only; got a tensor on {t.device}")
+        if t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _i32(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != torch.int32:
+        raise TypeError(f"{name} must be int32, got {t.dtype}")
+    return t.contiguous()
+
+
+def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+              slot_mapping: torch.Tensor) -> None:
+    """Scatters rows ``k_new[t], v_new[t]`` ([n_tok, Hkv, D], last dim contiguous) into
+    ``slot_mapping[t]`` of the pools, in place.  A slot of -1 (or any slot outside the
+    pool) leaves the pools untouched for that token.
+
+    Paged counterpart of ``KVCache.update`` (src/core/rope_kv.py:98-110) and the
+    ``torch.cat`` append of ``AttentionTorch.forward`` (src/core/attention.py:61-63).
+    """
+    dev = _require_gpu(k_new, v_new, k_pool, v_pool, slot_mapping)
+    num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
+    if k_new.dim() != 3 or tuple(k_new.shape) != tuple(v_new.shape):
+        raise ValueError(f"k_new/v_new must be [n_tok, Hkv, D]; got {tuple(k_new.shape)} and {tuple(v_new.shape)}")
+    n_tok = k_new.shape[0]
+    if k_new.shape[1:] != (hkv, head_dim):
+        raise ValueError(f"new rows are {tuple(k_new.shape[1:])}, pool holds ({hkv}, {head_dim})")
+    if k_new.dtype != k_pool.dtype or v_new.dtype != k_pool.dtype:
+        raise TypeError(f"new rows dtype {k_new.dtype}/{v_new.dtype} != pool dtype {k_pool.dtype}")
+    slot_mapping = _i32(slot_mapping, "slot_mapping").reshape(-1)
+    if slot_mapping.numel() != n_tok:
+        raise ValueError(f"slot_mapping has {slot_mapping.numel()} entries for {n_tok} tokens")
+    if n_tok == 0:
+        return
+    if k_new.stride(2) != 1:
+        k_new = k_new.contiguous()
+    if v_new.stride(2) != 1:
+        v_new = v_new.contiguous()
+    _abi.call("ivakv_append", k_new.data_ptr(), v_new.data_ptr(),
+              k_new.stride(0), k_new.stride(1), v_new.stride(0), v_new.stride(1),
+              k_pool.data_ptr(), v_pool.data_ptr(), slot_mapping.data_ptr(),
+              n_tok, hkv, head_dim, bs, num_pages, dtype_code(k_pool.dtype), _stream(dev))
+
+
+def kv_gather(k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Tensor,
+              context_lens: torch.Tensor, out_len: Optional[int] = None,
+              out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+              ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Gathers each sequence's pages back into contiguous ``[B, Hkv, out_len, D]`` K and V
+    (pool dtype).  Rows at or beyond ``context_lens[b]`` are zero.  ``out_len`` defaults to
+    ``block_tables.shape[1] * block_size``.
+
+    Paged counterpart of ``KVCache.get_slice`` (src/core/rope_kv.py:136-137) and the gather
+    branch of ``KVOpsTriton`` (src/kernels_t/kv_ops_triton.py:111-123).
+    """
+    dev = _require_gpu(k_pool, v_pool, block_tables, context_lens)
+    num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
+    block_tables = _i32(block_tables, "block_tables")
+    context_lens = _i32(context_lens, "context_lens").reshape(-1)
+    if block_tables.dim() != 2 or block_tables.shape[0] != context_lens.numel():
+        raise ValueError("block_tables must be [B, max_blocks] with B == len(context_lens)")
+    batch, max_blocks = block_tables.shape
+    if out_len is None:
+        out_len = max_blocks * bs
+    shape = (batch, hkv, out_len, head_dim)
+    if out is None:
+        k_out = torch.empty(shape, dtype=k_pool.dtype, device=dev)
+        v_out = torch.empty(shape, dtype=k_pool.dtype, device=dev)
+    else:
+        k_out, v_out = out
+        for t in (k_out, v_out):
+            if tuple(t.shape) != shape or t.dtype != k_pool.dtype or not t.is_contiguous():
+                raise ValueError(f"gather outputs must be contiguous {shape} {k_pool.dtype}")
+    _abi.call("ivakv_gather", k_pool.data_ptr(), v_pool.data_ptr(), block_tables.data_ptr(),
+              context_lens.data_ptr(), batch, max_blocks, hkv, head_dim, bs, num_pages, out_len,
+              k_out.data_ptr(), v_out.data_ptr(), dtype_code(k_pool.dtype), _stream(dev))
+    return k_out, v_out
+
+
+_WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
+
+
+def decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                           block_size: int, max_blocks: int, window: int = 0, n_sink: int = 0,
+                           partition_pages: int = 0) -> int:
+    import ctypes
+    out = ctypes.c_size_t(0)
+    _abi.call("ivakv_decode_workspace_size", batch, num_q_heads, num_kv_heads, head_dim,
+              block_size, max_blocks, window, n_sink, partition_pages, ctypes.byref(out))
+    return int(out.value)
+
+
+def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream(dev))
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def _decode(entry: str, q, k_pool, v_pool, block_tables, context_lens, scale, window, n_sink,
+            partition_pages, out, workspace):
+    dev = _require_gpu(q, k_pool, v_pool, block_tables, context_lens)
+    num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
+    if q.dim() != 3 or q.shape[2] != head_dim:
+        raise ValueError(f"q must be [B, Hq, {head_dim}]; got {tuple(q.shape)}")
+    if q.dtype != k_pool.dtype:
+        raise TypeError(f"q dtype {q.dtype} != pool dtype {k_pool.dtype}")
+    batch, hq, _ = q.shape
+    block_tables = _i32(block_tables, "block_tables")
+    context_lens = _i32(context_lens, "context_lens").reshape(-1)
+    if block_tables.dim() != 2 or block_tables.shape[0] != batch or context_lens.numel() != batch:
+        raise ValueError("block_tables must be [B, max_blocks] and context_lens [B]")
+    max_blocks = block_tables.shape[1]
+    q = q.contiguous()
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    window = int(window) if window else 0
+    n_sink = int(n_sink) if n_sink else 0
+    partition_pages = int(partition_pages) if partition_pages else 0
+    if out is None:
+        out = torch.empty_like(q)
+    elif tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped and typed like q")
+    nbytes = decode_workspace_bytes(batch, hq, hkv, head_dim, bs, max_blocks, window, n_sink,
+                                    partition_pages)
+    if workspace is None:
+        workspace = _workspace(dev, nbytes)
+    elif workspace.numel() * workspace.element_size() < nbytes:
+        raise ValueError(f"workspace has {workspace.numel() * workspace.element_size()} bytes, "
+                         f"{nbytes} needed")
+    _abi.call(entry, q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), block_tables.data_ptr(),
+              context_lens.data_ptr(), out.data_ptr(), workspace.data_ptr(),
+              workspace.numel() * workspace.element_size(), batch, hq, hkv, head_dim, bs,
+              max_blocks, num_pages, float(scale), window, n_sink, partition_pages,
+              dtype_code(q.dtype), _stream(dev))
+    return out
+
+
+def paged_decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                           block_tables: torch.Tensor, context_lens: torch.Tensor,
+                           scale: Optional[float] = None, window: Optional[int] = None,
+                           n_sink: int = 0, partition_pages: Optional[int] = None,
+                           out: Optional[torch.Tensor] = None,
+                           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Single-query attention over paged K/V: ``q`` is ``[B, Hq, D]``; returns ``[B, Hq, D]``.
+
+    Sequence b attends to positions ``j < context_lens[b]`` that lie in the sliding window
+    ``j >= L - window`` (all when ``window`` is None/0) or among the first ``n_sink``
+    attention-sink positions.  Query head h reads KV head ``h // (Hq // Hkv)``.
+    ``scale`` defaults to ``1/sqrt(D)`` as in ``AttentionTorch`` (src/core/attention.py:35).
+
+    Replaces the cache branch of ``AttentionTorch.forward`` (src/core/attention.py:77-102).
+    """
+    return _decode("ivakv_decode_attn", q, k_pool, v_pool, block_tables, context_lens, scale,
+                   window, n_sink, partition_pages, out, workspace)
+
+
+def paged_decode_attention_partial(q, k_pool, v_pool, block_tables, context_lens, scale=None,
+                                   window=None, n_sink=0, partition_pages=None, out=None,
+                                   workspace=None) -> torch.Tensor:
+    """First half of :func:`paged_decode_attention` (the paged walk); see include/ivakv.h."""
+    return _decode("ivakv_decode_attn_partial", q, k_pool, v_pool, block_tables, context_lens,
+                   scale, window, n_sink, partition_pages, out, workspace)
+
+
+def paged_decode_attention_merge(q, k_pool, v_pool, block_tables, context_lens, scale=None,
+                                 window=None, n_sink=0, partition_pages=None, out=None,
+                                 workspace=None) -> torch.Tensor:
+    """Second half of :func:`paged_decode_attention` (log-sum-exp merge of partitions)."""
+    return _decode("ivakv_decode_attn_merge", q, k_pool, v_pool, block_tables, context_lens,
+                   scale, window, n_sink, partition_pages, out, workspace)
+
+
+def kv_ops(kv_cache: torch.Tensor, indices: torch.Tensor, values: Optional[torch.Tensor] = None,
+           operation: str = "gather") -> torch.Tensor:
+    """Index gather / scatter along the sequence axis of a contiguous ``[B, H, S, D]`` cache.
+
+    Same signature, semantics and errors as ``kv_ops_triton``
+    (src/kernels_t/kv_ops_triton.py:150-156):
+      * ``"gather"``:  returns ``kv_cache[:, :, indices, :]`` as a new ``[B, H, N, D]`` tensor;
+      * ``"scatter"``: returns a copy of ``kv_cache`` with ``[:, :, indices[j], :]`` replaced
+        by ``values[:, :, j, :]`` (the input is not modified);
+      * ``ValueError`` for a scatter without values or an unknown operation
+        (kv_ops_triton.py:126-127,142-143).
+    Differences, both deliberate: the gather output keeps the cache dtype (the reference
+    allocated it in the default dtype, kv_ops_triton.py:112), and an index outside
+    ``[0, S)`` raises ``IndexError`` instead of reading or writing out of bounds.
+    """
+    if operation not in ("gather", "scatter"):
+        raise ValueError(f"Unknown operation: {operation}")
+    if operation == "scatter" and values is None:
+        raise ValueError("Values tensor required for scatter operation")
+    tensors = [kv_cache, indices] + ([values] if values is not None else [])
+    dev = _require_gpu(*tensors)
+    if kv_cache.dim() != 4:
+        raise ValueError(f"kv_cache must be [B, H, S, D]; got {tuple(kv_cache.shape)}")
+    batch, n_heads, seq_len, head_dim = kv_cache.shape
+    idx = indices.reshape(-1).to(torch.int64).contiguous()
+    n_idx = idx.numel()
+    if n_idx and bool(((idx < 0) | (idx >= seq_len)).any()):
+        raise IndexError(f"kv_ops index out of range for sequence length {seq_len}")
+    code = dtype_code(kv_cache.dtype)
+    if operation == "gather":
+        out = torch.empty((batch, n_heads, n_idx, head_dim), dtype=kv_cache.dtype, device=dev)
+        _abi.call("ivakv_index_gather", kv_cache.data_ptr(), *kv_cache.stride(), idx.data_ptr(),
+                  n_idx, batch, n_heads, seq_len, head_dim, out.data_ptr(), code, _stream(dev))
+        return out
+    if tuple(values.shape) != (batch, n_heads, n_idx, head_dim):
+        raise ValueError(f"values must be {(batch, n_heads, n_idx, head_dim)}; got {tuple(values.shape)}")
+    if values.dtype != kv_cache.dtype:
+        raise TypeError(f"values dtype {values.dtype} != cache dtype {kv_cache.dtype}")
+    out = kv_cache.clone()
+    _abi.call("ivakv_index_scatter", out.data_ptr(), *out.stride(), idx.data_ptr(), n_idx,
+              values.data_ptr(), *values.stride(), batch, n_heads, seq_len, head_dim, code,
+              _stream(dev))
+    return out

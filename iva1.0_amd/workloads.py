@@ -1,0 +1,142 @@
+"""Seeded synthetic workloads for the paged KV hot path (the five BASELINE configs).
+
+Every generator is deterministic in its seed.  Host-side randomness (lengths,
+page permutations) comes from ``torch.Generator().manual_seed(seed)`` on the CPU;
+bulk K/V/Q values are drawn with a generator on ``device`` (the CPU by default,
+so the oracle and the GPU path see identical bits; the bench draws on the GPU).
+
+  C1  paged append then gather, fp32: 4 sequences of {17, 64, 129, 200} tokens,
+      8 KV heads, head_dim 64, block 16; block tables are the first pages of a
+      seeded permutation of a 64-page pool; K/V ~ N(0, 1).
+  C2  paged decode attention, fp16: 32 sequences, 32 query / 8 KV heads,
+      head_dim 128, block 16, context ~ U[512, 4096]; Q/K/V ~ N(0,1)/sqrt(128);
+      block tables are a seeded page permutation.
+  C4  long-context decode, bf16: 4 sequences of 32k/64k/96k/128k tokens, window
+      4096 + 4 sinks, 32/8 heads, head_dim 128, K/V ~ N(0, 1).
+  C5  ragged churn, fp16: 256 sequences, lengths LogNormal(ln 1024, sigma=1.0)
+      capped at 16384 (sigma is not given by the config; 1.0 is stated here),
+      block tables fragmented by LIFO free-list reuse (see PagedKVPool).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import List, Optional
+
+import torch
+
+from .ops import pool_shapes
+
+BLOCK_SIZE = 16
+
+
+@dataclass
+class PagedLayout:
+    """Block tables of a batch: sequence b owns pages block_tables[b, :ceil(L_b / bs)]."""
+    lengths: List[int]
+    block_tables: torch.Tensor  # int32 [B, max_blocks], -1 past each sequence's pages
+    num_pages: int
+    block_size: int = BLOCK_SIZE
+
+    @property
+    def context_lens(self) -> torch.Tensor:
+        return torch.tensor(self.lengths, dtype=torch.int32)
+
+    def slots(self, b: int, positions: torch.Tensor) -> torch.Tensor:
+        """Slot ids of positions of sequence b."""
+        pages = self.block_tables[b].to(torch.int64)[positions // self.block_size]
+        return (pages * self.block_size + positions % self.block_size).to(torch.int32)
+
+
+def permuted_layout(lengths: List[int], num_pages: int, gen: torch.Generator,
+                    block_size: int = BLOCK_SIZE, max_blocks: Optional[int] = None) -> PagedLayout:
+    """Sequences take consecutive runs of one seeded permutation of the pool's pages."""
+    need = [math.ceil(int(n) / block_size) for n in lengths]
+    if sum(need) > num_pages:
+        raise ValueError(f"{sum(need)} pages needed, pool has {num_pages}")
+    perm = torch.randperm(num_pages, generator=gen).to(torch.int32)
+    mb = max_blocks if max_blocks is not None else max(need + [1])
+    bt = torch.full((len(lengths), mb), -1, dtype=torch.int32)
+    cur = 0
+    for b, n in enumerate(need):
+        bt[b, :n] = perm[cur:cur + n]
+        cur += n
+    return PagedLayout([int(n) for n in lengths], bt, num_pages, block_size)
+
+
+def _randn(shape, gen_seed: int, device, dtype, scale: float = 1.0) -> torch.Tensor:
+    dev = torch.device(device) if device is not None else torch.device("cpu")
+    g = torch.Generator(device=dev).manual_seed(gen_seed)
+    x = torch.randn(shape, generator=g, device=dev, dtype=torch.float32)
+    if scale != 1.0:
+        x.mul_(scale)
+    return x.to(dtype)
+
+
+def c1_append_gather(seed: int = 0, dtype: torch.dtype = torch.float32, device=None) -> dict:
+    """C1: rows of every token of the four sequences plus the slots they go to."""
+    lengths = [17, 64, 129, 200]
+    hkv, head_dim, num_pages = 8, 64, 64
+    gen = torch.Generator().manual_seed(seed)
+    layout = permuted_layout(lengths, num_pages, gen)
+    n_tok = sum(lengths)
+    k_new = _randn((n_tok, hkv, head_dim), seed * 1000 + 1, device, dtype)
+    v_new = _randn((n_tok, hkv, head_dim), seed * 1000 + 2, device, dtype)
+    slots = torch.cat([layout.slots(b, torch.arange(n)) for b, n in enumerate(lengths)])
+    return dict(lengths=lengths, layout=layout, k_new=k_new, v_new=v_new, slot_mapping=slots,
+                num_kv_heads=hkv, head_dim=head_dim, num_pages=num_pages, block_size=BLOCK_SIZE)
+
+
+def random_pools(num_pages: int, hkv: int, head_dim: int, dtype: torch.dtype, seed: int,
+                 device=None, scale: float = 1.0):
+    """A pool pair filled with N(0, scale^2) values (page contents are i.i.d., so the
+    layout of the values inside a page is immaterial)."""
+    ks, vs = pool_shapes(num_pages, hkv, head_dim, BLOCK_SIZE, dtype)
+    return (_randn(ks, seed * 1000 + 11, device, dtype, scale),
+            _randn(vs, seed * 1000 + 12, device, dtype, scale))
+
+
+def decode_batch(lengths: List[int], num_q_heads: int, num_kv_heads: int, head_dim: int,
+                 dtype: torch.dtype, seed: int, device=None, scale: float = 1.0,
+                 extra_pages: int = 0, max_blocks: Optional[int] = None) -> dict:
+    """Decode inputs: a permuted page layout for ``lengths``, random pools, random q."""
+    gen = torch.Generator().manual_seed(seed)
+    need = sum(math.ceil(n / BLOCK_SIZE) for n in lengths)
+    num_pages = max(need + extra_pages, 1)
+    layout = permuted_layout(lengths, num_pages, gen, max_blocks=max_blocks)
+    k_pool, v_pool = random_pools(num_pages, num_kv_heads, head_dim, dtype, seed, device, scale)
+    q = _randn((len(lengths), num_q_heads, head_dim), seed * 1000 + 13, device, dtype, scale)
+    return dict(lengths=list(lengths), layout=layout, k_pool=k_pool, v_pool=v_pool, q=q,
+                num_q_heads=num_q_heads, num_kv_heads=num_kv_heads, head_dim=head_dim)
+
+
+def c2_lengths(seed: int, batch: int = 32, lo: int = 512, hi: int = 4096) -> List[int]:
+    gen = torch.Generator().manual_seed(seed)
+    return torch.randint(lo, hi + 1, (batch,), generator=gen).tolist()
+
+
+def c2_decode(seed: int = 0, device=None, batch: int = 32, dtype: torch.dtype = torch.float16) -> dict:
+    """C2 at full size: B 32, GQA 32/8, head_dim 128, context U[512, 4096], values N(0,1)/sqrt(128)."""
+    lengths = c2_lengths(seed, batch)
+    return decode_batch(lengths, 32, 8, 128, dtype, seed, device, scale=1.0 / math.sqrt(128))
+
+
+C4_LENGTHS = [32 * 1024, 64 * 1024, 96 * 1024, 128 * 1024]
+C4_WINDOW = 4096
+C4_SINKS = 4
+
+
+def c4_long_context(seed: int = 0, device=None, lengths: Optional[List[int]] = None,
+                    dtype: torch.dtype = torch.bfloat16) -> dict:
+    """C4: 4 long sequences, window 4096 + 4 sinks, bf16, K/V ~ N(0, 1)."""
+    d = decode_batch(lengths or C4_LENGTHS, 32, 8, 128, dtype, seed, device, scale=1.0)
+    d.update(window=C4_WINDOW, n_sink=C4_SINKS)
+    return d
+
+
+def c5_lengths(seed: int, n_seqs: int = 256, median: int = 1024, sigma: float = 1.0,
+               cap: int = 16384) -> List[int]:
+    gen = torch.Generator().manual_seed(seed)
+    z = torch.randn(n_seqs, generator=gen, dtype=torch.float64)
+    lens = torch.exp(math.log(median) + sigma * z).round().clamp(1, cap)
+    return [int(x) for x in lens.tolist()]

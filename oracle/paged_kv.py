@@ -1,0 +1,224 @@
+"""numpy oracle of the paged KV hot path.  TEST INFRASTRUCTURE ONLY.
+
+Restates, on the paged layout, the semantics of the reference's
+  - KVCache.update slice-assign            src/core/rope_kv.py:98-110
+  - AttentionTorch cache append (torch.cat) src/core/attention.py:61-63
+  - KVCache.get_slice                      src/core/rope_kv.py:136-137
+  - AttentionTorch math                    src/core/attention.py:77-102
+  - masks (window / sink)                  src/core/attention.py:115-148
+  - kv_gather / kv_scatter kernels         src/kernels_t/kv_ops_triton.py:18-65,129
+
+Layout (X = 16 // itemsize, BS = block size):
+  k_pool [P, Hkv, D/X, BS, X]: K(page, h, t, d) at ((d // X) * BS + t) * X + d % X
+  v_pool [P, Hkv, D, BS]:      V(page, h, t, d) at d * BS + t
+Slot s -> page s // BS, row s % BS.
+
+Decisions the reference leaves open (fixed here and in the kernels):
+  * GQA: query head h reads KV head h // (Hq // Hkv) (repeat_interleave order).
+  * Decode positions are absolute: with context length L (the new token already
+    appended) the query sits at L - 1 and sees keys 0..L-1 (append-before-score
+    order of attention.py:61-77).
+  * Window W keeps keys j >= L - W, i.e. [i - W + 1, i] for query i = L - 1
+    (attention.py:124-127 at absolute positions).
+  * Sinks are the union [0, n_sink) | window, not the reference's AND of masks.
+  * An empty context (L == 0) yields a zero output row.
+  * Gather keeps the cache dtype.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import numpy as np
+
+
+def chunk_elems(itemsize: int) -> int:
+    return 16 // itemsize
+
+
+def empty_pools(num_pages: int, hkv: int, head_dim: int, block_size: int, dtype,
+                fill=0) -> Tuple[np.ndarray, np.ndarray]:
+    """Pools of one layer filled with ``fill`` (a canary value for untouched slots)."""
+    dt = np.dtype(dtype)
+    x = chunk_elems(dt.itemsize)
+    assert head_dim % x == 0
+    k = np.full((num_pages, hkv, head_dim // x, block_size, x), fill, dtype=dt)
+    v = np.full((num_pages, hkv, head_dim, block_size), fill, dtype=dt)
+    return k, v
+
+
+def append(k_pool: np.ndarray, v_pool: np.ndarray, k_new: np.ndarray, v_new: np.ndarray,
+           slot_mapping: np.ndarray) -> None:
+    """In place: row ``t`` of ``k_new/v_new`` ([n_tok, Hkv, D]) lands in slot ``slot_mapping[t]``;
+    slots outside ``[0, P*BS)`` (e.g. -1) are skipped.  ``KVCache.update`` writes new rows at
+    their sequence positions (rope_kv.py:109-110); on the paged cache the position is the slot."""
+    num_pages, hkv, nch, bs, x = k_pool.shape
+    slots = np.asarray(slot_mapping, dtype=np.int64).reshape(-1)
+    valid = (slots >= 0) & (slots < num_pages * bs)
+    ts = np.nonzero(valid)[0]
+    if ts.size == 0:
+        return
+    s = slots[ts]
+    page, off = s // bs, s % bs
+    k_pool[page, :, :, off, :] = k_new[ts].reshape(ts.size, hkv, nch, x)
+    v_pool[page, :, :, off] = v_new[ts]
+
+
+def gather(k_pool: np.ndarray, v_pool: np.ndarray, block_tables: np.ndarray, ctx_lens: np.ndarray,
+           out_len: Optional[int] = None) -> Tuple[np.ndarray, np.ndarray]:
+    """Contiguous ``[B, Hkv, out_len, D]`` K and V of each sequence (``KVCache.get_slice``,
+    rope_kv.py:136-137); rows at or past ``ctx_lens[b]`` and rows on invalid pages are zero."""
+    num_pages, hkv, nch, bs, x = k_pool.shape
+    d = nch * x
+    bt = np.asarray(block_tables, dtype=np.int64)
+    ctx = np.asarray(ctx_lens, dtype=np.int64).reshape(-1)
+    batch, max_blocks = bt.shape
+    if out_len is None:
+        out_len = max_blocks * bs
+    k_out = np.zeros((batch, hkv, out_len, d), dtype=k_pool.dtype)
+    v_out = np.zeros((batch, hkv, out_len, d), dtype=v_pool.dtype)
+    for b in range(batch):
+        lim = min(max(int(ctx[b]), 0), out_len)
+        for j in range(min(-(-lim // bs), max_blocks)):
+            p = int(bt[b, j])
+            if p < 0 or p >= num_pages:
+                continue
+            n = min(bs, lim - j * bs)
+            k_out[b, :, j * bs:j * bs + n, :] = (
+                k_pool[p, :, :, :n, :].transpose(0, 2, 1, 3).reshape(hkv, n, d))
+            v_out[b, :, j * bs:j * bs + n, :] = v_pool[p, :, :, :n].transpose(0, 2, 1)
+    return k_out, v_out
+
+
+def append_loops(k_flat: np.ndarray, v_flat: np.ndarray, k_new, v_new, slot_mapping,
+                 num_pages: int, hkv: int, head_dim: int, bs: int) -> None:
+    """Brute-force append on FLAT pools using the address formula of include/ivakv.h."""
+    x = chunk_elems(k_flat.dtype.itemsize)
+    tile = head_dim * bs
+    for t, s in enumerate(list(np.asarray(slot_mapping).reshape(-1))):
+        s = int(s)
+        if s < 0 or s >= num_pages * bs:
+            continue
+        page, row = divmod(s, bs)
+        for h in range(hkv):
+            base = (page * hkv + h) * tile
+            for dd in range(head_dim):
+                k_flat[base + ((dd // x) * bs + row) * x + dd % x] = k_new[t][h][dd]
+                v_flat[base + dd * bs + row] = v_new[t][h][dd]
+
+
+def gather_loops(k_flat: np.ndarray, v_flat: np.ndarray, block_tables, ctx_lens, num_pages: int,
+                 hkv: int, head_dim: int, bs: int, out_len: int):
+    """Brute-force gather from FLAT pools using the address formula of include/ivakv.h."""
+    x = chunk_elems(k_flat.dtype.itemsize)
+    tile = head_dim * bs
+    batch = len(ctx_lens)
+    k_out = np.zeros((batch, hkv, out_len, head_dim), dtype=k_flat.dtype)
+    v_out = np.zeros((batch, hkv, out_len, head_dim), dtype=v_flat.dtype)
+    for b in range(batch):
+        for pos in range(min(int(ctx_lens[b]), out_len)):
+            j, row = divmod(pos, bs)
+            if j >= len(block_tables[b]):
+                continue
+            page = int(block_tables[b][j])
+            if page < 0 or page >= num_pages:
+                continue
+            for h in range(hkv):
+                base = (page * hkv + h) * tile
+                for dd in range(head_dim):
+                    k_out[b, h, pos, dd] = k_flat[base + ((dd // x) * bs + row) * x + dd % x]
+                    v_out[b, h, pos, dd] = v_flat[base + dd * bs + row]
+    return k_out, v_out
+
+
+def visible(length: int, window: int = 0, n_sink: int = 0) -> np.ndarray:
+    """Keys a decode query at position ``length - 1`` attends to: causal, within the
+    sliding window (attention.py:124-127 at absolute positions) or an attention sink."""
+    j = np.arange(max(length, 0))
+    if window and window > 0:
+        return (j >= length - window) | (j < n_sink)
+    return np.ones_like(j, dtype=bool)
+
+
+def expand_gqa(x: np.ndarray, group: int) -> np.ndarray:
+    """[Hkv, ...] -> [Hkv * group, ...] with query head h reading KV head h // group
+    (torch ``repeat_interleave`` order)."""
+    return np.repeat(x, group, axis=0)
+
+
+def decode_attention(q: np.ndarray, k_pool: np.ndarray, v_pool: np.ndarray,
+                     block_tables: np.ndarray, ctx_lens: np.ndarray, scale: Optional[float] = None,
+                     window: int = 0, n_sink: int = 0) -> np.ndarray:
+    """fp64 single-query attention of ``q`` ([B, Hq, D]) over each sequence's paged K/V:
+    ``softmax(q k^T * scale) v`` over the visible keys (attention.py:77-102)."""
+    q = np.asarray(q, dtype=np.float64)
+    batch, hq, d = q.shape
+    hkv = k_pool.shape[1]
+    g = hq // hkv
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    ctx = np.asarray(ctx_lens, dtype=np.int64).reshape(-1)
+    bt = np.asarray(block_tables, dtype=np.int64)
+    num_pages, bs = k_pool.shape[0], k_pool.shape[3]
+    max_len = int(max(ctx.max(initial=0), 0))
+    k_all, v_all = gather(k_pool, v_pool, bt, ctx, out_len=max_len)
+    out = np.zeros((batch, hq, d), dtype=np.float64)
+    for b in range(batch):
+        length = int(ctx[b])
+        if length <= 0:
+            continue
+        # keys on a page id outside the pool (or past the table) are not attended
+        page_idx = np.arange(length) // bs
+        pid = np.full(length, -1, dtype=np.int64)
+        in_table = page_idx < bt.shape[1]
+        pid[in_table] = bt[b, page_idx[in_table]]
+        vis = visible(length, window, n_sink) & (pid >= 0) & (pid < num_pages)
+        if not vis.any():
+            continue
+        k = expand_gqa(k_all[b, :, :length][:, vis].astype(np.float64), g)
+        v = expand_gqa(v_all[b, :, :length][:, vis].astype(np.float64), g)
+        scores = np.einsum("hd,had->ha", q[b], k) * scale
+        scores -= scores.max(axis=1, keepdims=True)
+        p = np.exp(scores)
+        p /= p.sum(axis=1, keepdims=True)
+        out[b] = np.einsum("ha,had->hd", p, v)
+    return out
+
+
+def decode_attention_loops(q, k_rows, v_rows, ctx_lens, scale: float, window: int = 0,
+                           n_sink: int = 0):
+    """Pure-Python single-query attention on contiguous rows ``k_rows[b][h][j][d]`` (tiny
+    inputs only): the textbook formula evaluated term by term."""
+    batch, hq, d = len(q), len(q[0]), len(q[0][0])
+    hkv = len(k_rows[0])
+    g = hq // hkv
+    out = [[[0.0] * d for _ in range(hq)] for _ in range(batch)]
+    for b in range(batch):
+        length = int(ctx_lens[b])
+        keys = [j for j in range(length)
+                if not window or window <= 0 or j >= length - window or j < n_sink]
+        if not keys:
+            continue
+        for h in range(hq):
+            kh = h // g
+            s = [sum(float(q[b][h][i]) * float(k_rows[b][kh][j][i]) for i in range(d)) * scale
+                 for j in keys]
+            m = max(s)
+            e = [math.exp(x - m) for x in s]
+            z = sum(e)
+            for i in range(d):
+                out[b][h][i] = sum(e[n] * float(v_rows[b][kh][j][i]) for n, j in enumerate(keys)) / z
+    return out
+
+
+def index_gather(kv: np.ndarray, indices: np.ndarray) -> np.ndarray:
+    """``out[b, h, j] = kv[b, h, indices[j]]`` (kv_gather_kernel, kv_ops_triton.py:33-40)."""
+    return kv[:, :, np.asarray(indices, dtype=np.int64), :].copy()
+
+
+def index_scatter(kv: np.ndarray, indices: np.ndarray, values: np.ndarray) -> np.ndarray:
+    """Functional scatter: a copy of ``kv`` with ``[:, :, indices[j]] = values[:, :, j]``
+    (kv_ops_triton.py:58-65 on the clone made at :129)."""
+    out = kv.copy()
+    out[:, :, np.asarray(indices, dtype=np.int64), :] = values
+    return out

@@ -1,0 +1,282 @@
+"""Paged decode attention on the GPU vs the fp64 CPU oracle and a torch fp32 reference.
+
+Tolerance (written here, per the north star): max |out - exact| <= 2e-3 for fp16/bf16
+and <= 1e-5 for fp32, where `exact` is the fp64 oracle.  For unit-scale test data
+with peaky softmaxes the bf16/fp16 OUTPUT rounding alone can exceed that, so the
+bound used in the small-shape sweeps is 2e-3 (1e-5) plus one half-ulp of the output
+dtype times |exact|; the full-size config tests use the plain 2e-3 bound.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_kv as orc
+
+pytestmark = pytest.mark.gpu
+
+ATOL = {torch.float16: 2e-3, torch.bfloat16: 2e-3, torch.float32: 1e-5}
+OUT_ULP = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8, torch.float32: 2.0 ** -23}
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def oracle_out(d, scale=None, window=0, n_sink=0, layout=None):
+    lay = layout or d["layout"]
+    return orc.decode_attention(to_np(d["q"]), to_np(d["k_pool"]), to_np(d["v_pool"]),
+                                lay.block_tables.numpy(), lay.context_lens.numpy(),
+                                scale=scale, window=window, n_sink=n_sink)
+
+
+def run_gpu(iva, dev, d, layout=None, **kw):
+    lay = layout or d["layout"]
+    return iva.paged_decode_attention(d["q"].to(dev), d["k_pool"].to(dev), d["v_pool"].to(dev),
+                                      lay.block_tables.to(dev), lay.context_lens.to(dev), **kw)
+
+
+def assert_close(out: torch.Tensor, ref: np.ndarray, dtype, rel_ulp=True, what=""):
+    err = np.abs(to_np(out) - ref)
+    bound = ATOL[dtype] + (OUT_ULP[dtype] * np.abs(ref) if rel_ulp else 0.0)
+    worst = float((err - bound).max()) if err.size else -1.0
+    assert worst <= 0.0, f"{what}: max abs err {err.max():.3e} exceeds bound (excess {worst:.3e})"
+    return float(err.max()) if err.size else 0.0
+
+
+def torch_rows(k_pool, v_pool, bt_row, length):
+    """Contiguous [Hkv, L, D] K/V of one sequence by plain torch indexing of the pools."""
+    n = -(-length // 16)
+    pages = bt_row[:n].long()
+    hkv = k_pool.shape[1]
+    d = k_pool.shape[2] * k_pool.shape[4]
+    k = k_pool[pages].permute(1, 0, 3, 2, 4).reshape(hkv, n * 16, d)[:, :length]
+    v = v_pool[pages].permute(1, 0, 3, 2).reshape(hkv, n * 16, d)[:, :length]
+    return k, v
+
+
+def torch_reference(q, k_pool, v_pool, bt, lengths, scale, window=0, n_sink=0):
+    """fp32 torch attention on the GPU, one sequence at a time (visible keys only)."""
+    batch, hq, d = q.shape
+    hkv = k_pool.shape[1]
+    out = torch.zeros(batch, hq, d, dtype=torch.float32, device=q.device)
+    for b, length in enumerate(lengths):
+        if length <= 0:
+            continue
+        k, v = torch_rows(k_pool, v_pool, bt[b], length)
+        j = torch.arange(length, device=q.device)
+        vis = (j >= length - window) | (j < n_sink) if window else torch.ones_like(j, dtype=torch.bool)
+        k = k[:, vis].float().repeat_interleave(hq // hkv, dim=0).contiguous()
+        v = v[:, vis].float().repeat_interleave(hq // hkv, dim=0).contiguous()
+        s = torch.matmul(q[b].float().unsqueeze(1), k.transpose(1, 2).contiguous()) * scale
+        out[b] = torch.matmul(torch.softmax(s, dim=-1), v).squeeze(1)
+    return out
+
+
+LENGTHS = [1, 15, 16, 17, 100, 257, 513, 1100]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("group", [1, 4, 16])
+def test_small_vs_oracle(iva, dev, dtype, head_dim, group):
+    hkv = 2
+    d = iva.workloads.decode_batch(LENGTHS, hkv * group, hkv, head_dim, dtype,
+                                   seed=head_dim + group, extra_pages=3)
+    out = run_gpu(iva, dev, d)
+    assert_close(out, oracle_out(d), dtype, what=f"{dtype} D{head_dim} G{group}")
+
+
+@pytest.mark.parametrize("group", [2, 8])
+def test_other_groups(iva, dev, group):
+    d = iva.workloads.decode_batch([5, 300, 999], 3 * group, 3, 128, torch.float16, seed=group,
+                                   scale=128 ** -0.5)
+    assert_close(run_gpu(iva, dev, d), oracle_out(d), torch.float16, rel_ulp=False)
+
+
+@pytest.mark.parametrize("pp", [1, 2, 3, 5, 16, 64])
+def test_partition_sizes_agree(iva, dev, pp):
+    d = iva.workloads.decode_batch([700, 1, 33, 4096], 32, 8, 128, torch.float16, seed=7,
+                                   scale=128 ** -0.5)
+    out = run_gpu(iva, dev, d, partition_pages=pp)
+    assert_close(out, oracle_out(d), torch.float16, rel_ulp=False, what=f"partition {pp}")
+
+
+def test_partial_then_merge_equals_full(iva, dev):
+    d = iva.workloads.decode_batch([900, 20, 2000], 16, 4, 128, torch.bfloat16, seed=8)
+    lay = d["layout"]
+    args = (d["q"].to(dev), d["k_pool"].to(dev), d["v_pool"].to(dev), lay.block_tables.to(dev),
+            lay.context_lens.to(dev))
+    full = iva.paged_decode_attention(*args)
+    ws = torch.empty(iva.decode_workspace_bytes(3, 16, 4, 128, 16, lay.block_tables.shape[1]),
+                     dtype=torch.uint8, device=dev)
+    out = torch.empty_like(full)
+    iva.paged_decode_attention_partial(*args, out=out, workspace=ws)
+    iva.paged_decode_attention_merge(*args, out=out, workspace=ws)
+    assert torch.equal(out.view(torch.int16), full.view(torch.int16))
+
+
+def test_deterministic(iva, dev):
+    d = iva.workloads.decode_batch([4000, 37, 1500], 32, 8, 128, torch.float16, seed=9,
+                                   scale=128 ** -0.5)
+    a = run_gpu(iva, dev, d)
+    b = run_gpu(iva, dev, d)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_closed_forms(iva, dev, dtype):
+    """One key -> exactly v[0]; all keys equal -> mean of v; empty context -> zeros."""
+    d = iva.workloads.decode_batch([1, 64, 0], 8, 2, 128, dtype, seed=10)
+    lay = d["layout"]
+    k_pool, v_pool = d["k_pool"].clone(), d["v_pool"].clone()
+    # sequence 1: make all 64 keys identical (copy row 0 of its first page everywhere)
+    pages = lay.block_tables[1, :4].long()
+    k_pool[pages] = k_pool[pages[0]].select(3, 0).unsqueeze(3).unsqueeze(0).expand_as(k_pool[pages]).clone()
+    d2 = dict(d, k_pool=k_pool, v_pool=v_pool)
+    out = run_gpu(iva, dev, d2).float().cpu()
+    # one key: exactly the V row of position 0
+    _, v0 = torch_rows(k_pool, v_pool, lay.block_tables[0], 1)
+    g = 4
+    for h in range(8):
+        assert torch.equal(out[0, h], v0[h // g, 0].float()), "single key must return v[0] exactly"
+    # equal keys: mean of the 64 V rows
+    _, v1 = torch_rows(k_pool, v_pool, lay.block_tables[1], 64)
+    mean = v1.double().mean(dim=1)
+    for h in range(8):
+        err = (out[1, h].double() - mean[h // g]).abs().max().item()
+        assert err <= ATOL[dtype] + OUT_ULP[dtype] * mean[h // g].abs().max().item()
+    assert not out[2].any(), "empty context must give a zero row"
+
+
+@pytest.mark.parametrize("window,n_sink,lengths", [
+    (64, 4, [5000, 64, 65, 63, 1]),
+    (100, 0, [5000, 101, 99]),
+    (16, 20, [300, 17, 40]),          # sinks reach past the window start of short sequences
+    (4096, 4, [4100, 8192, 4097]),
+    (1, 1, [50, 1, 2]),
+])
+def test_window_and_sinks(iva, dev, window, n_sink, lengths):
+    d = iva.workloads.decode_batch(lengths, 8, 2, 128, torch.bfloat16, seed=window + n_sink)
+    out = run_gpu(iva, dev, d, window=window, n_sink=n_sink)
+    ref = oracle_out(d, window=window, n_sink=n_sink)
+    assert_close(out, ref, torch.bfloat16, what=f"window {window} sinks {n_sink}")
+
+
+def test_invalid_pages_are_not_attended(iva, dev):
+    d = iva.workloads.decode_batch([300, 300], 8, 2, 64, torch.float32, seed=11)
+    lay = d["layout"]
+    bt = lay.block_tables.clone()
+    bt[0, 3] = -1
+    bt[1, 5] = lay.num_pages + 7
+    lay2 = iva.workloads.PagedLayout(lay.lengths, bt, lay.num_pages)
+    out = run_gpu(iva, dev, d, layout=lay2)
+    assert_close(out, oracle_out(d, layout=lay2), torch.float32, what="invalid pages")
+
+
+def test_argument_errors(iva, dev):
+    d = iva.workloads.decode_batch([10], 4, 2, 128, torch.float16, seed=12)
+    lay = d["layout"]
+    q, kp, vp = d["q"].to(dev), d["k_pool"].to(dev), d["v_pool"].to(dev)
+    bt, cl = lay.block_tables.to(dev), lay.context_lens.to(dev)
+    with pytest.raises(iva._abi.IvakvError, match="GQA group"):
+        iva.paged_decode_attention(torch.zeros(1, 34, 128, dtype=torch.float16, device=dev),
+                                   torch.zeros(1, 2, 16, 16, 8, dtype=torch.float16, device=dev),
+                                   torch.zeros(1, 2, 128, 16, dtype=torch.float16, device=dev), bt, cl)
+    with pytest.raises(iva._abi.IvakvError, match="head_dim"):
+        iva.paged_decode_attention(torch.zeros(1, 4, 96, dtype=torch.float16, device=dev),
+                                   torch.zeros(1, 2, 12, 16, 8, dtype=torch.float16, device=dev),
+                                   torch.zeros(1, 2, 96, 16, dtype=torch.float16, device=dev), bt, cl)
+    with pytest.raises(TypeError):
+        iva.paged_decode_attention(q.float(), kp, vp, bt, cl)
+    with pytest.raises(ValueError):
+        iva.paged_decode_attention(q, kp, vp, bt, cl, workspace=torch.empty(1, dtype=torch.uint8, device=dev),
+                                   partition_pages=1)
+
+
+# ---------------------------------------------------------------- full-size configs
+
+def test_c2_full_size(iva, dev):
+    """C2: B 32, GQA 32/8, D 128, fp16, context U[512, 4096]: every sequence vs torch fp32,
+    four of them vs the fp64 oracle; max abs err <= 2e-3."""
+    d = iva.workloads.c2_decode(seed=0, device=dev)
+    lay = d["layout"]
+    bt = lay.block_tables.to(dev)
+    out = iva.paged_decode_attention(d["q"], d["k_pool"], d["v_pool"], bt, lay.context_lens.to(dev))
+    scale = 1 / math.sqrt(128)
+    ref = torch_reference(d["q"], d["k_pool"], d["v_pool"], bt, lay.lengths, scale)
+    err = (out.float() - ref).abs().max().item()
+    assert err <= 2e-3, f"C2 max abs err vs torch fp32 {err}"
+    pick = [0, 7, 19, 31]
+    sub = iva.workloads.PagedLayout([lay.lengths[i] for i in pick], lay.block_tables[pick], lay.num_pages)
+    exact = orc.decode_attention(to_np(d["q"][pick]), to_np(d["k_pool"]), to_np(d["v_pool"]),
+                                 sub.block_tables.numpy(), sub.context_lens.numpy())
+    err64 = float(np.abs(to_np(out[pick]) - exact).max())
+    assert err64 <= 2e-3, f"C2 max abs err vs fp64 oracle {err64}"
+
+
+def test_c4_long_context(iva, dev):
+    """C4: B 4 at 32k..128k tokens, window 4096 + 4 sinks, bf16, K/V ~ N(0,1)."""
+    d = iva.workloads.c4_long_context(seed=0, device=dev)
+    lay = d["layout"]
+    bt = lay.block_tables.to(dev)
+    out = iva.paged_decode_attention(d["q"], d["k_pool"], d["v_pool"], bt, lay.context_lens.to(dev),
+                                     window=d["window"], n_sink=d["n_sink"])
+    ref = torch_reference(d["q"], d["k_pool"], d["v_pool"], bt, lay.lengths, 1 / math.sqrt(128),
+                          window=d["window"], n_sink=d["n_sink"])
+    err = (out.float() - ref).abs().max().item()
+    assert err <= 2e-3, f"C4 max abs err {err}"
+
+
+def test_c5_ragged(iva, dev):
+    """C5 shapes: 256 ragged sequences (LogNormal median 1024, sigma 1, cap 16k), fp16."""
+    lengths = iva.workloads.c5_lengths(seed=0)
+    d = iva.workloads.decode_batch(lengths, 32, 8, 128, torch.float16, seed=5, device=dev,
+                                   scale=128 ** -0.5)
+    lay = d["layout"]
+    bt = lay.block_tables.to(dev)
+    out = iva.paged_decode_attention(d["q"], d["k_pool"], d["v_pool"], bt, lay.context_lens.to(dev))
+    ref = torch_reference(d["q"], d["k_pool"], d["v_pool"], bt, lay.lengths, 1 / math.sqrt(128))
+    err = (out.float() - ref).abs().max().item()
+    assert err <= 2e-3, f"C5 max abs err {err}"
+
+
+def test_golden_tiny_fixture(iva, dev):
+    """tests/golden/decode_tiny.npz: fp32, GQA 4/2, head_dim 8 is below the kernel's minimum
+    head_dim, so the fixture's rows are zero-padded to 64 dims (padding changes no score
+    and no output column); expected values were evaluated term by term in pure Python."""
+    from pathlib import Path
+    g = np.load(Path(__file__).resolve().parent / "golden" / "decode_tiny.npz")
+    kp8, vp8 = g["k_pool"], g["v_pool"]            # [P, 2, 2, 16, 4], [P, 2, 8, 16]
+    p, h = kp8.shape[:2]
+    kp = np.zeros((p, h, 16, 16, 4), np.float32)
+    kp[:, :, :2] = kp8
+    vp = np.zeros((p, h, 64, 16), np.float32)
+    vp[:, :, :8] = vp8
+    q = np.zeros((2, 4, 64), np.float32)
+    q[:, :, :8] = g["q"]
+    out = iva.paged_decode_attention(torch.from_numpy(q).to(dev), torch.from_numpy(kp).to(dev),
+                                     torch.from_numpy(vp).to(dev),
+                                     torch.from_numpy(g["block_tables"]).to(dev),
+                                     torch.from_numpy(g["context_lens"]).to(dev),
+                                     scale=1 / math.sqrt(8), window=int(g["window"]),
+                                     n_sink=int(g["n_sink"]))
+    err = np.abs(to_np(out)[:, :, :8] - g["expected"]).max()
+    assert err <= 1e-5, f"golden fixture max abs err {err}"
+    assert not to_np(out)[:, :, 8:].any()
+
+
+def test_context_beyond_block_table(iva, dev):
+    """context_lens larger than the block table can address: positions past the table are
+    not attended (and no partition reaches past the workspace)."""
+    d = iva.workloads.decode_batch([300, 40], 8, 2, 128, torch.float16, seed=13, scale=128 ** -0.5)
+    lay = d["layout"]
+    lay2 = iva.workloads.PagedLayout([300 + 5000, 40], lay.block_tables, lay.num_pages)
+    out = run_gpu(iva, dev, d, layout=lay2)
+    assert_close(out, oracle_out(d, layout=lay2), torch.float16, rel_ulp=False, what="ctx > table")
+    out_w = run_gpu(iva, dev, d, layout=lay2, window=200, n_sink=4)
+    assert_close(out_w, oracle_out(d, layout=lay2, window=200, n_sink=4), torch.float16,
+                 rel_ulp=False, what="ctx > table, window")

@@ -1,0 +1,325 @@
+"""Pins the CPU oracle (no GPU).  Each check is independent of the formula it pins:
+brute-force loops over the documented address formula, round trips, the
+reference's own contiguous KVCache restatement, a library routine (torch SDPA),
+closed forms, invariances, and golden fixtures.  Planted mistakes in the oracle
+must make at least one check fail."""
+from __future__ import annotations
+
+import hashlib
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import paged_kv as orc
+from oracle import reference_path as rp
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def rand_case(seed, lengths, hkv, d, bs, dtype=np.float32, extra=3):
+    rng = np.random.default_rng(seed)
+    need = sum(-(-n // bs) for n in lengths)
+    num_pages = need + extra
+    perm = rng.permutation(num_pages)
+    mb = max(-(-n // bs) for n in lengths) if lengths else 1
+    bt = np.full((len(lengths), max(mb, 1)), -1, dtype=np.int64)
+    cur = 0
+    for b, n in enumerate(lengths):
+        k = -(-n // bs)
+        bt[b, :k] = perm[cur:cur + k]
+        cur += k
+    n_tok = sum(lengths)
+    k_new = rng.standard_normal((n_tok, hkv, d)).astype(dtype)
+    v_new = rng.standard_normal((n_tok, hkv, d)).astype(dtype)
+    slots = np.concatenate([[bt[b, p // bs] * bs + p % bs for p in range(n)]
+                            for b, n in enumerate(lengths)]).astype(np.int64) if n_tok else np.zeros(0, np.int64)
+    return dict(bt=bt, ctx=np.array(lengths, dtype=np.int64), k_new=k_new, v_new=v_new, slots=slots,
+                num_pages=num_pages)
+
+
+# ------------------------------------------------------------------ append / gather
+
+@pytest.mark.parametrize("dtype,d,bs", [(np.float32, 8, 4), (np.float16, 16, 16), (np.float32, 12, 3)])
+def test_append_gather_vs_address_formula_loops(dtype, d, bs):
+    c = rand_case(1, [5, 1, 9], 2, d, bs, dtype)
+    slots = c["slots"].copy()
+    slots[2] = -1
+    kp, vp = orc.empty_pools(c["num_pages"], 2, d, bs, dtype, fill=7)
+    orc.append(kp, vp, c["k_new"], c["v_new"], slots)
+    kf, vf = orc.empty_pools(c["num_pages"], 2, d, bs, dtype, fill=7)
+    kf, vf = kf.reshape(-1), vf.reshape(-1)
+    orc.append_loops(kf, vf, c["k_new"], c["v_new"], slots, c["num_pages"], 2, d, bs)
+    assert np.array_equal(kp.reshape(-1), kf) and np.array_equal(vp.reshape(-1), vf)
+    bt = c["bt"].copy()
+    bt[2, 0] = -4  # invalid page
+    ko, vo = orc.gather(kp, vp, bt, c["ctx"], out_len=12)
+    lk, lv = orc.gather_loops(kf, vf, bt, c["ctx"], c["num_pages"], 2, d, bs, 12)
+    assert np.array_equal(ko, lk) and np.array_equal(vo, lv)
+
+
+def test_round_trip_and_canary():
+    c = rand_case(2, [17, 64, 129, 200], 8, 64, 16)
+    kp, vp = orc.empty_pools(c["num_pages"], 8, 64, 16, np.float32, fill=np.float32(-3.5))
+    orc.append(kp, vp, c["k_new"], c["v_new"], c["slots"])
+    ko, vo = orc.gather(kp, vp, c["bt"], c["ctx"])
+    start = 0
+    for b, n in enumerate(c["ctx"]):
+        assert np.array_equal(ko[b, :, :n], c["k_new"][start:start + n].transpose(1, 0, 2))
+        assert np.array_equal(vo[b, :, :n], c["v_new"][start:start + n].transpose(1, 0, 2))
+        assert not ko[b, :, n:].any()
+        start += n
+    # pages no sequence owns keep the canary in every word
+    used = set(c["bt"][c["bt"] >= 0].tolist())
+    for p in range(c["num_pages"]):
+        if p not in used:
+            assert (kp[p] == -3.5).all() and (vp[p] == -3.5).all()
+
+
+def test_page_permutation_invariance():
+    """The same logical content under two different page assignments gathers identically."""
+    a = rand_case(3, [40, 7], 2, 16, 8)
+    b = dict(a)
+    rng = np.random.default_rng(99)
+    perm = rng.permutation(a["num_pages"])
+    b_bt = np.where(a["bt"] >= 0, perm[np.maximum(a["bt"], 0)], -1)
+    b_slots = perm[a["slots"] // 8] * 8 + a["slots"] % 8
+    outs = []
+    for bt, slots in ((a["bt"], a["slots"]), (b_bt, b_slots)):
+        kp, vp = orc.empty_pools(a["num_pages"], 2, 16, 8, np.float32)
+        orc.append(kp, vp, a["k_new"], a["v_new"], slots)
+        outs.append(orc.gather(kp, vp, bt, a["ctx"]))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+
+
+def test_gather_matches_reference_kvcache():
+    """Paged gather == the reference's contiguous KVCache (rope_kv.py:98-137) fed with the
+    same rows through update() in uneven chunks (exercising its grow-by-copy resize)."""
+    c = rand_case(4, [17, 64, 129, 200], 8, 64, 16)
+    kp, vp = orc.empty_pools(c["num_pages"], 8, 64, 16, np.float32)
+    orc.append(kp, vp, c["k_new"], c["v_new"], c["slots"])
+    ko, vo = orc.gather(kp, vp, c["bt"], c["ctx"])
+    start = 0
+    for b, n in enumerate(c["ctx"].tolist()):
+        cache = rp.ContiguousKVCache(1, 8, 64, 0, dtype=torch.float32)
+        rows_k = torch.from_numpy(c["k_new"][start:start + n]).permute(1, 0, 2).unsqueeze(0)
+        rows_v = torch.from_numpy(c["v_new"][start:start + n]).permute(1, 0, 2).unsqueeze(0)
+        pos = 0
+        for chunk in (1, 3, 16, 50, 1000):
+            e = min(n, pos + chunk)
+            if e > pos:
+                cache.update(rows_k[:, :, pos:e], rows_v[:, :, pos:e], pos)
+            pos = e
+        ck, cv = cache.get_slice(0, n)
+        assert np.array_equal(ck[0].numpy(), ko[b, :, :n]) and np.array_equal(cv[0].numpy(), vo[b, :, :n])
+        start += n
+
+
+def test_c1_golden_digests():
+    """The oracle reproduces the committed C1 digests from the seed."""
+    import __graft_entry__
+    iva = __graft_entry__.load_package()
+    gold = json.loads((GOLDEN / "c1.json").read_text())
+    w = iva.workloads.c1_append_gather(seed=gold["seed"])
+    sha = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+    k_new, v_new = w["k_new"].numpy().view(np.uint32), w["v_new"].numpy().view(np.uint32)
+    assert sha(k_new) == gold["k_new_sha256"] and sha(v_new) == gold["v_new_sha256"]
+    assert w["layout"].block_tables.tolist() == gold["block_tables"]
+    kp, vp = orc.empty_pools(64, 8, 64, 16, np.uint32)
+    orc.append(kp, vp, k_new, v_new, w["slot_mapping"].numpy())
+    ko, vo = orc.gather(kp, vp, w["layout"].block_tables.numpy(), w["layout"].context_lens.numpy())
+    assert sha(ko) == gold["k_out_sha256"] and sha(vo) == gold["v_out_sha256"]
+
+
+# ------------------------------------------------------------------ decode attention
+
+def attn_case(seed, lengths, hq, hkv, d, bs=16, scale_vals=1.0):
+    c = rand_case(seed, lengths, hkv, d, bs)
+    c["k_new"] *= scale_vals
+    kp, vp = orc.empty_pools(c["num_pages"], hkv, d, bs, np.float32)
+    orc.append(kp, vp, c["k_new"], c["v_new"], c["slots"])
+    rng = np.random.default_rng(seed + 1000)
+    c.update(kp=kp, vp=vp, q=rng.standard_normal((len(lengths), hq, d)), hq=hq, hkv=hkv, d=d)
+    return c
+
+
+def sdpa_reference(c, scale=None, window=0, n_sink=0):
+    """torch.nn.functional.scaled_dot_product_attention in fp64 on the gathered rows."""
+    ko, vo = orc.gather(c["kp"], c["vp"], c["bt"], c["ctx"])
+    out = np.zeros((len(c["ctx"]), c["hq"], c["d"]))
+    g = c["hq"] // c["hkv"]
+    for b, n in enumerate(c["ctx"].tolist()):
+        if n == 0:
+            continue
+        k = torch.from_numpy(ko[b, :, :n]).double().repeat_interleave(g, 0)
+        v = torch.from_numpy(vo[b, :, :n]).double().repeat_interleave(g, 0)
+        q = torch.from_numpy(c["q"][b]).double().unsqueeze(1)
+        j = torch.arange(n)
+        mask = (j >= n - window) | (j < n_sink) if window else torch.ones(n, dtype=torch.bool)
+        o = F.scaled_dot_product_attention(q, k, v, attn_mask=mask.view(1, 1, n), scale=scale)
+        out[b] = o.squeeze(1).numpy()
+    return out
+
+
+def check_sdpa(fn, seed=5):
+    ok = True
+    for lengths, hq, hkv, d, window, sink in (([1, 20, 77], 8, 2, 16, 0, 0),
+                                              ([90, 33, 5], 4, 4, 8, 10, 3),
+                                              ([64, 200], 6, 2, 32, 31, 0)):
+        c = attn_case(seed, lengths, hq, hkv, d)
+        got = fn(c["q"], c["kp"], c["vp"], c["bt"], c["ctx"], window=window, n_sink=sink)
+        ok &= np.allclose(got, sdpa_reference(c, window=window, n_sink=sink), atol=1e-10)
+    return ok
+
+
+def check_closed_forms(fn):
+    ok = True
+    # one key -> v[0]
+    c = attn_case(6, [1], 4, 2, 8)
+    got = fn(c["q"], c["kp"], c["vp"], c["bt"], c["ctx"])
+    _, vo = orc.gather(c["kp"], c["vp"], c["bt"], c["ctx"])
+    ok &= np.allclose(got[0], np.repeat(vo[0, :, 0], 2, axis=0), atol=1e-12)
+    # identical keys -> mean of v (per kv head)
+    c = attn_case(7, [37], 4, 2, 8)
+    c["kp"][:] = c["kp"][c["bt"][0, 0], :, :, :1, :][None]
+    got = fn(c["q"], c["kp"], c["vp"], c["bt"], c["ctx"])
+    _, vo = orc.gather(c["kp"], c["vp"], c["bt"], c["ctx"])
+    ok &= np.allclose(got[0], np.repeat(vo[0, :, :37].mean(axis=1), 2, axis=0), atol=1e-12)
+    # one dominant score -> that row's v: key 13 of kv head h is 60*q of query head 2h
+    c = attn_case(8, [40], 4, 2, 8)
+    ko, vo = orc.gather(c["kp"], c["vp"], c["bt"], c["ctx"])
+    rows_k = ko[0].transpose(1, 0, 2).copy()  # [L, Hkv, D]
+    for h in range(2):
+        rows_k[13, h] = 60.0 * c["q"][0, 2 * h]
+    kp, vp = orc.empty_pools(c["num_pages"], 2, 8, 16, np.float32)
+    slots = np.array([c["bt"][0, p // 16] * 16 + p % 16 for p in range(40)])
+    orc.append(kp, vp, rows_k.astype(np.float32), vo[0].transpose(1, 0, 2), slots)
+    got = fn(c["q"], kp, vp, c["bt"], c["ctx"])
+    for h in range(2):
+        ok &= np.allclose(got[0, 2 * h], vo[0, h, 13], atol=1e-6)
+    return ok
+
+
+def check_window_brute_force(fn):
+    """Window/sink sets vs pure-Python term-by-term evaluation on tiny inputs."""
+    ok = True
+    for window, sink in ((3, 0), (4, 2), (1, 1), (50, 1)):
+        c = attn_case(9 + window, [11, 3, 20], 4, 2, 4, bs=4)
+        ko, vo = orc.gather(c["kp"], c["vp"], c["bt"], c["ctx"])
+        exp = orc.decode_attention_loops(c["q"].tolist(), ko.tolist(), vo.tolist(), c["ctx"].tolist(),
+                                         1 / math.sqrt(4), window, sink)
+        got = fn(c["q"], c["kp"], c["vp"], c["bt"], c["ctx"], window=window, n_sink=sink)
+        ok &= np.allclose(got, np.array(exp), atol=1e-12)
+    return ok
+
+
+def check_reference_path(fn):
+    """Agreement with the restated reference path (torch.cat append + AttentionTorch math)."""
+    lengths = [30, 7, 64]
+    c = attn_case(11, lengths, 8, 2, 16)
+    ko, vo = orc.gather(c["kp"], c["vp"], c["bt"], c["ctx"])
+    lmax = max(lengths)
+    cache_k = torch.zeros(3, 2, lmax - 1, 16, dtype=torch.float64)
+    cache_v = torch.zeros_like(cache_k)
+    valid = torch.zeros(3, lmax - 1, dtype=torch.bool)
+    k_new = torch.zeros(3, 2, 1, 16, dtype=torch.float64)
+    v_new = torch.zeros_like(k_new)
+    for b, n in enumerate(lengths):
+        cache_k[b, :, :n - 1] = torch.from_numpy(ko[b, :, :n - 1])
+        cache_v[b, :, :n - 1] = torch.from_numpy(vo[b, :, :n - 1])
+        valid[b, :n - 1] = True
+        k_new[b, :, 0] = torch.from_numpy(ko[b, :, n - 1])
+        v_new[b, :, 0] = torch.from_numpy(vo[b, :, n - 1])
+    ok = True
+    for window, sink in ((None, 0), (9, 2)):
+        ref = rp.reference_decode_step(cache_k, cache_v, valid, torch.tensor(lengths),
+                                       torch.from_numpy(c["q"]).unsqueeze(2), k_new, v_new,
+                                       1 / math.sqrt(16), window=window, n_sink=sink)
+        got = fn(c["q"], c["kp"], c["vp"], c["bt"], c["ctx"], window=window or 0, n_sink=sink)
+        ok &= np.allclose(got, ref.squeeze(2).numpy(), atol=1e-12)
+    return ok
+
+
+def check_permutation(fn):
+    c = attn_case(12, [70, 19], 4, 2, 8)
+    got_a = fn(c["q"], c["kp"], c["vp"], c["bt"], c["ctx"])
+    perm = np.random.default_rng(5).permutation(c["num_pages"])
+    inv = np.argsort(perm)
+    kp2, vp2 = c["kp"][inv], c["vp"][inv]  # page p moves to index perm[p]
+    bt2 = np.where(c["bt"] >= 0, perm[np.maximum(c["bt"], 0)], -1)
+    got_b = fn(c["q"], kp2, vp2, bt2, c["ctx"])
+    return np.allclose(got_a, got_b, atol=1e-13)
+
+
+PIN_CHECKS = [check_sdpa, check_closed_forms, check_window_brute_force, check_reference_path,
+              check_permutation]
+
+
+@pytest.mark.parametrize("check", PIN_CHECKS, ids=lambda f: f.__name__)
+def test_decode_oracle_pins(check):
+    assert check(orc.decode_attention)
+
+
+def test_decode_golden_fixture():
+    g = np.load(GOLDEN / "decode_tiny.npz")
+    got = orc.decode_attention(g["q"], g["k_pool"], g["v_pool"], g["block_tables"],
+                               g["context_lens"], window=int(g["window"]), n_sink=int(g["n_sink"]))
+    assert np.allclose(got, g["expected"], atol=1e-12)
+
+
+def _mutant_no_scale(q, kp, vp, bt, ctx, scale=None, window=0, n_sink=0):
+    return orc.decode_attention(q, kp, vp, bt, ctx, scale=1.0, window=window, n_sink=n_sink)
+
+
+def _mutant_swap_kv(q, kp, vp, bt, ctx, scale=None, window=0, n_sink=0):
+    # K pages read as if they were V pages and vice versa (transposed operand roles)
+    p, h, nch, bs, x = kp.shape
+    kp2 = vp.reshape(p, h, nch, x, bs).transpose(0, 1, 2, 4, 3).copy()
+    vp2 = kp.transpose(0, 1, 2, 4, 3).reshape(p, h, nch * x, bs).copy()
+    return orc.decode_attention(q, kp2, vp2, bt, ctx, scale=scale, window=window, n_sink=n_sink)
+
+
+@pytest.mark.parametrize("mutant", ["no_scale", "gqa_tile", "window_off_by_one", "sink_and",
+                                    "swap_kv"])
+def test_planted_mistakes_are_caught(monkeypatch, mutant):
+    fn = orc.decode_attention
+    if mutant == "no_scale":
+        fn = _mutant_no_scale
+    elif mutant == "swap_kv":
+        fn = _mutant_swap_kv
+    elif mutant == "gqa_tile":
+        monkeypatch.setattr(orc, "expand_gqa", lambda x, g: np.concatenate([x] * g, axis=0))
+    elif mutant == "window_off_by_one":
+        real = orc.visible
+        monkeypatch.setattr(orc, "visible",
+                            lambda n, w=0, s=0: real(n, w - 1, s) if w and w > 1 else real(n, w, s))
+    elif mutant == "sink_and":
+        # the reference's successive masked_fill ANDs the sink mask into the window mask,
+        # which drops the sinks (attention.py:83-93)
+        real = orc.visible
+        monkeypatch.setattr(orc, "visible", lambda n, w=0, s=0: real(n, w, 0))
+    results = [check(fn) for check in PIN_CHECKS]
+    assert not all(results), f"planted mistake {mutant} passed every pin check"
+
+
+# ------------------------------------------------------------------ index ops
+
+def test_index_ops_vs_torch():
+    rng = np.random.default_rng(13)
+    kv = rng.standard_normal((2, 3, 10, 8)).astype(np.float32)
+    idx = np.array([9, 0, 4, 4, 7])
+    got = orc.index_gather(kv, idx)
+    assert np.array_equal(got, torch.from_numpy(kv)[:, :, torch.from_numpy(idx)].numpy())
+    for j, i in enumerate(idx):
+        assert np.array_equal(got[:, :, j], kv[:, :, i])
+    uniq = np.array([9, 0, 4, 7])
+    vals = rng.standard_normal((2, 3, 4, 8)).astype(np.float32)
+    out = orc.index_scatter(kv, uniq, vals)
+    ref = torch.from_numpy(kv).clone()
+    ref[:, :, torch.from_numpy(uniq)] = torch.from_numpy(vals)
+    assert np.array_equal(out, ref.numpy())
+    assert not np.shares_memory(out, kv)
