@@ -241,10 +241,10 @@ __global__ __launch_bounds__(kThreads) void decode_partial_kernel(DecodeArgs a) 
       vis[r] = cur_phys >= 0 && pos < w.L && (pos >= w.win_start || pos < a.n_sink);
       sl[r] = vis[r] ? s[r] * a.scale_log2 : kNegInf;
     }
-    if (__any(!(vis[0] && vis[1] && vis[2] && vis[3]))) {
+    // Unconditional (branch-free): a branch here would separate the QK MFMAs
+    // from the first read of their accumulator by a basic-block boundary.
 #pragma unroll
-      for (int m = 0; m < NB; ++m) Tr::mask_rows(vc[m], vis);
-    }
+    for (int m = 0; m < NB; ++m) Tr::mask_rows(vc[m], vis);
     float mx = fmaxf(fmaxf(sl[0], sl[1]), fmaxf(sl[2], sl[3]));
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));

@@ -135,7 +135,8 @@ def test_closed_forms(iva, dev, dtype):
     k_pool, v_pool = d["k_pool"].clone(), d["v_pool"].clone()
     # sequence 1: make all 64 keys identical (copy row 0 of its first page everywhere)
     pages = lay.block_tables[1, :4].long()
-    k_pool[pages] = k_pool[pages[0]].select(3, 0).unsqueeze(3).unsqueeze(0).expand_as(k_pool[pages]).clone()
+    # k_pool[p] is [Hkv, D/X, bs, X]: row 0 of the first page is [:, :, 0:1, :]
+    k_pool[pages] = k_pool[pages[0]][:, :, 0:1, :].unsqueeze(0).expand_as(k_pool[pages]).clone()
     d2 = dict(d, k_pool=k_pool, v_pool=v_pool)
     out = run_gpu(iva, dev, d2).float().cpu()
     # one key: exactly the V row of position 0
@@ -178,7 +179,7 @@ def test_invalid_pages_are_not_attended(iva, dev):
 
 
 def test_argument_errors(iva, dev):
-    d = iva.workloads.decode_batch([10], 4, 2, 128, torch.float16, seed=12)
+    d = iva.workloads.decode_batch([40], 4, 2, 128, torch.float16, seed=12)  # 3 pages
     lay = d["layout"]
     q, kp, vp = d["q"].to(dev), d["k_pool"].to(dev), d["v_pool"].to(dev)
     bt, cl = lay.block_tables.to(dev), lay.context_lens.to(dev)
