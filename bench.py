@@ -139,7 +139,7 @@ def main():
     max_blocks = sets[0]["bt"].shape[1]
     ws_bytes = iva.decode_workspace_bytes(batch, hq, hkv, d, 16, max_blocks,
                                           partition_pages=args.partition_pages)
-    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    workspace = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     pp = args.partition_pages or None
 
     def step(s):

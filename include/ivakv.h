@@ -96,9 +96,14 @@ int ivakv_gather(const void* k_pool, const void* v_pool,
                  void* k_out, void* v_out, int dtype, hipStream_t stream);
 
 /*
- * Bytes of device workspace ivakv_decode_attn needs for this geometry
- * (fp32 partial accumulators + per-partition max/sum).  partition_pages <= 0
- * selects the library default.
+ * Bytes of device workspace ivakv_decode_attn (and its _partial/_merge halves)
+ * needs for this geometry.  The default walk (partition_pages <= 0, batch <=
+ * 8192) keeps one fp32 partial (max, sum, acc[G][D]) per wave of its wave
+ * budget (4096) plus one per (sequence, kv head), and the batch's page prefix.
+ * partition_pages > 0 selects the partitioned walk, whose workspace holds one
+ * partial per (sequence, kv head, partition) and is 0 when no sequence spans
+ * more than one partition.  The contents need no initialisation; calls that
+ * share a workspace must not run concurrently.
  */
 int ivakv_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
                                 int head_dim, int block_size, int max_blocks,
@@ -112,8 +117,12 @@ int ivakv_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
  *   j < L  and  (window <= 0  or  j >= L - window  or  j < n_sink).
  * KV head of query head hq is hq / (num_q_heads / num_kv_heads).
  * q, out = [batch][num_q_heads][D] dense.  L == 0 gives a zero row.
- * fp32 accumulation; the context is split into partitions of
- * partition_pages pages that are merged with a log-sum-exp reduction.
+ * fp32 accumulation.  Default walk: the (sequence, kv head, page) tiles of the
+ * whole batch are dealt out in equal contiguous shares to a fixed set of
+ * wavefronts sized to the device; a (sequence, kv head) split between
+ * wavefronts is merged with a log-sum-exp reduction.  partition_pages > 0
+ * instead splits each sequence into partitions of that many pages (one
+ * workgroup each) merged the same way.
  * Supported: block_size 16, head_dim 64/128/256, num_q_heads/num_kv_heads
  * in {1,2,4,8,16}.
  * Replaces: the cache branch of AttentionTorch.forward -- scores, causal /
@@ -129,11 +138,12 @@ int ivakv_decode_attn(const void* q, const void* k_pool, const void* v_pool,
                       hipStream_t stream);
 
 /*
- * The two halves of ivakv_decode_attn, same arguments.  _partial runs the
- * paged walk (and writes `out` directly for sequences that fit in one
- * partition); _merge folds the per-partition (max, sum, acc) triples into
- * `out`.  Exposed so a caller can time the walk alone or merge partials that
- * come from several devices (context-parallel sharding of one sequence).
+ * The two launches of ivakv_decode_attn, same arguments and same walk.
+ * _partial runs the paged walk (writing `out` directly for every (sequence, kv
+ * head) a single wavefront or partition covers); _merge folds the partials of
+ * the others into `out` (and zero-fills empty sequences).  Exposed so a caller
+ * can time the walk alone or merge partials that come from several devices
+ * (context-parallel sharding of one sequence).
  * Replaces: same reference code as ivakv_decode_attn.
  */
 int ivakv_decode_attn_partial(const void* q, const void* k_pool, const void* v_pool,

@@ -1,22 +1,31 @@
 // Paged single-query (decode) attention for gfx950.
 //
-// Work split: grid (partition, kv head, sequence), 4 wavefronts per workgroup.
-// A partition is `part_pages` consecutive effective pages of one (sequence,
-// kv head); wave w of the workgroup walks pages w, w+4, w+8, ... of it.  All
-// Hq/Hkv query heads of the kv head share every page the wave loads (GQA reuse).
+// One tile = one (page, kv head): 16 rows of K and of V, 2 * 16 * D * esize
+// contiguous bytes in the pools.  A wavefront scores a tile for all Hq/Hkv
+// query heads of its kv head at once (GQA reuse of every byte loaded).
 //
-// Per page (16 rows) a wave issues D/X/4 16-byte K loads and D/16 V loads per
-// lane.  The pool layout puts these loads directly in MFMA operand order:
+// Per tile a wave issues D/X/4 16-byte K loads and D/16 V loads per lane.  The
+// pool layout puts these loads directly in MFMA operand order:
 //   S^T[row][head]  = K_page(16 x D) . Q^T(D x 16)      v_mfma 16x16x32 (f16/bf16)
 //   O^T[dim][head] += V^T_page(D x 16) . P^T(16 x 16)   v_mfma 16x16x16 (f16/bf16)
 // (16x16x4 f32 MFMAs for fp32).  The QK accumulator of lane l holds rows
 // 4*(l/16)+r of head l%16, which is exactly the B operand layout the PV MFMA
 // wants, so P never leaves registers.  Only heads l%16 < Hq/Hkv carry data.
-//
 // Softmax runs online in fp32 in the log2 domain (scale*log2(e) folded into the
-// scores, v_exp_f32).  The four waves merge through LDS; a sequence that fits in
-// one partition writes `out` directly, otherwise each partition writes an
-// unnormalised (max, sum, acc) triple that decode_merge_kernel folds together.
+// scores, v_exp_f32).
+//
+// Two walks share that tile code:
+//   stream walk (default): a fixed set of waves, sized to
+//     what the CUs hold at once, each takes an equal contiguous share of the
+//     flattened (sequence, kv head, page) tile list and streams it through a
+//     ring of register page buffers, crossing (sequence, kv head) boundaries
+//     without draining.  Exact load balance in bytes whatever the context
+//     lengths; a unit split between waves leaves one partial per wave that
+//     decode_stream_merge_kernel folds together (log-sum-exp).
+//   partitioned walk (partition_pages > 0, or a batch too large for the
+//     stream walk's page prefix in LDS): grid (kv head, sequence, partition) of 4-wave
+//     workgroups; a partition of part_pages pages is split over the 4 waves
+//     and merged through LDS, then across partitions by decode_merge_kernel.
 #include "ivakv_internal.h"
 
 namespace ivakv {
@@ -39,7 +48,16 @@ struct alignas(8) Chunk8 {
 constexpr int kBS = 16;       // rows per page == MFMA tile edge
 constexpr int kWaves = 4;     // wavefronts per workgroup
 constexpr int kThreads = 64 * kWaves;
-constexpr int kDefaultPartitionPages = 16;
+constexpr int kDefaultPartitionPages = 32;
+constexpr int kPageBufs = 2;  // register page buffers per wave (ring)
+// Workgroups per CU both walks are built for (two 4-wave groups: 2 waves per
+// SIMD, up to 256 registers each), and for the stream walk the wave
+// budget the workspace is sized for, the fewest tiles worth giving a wave, and
+// the largest batch whose page prefix fits the workgroup's LDS.
+constexpr int kStreamWGsPerCU = 2;
+constexpr int kMaxStreamWaves = 4096;
+constexpr int kMinTilesPerWave = 4;
+constexpr int kMaxStreamBatch = 8192;
 constexpr float kNegInf = -__builtin_huge_valf();
 
 struct DecodeArgs {
@@ -49,11 +67,13 @@ struct DecodeArgs {
   const int32_t* bt;
   const int32_t* ctx;
   void* out;
-  float* ws_acc;  // [B][Hkv][n_parts_max][G][D]
-  float* ws_ml;   // [B][Hkv][n_parts_max][G][2]  (max, sum)
-  int Hkv, G, max_blocks, num_pages;
+  float* ws_acc;       // partitioned: [B][Hkv][n_parts_max][G][D]; stream: [slot][G][D]
+  float* ws_ml;        // same slots x [G][2]  (max, sum)
+  int32_t* ws_pref;    // stream: [B + 1] page prefix of the batch (written by workgroup 0)
+  int batch, Hkv, G, max_blocks, num_pages;
   float scale_log2;
   int window, n_sink, part_pages, n_parts_max;
+  int n_waves;         // stream: waves launched
 };
 
 // Zeroes the 16-bit V elements of rows that are not attended.  A row outside
@@ -144,6 +164,25 @@ struct Traits<IVAKV_F32> {
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// A value every lane of the wave holds (e.g. read from LDS at a uniform
+// address), made visibly uniform so addresses built from it stay scalar: block
+// table and context reads then use the scalar cache and lgkmcnt, and never make
+// the wave wait for its outstanding page loads.
+__device__ inline int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ inline int logical_page(const PageWalk& w, int v) {
+  return v < w.sink_pages ? v : w.win_first + (v - w.sink_pages);
+}
+
+// Effective pages of a walk whose logical page lies inside the block table
+// (logical_page is increasing, so these are the first ones).  Positions on the
+// pages past the table are never attended, so the walks stop there.
+__device__ inline int table_pages(const PageWalk& w, int max_blocks) {
+  const int sink = min(w.sink_pages, max_blocks);
+  const int win = min(cdiv(w.L, kBS), max_blocks) - w.win_first;
+  return sink + (win > 0 ? win : 0);
+}
+
 // Partitions of one sequence, capped at the grid's partition count.  The cap only
 // bites when context_lens[b] exceeds what the block table can address; every
 // effective page it drops lies past max_blocks and would be masked anyway.
@@ -152,26 +191,143 @@ __device__ inline int num_partitions(const PageWalk& w, const DecodeArgs& a) {
   return n < a.n_parts_max ? n : a.n_parts_max;
 }
 
-__device__ inline int logical_page(const PageWalk& w, int v) {
-  return v < w.sink_pages ? v : w.win_first + (v - w.sink_pages);
-}
-
+// Register-level tile machinery of one wave (lane = 16 * lq + ln).
 template <int DT, int D>
-__global__ __launch_bounds__(kThreads) void decode_partial_kernel(DecodeArgs a) {
+struct TileOps {
   using Tr = Traits<DT>;
   using E = typename Tr::E;
   using VChunk = typename Tr::VChunk;
-  constexpr int X = 16 / (int)sizeof(E);  // elements per 16-byte K chunk
-  constexpr int KLD = D / X / 4;          // K loads per lane per page
-  constexpr int NB = D / 16;              // 16-dim blocks (PV MFMAs per page)
-  constexpr int64_t kTile = (int64_t)D * kBS;  // elements of one (page, head) tile
+  static constexpr int X = 16 / (int)sizeof(E);  // elements per 16-byte K chunk
+  static constexpr int KLD = D / X / 4;          // K loads per lane per tile
+  static constexpr int NB = D / 16;              // 16-dim blocks (PV MFMAs per tile)
+  static constexpr int64_t kTile = (int64_t)D * kBS;  // elements of one tile
 
-  const int part = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // Online-softmax state of the wave: lane holds head ln's running max (the
+  // same in every k-group), its k-group's share of the running sum, and
+  // O^T[16m + 4lq + r][ln] in acc[m][r].
+  struct State {
+    f32x4 acc[NB];
+    float m_run, l_run;
+    __device__ inline void reset() {
+#pragma unroll
+      for (int m = 0; m < NB; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m_run = kNegInf;
+      l_run = 0.f;
+    }
+    // Sum of head ln over the four k-groups.
+    __device__ inline float total() const {
+      float l = l_run + __shfl_xor(l_run, 16);
+      return l + __shfl_xor(l, 32);
+    }
+  };
+
+  // Query rows of kv head h's group for sequence b, in K-chunk order (chunk
+  // 4*j + lq).  MFMA columns ln >= G repeat head G-1: their scores are never
+  // written out, and the loads stay unconditional (no exec-masked branch,
+  // whose join would make the compiler wait for every outstanding load).
+  static __device__ inline void load_q(const DecodeArgs& a, int b, int h, int ln, int lq,
+                                       Chunk16 (&qr)[KLD]) {
+    const int g = ln < a.G ? ln : a.G - 1;
+    const E* qb = static_cast<const E*>(a.q) + ((int64_t)b * a.Hkv * a.G + h * a.G + g) * D;
+#pragma unroll
+    for (int j = 0; j < KLD; ++j) qr[j] = *reinterpret_cast<const Chunk16*>(qb + (4 * j + lq) * X);
+  }
+
+  // Physical page of logical page lp of sequence b, or -1 when the table entry
+  // is outside the pool.  The tile of an invalid page is read from page 0 and
+  // fully masked.
+  static __device__ inline int64_t phys_page(const DecodeArgs& a, const int32_t* bt, int b, int lp) {
+    const int64_t p = bt[(int64_t)b * a.max_blocks + lp];
+    return (p < 0 || p >= a.num_pages) ? -1 : p;
+  }
+
+  // Issues the loads of one tile.  The empty asm with a memory clobber pins
+  // them here: loads of read-only memory may otherwise be sunk down to their
+  // first use in the next ring step, which serialises load and compute.
+  static __device__ inline void load_tile(const DecodeArgs& a, int64_t phys, int h, int ln, int lq,
+                                          Chunk16 (&kd)[KLD], VChunk (&vd)[NB]) {
+    const int64_t tile = ((phys < 0 ? 0 : phys) * a.Hkv + h) * kTile;
+    const E* kp = static_cast<const E*>(a.k_pool) + tile;
+    const E* vp = static_cast<const E*>(a.v_pool) + tile;
+#pragma unroll
+    for (int j = 0; j < KLD; ++j) kd[j] = *reinterpret_cast<const Chunk16*>(kp + ((4 * j + lq) * kBS + ln) * X);
+#pragma unroll
+    for (int m = 0; m < NB; ++m) vd[m] = *reinterpret_cast<const VChunk*>(vp + (16 * m + ln) * kBS + 4 * lq);
+    __asm__ volatile("" ::: "memory");
+  }
+
+  // Scores one loaded tile of logical page lp and folds it into st.  With
+  // live == false (a padding slot of the ring) every row is masked.
+  static __device__ inline void score(State& st, const Chunk16 (&kc)[KLD], VChunk (&vc)[NB],
+                                      const Chunk16 (&qr)[KLD], const PageWalk& w, int lp,
+                                      bool live, const DecodeArgs& a, int lq) {
+    // S^T = K . Q^T : lane holds rows 4*lq + r of head ln.
+    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KLD; ++j) s = Tr::qk(kc[j], qr[j], s);
+    const int pos0 = lp * kBS + 4 * lq;
+    float sl[4];
+    bool vis[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int pos = pos0 + r;
+      vis[r] = live && pos < w.L && (pos >= w.win_start || pos < a.n_sink);
+      sl[r] = vis[r] ? s[r] * a.scale_log2 : kNegInf;
+    }
+    // Rows that are not attended may hold any bits (0 * NaN would poison acc).
+    // Branch-free: no block boundary between the MFMAs and their first use.
+#pragma unroll
+    for (int m = 0; m < NB; ++m) Tr::mask_rows(vc[m], vis);
+    float mx = fmaxf(fmaxf(sl[0], sl[1]), fmaxf(sl[2], sl[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(st.m_run, mx);
+    const float m_use = m_new == kNegInf ? 0.f : m_new;
+    const float alpha = exp2_fast(st.m_run - m_use);
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = exp2_fast(sl[r] - m_use);
+    st.l_run = st.l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    st.m_run = m_new;
+#pragma unroll
+    for (int m = 0; m < NB; ++m) st.acc[m] *= alpha;
+    // O^T += V^T . P^T
+    const typename Tr::PVec pv = Tr::pack_p(p);
+#pragma unroll
+    for (int m = 0; m < NB; ++m) st.acc[m] = Tr::pv(vc[m], pv, st.acc[m]);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// partitioned walk
+// ---------------------------------------------------------------------------
+
+// Wave w of partition `part` owns effective pages part*part_pages + w + 4*i,
+// i = 0 .. n_mine-1, and streams them through a ring of kPageBufs register
+// page buffers.  Loads are never skipped: past the wave's last page the index
+// is clamped to that page (an L2 hit) and the duplicate is fully masked, so the
+// loop body has no branches and the compiler's vmcnt waits only cover the
+// buffer about to be consumed.
+//
+// Built for two workgroups per CU (like the stream walk): with a higher
+// occupancy target the scheduler sinks each load next to its use and the ring
+// stops overlapping loads with compute.
+// Block table and context lengths come in as __restrict__ parameters, which
+// keeps their reads on the scalar cache (see decode_stream_kernel).
+template <int DT, int D>
+__global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_partial_kernel(
+    DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ ctx) {
+  using Ops = TileOps<DT, D>;
+  using E = typename Ops::E;
+  using VChunk = typename Ops::VChunk;
+  constexpr int KLD = Ops::KLD, NB = Ops::NB;
+
+  const int h = blockIdx.x, b = blockIdx.y, part = blockIdx.z;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ln = lane & 15;  // MFMA column (query head) / row (K row, V dim)
-  const int lq = lane >> 4;  // MFMA k-group
-  const PageWalk w = make_walk(a.ctx[b], a.window, a.n_sink, kBS);
+  const int ln = lane & 15;
+  const int lq = lane >> 4;
+  const PageWalk w = make_walk(ctx[b], a.window, a.n_sink, kBS);
   const int n_parts = num_partitions(w, a);
   if (part >= n_parts) return;
 
@@ -179,103 +335,38 @@ __global__ __launch_bounds__(kThreads) void decode_partial_kernel(DecodeArgs a) 
   const int Hq = a.Hkv * G;
   const bool g_ok = ln < G;
 
-  // Query rows of this kv head's group, in K-chunk order: chunk 4*j + lq.
   Chunk16 qr[KLD];
-  {
-    const E* qb = static_cast<const E*>(a.q) + ((int64_t)b * Hq + h * G + (g_ok ? ln : 0)) * D;
+  Ops::load_q(a, b, h, ln, lq, qr);
+  typename Ops::State st;
+  st.reset();
+
+  const int v_begin = part * a.part_pages + wave;
+  const int v_end = min(min((part + 1) * a.part_pages, w.n_eff), table_pages(w, a.max_blocks));
+  const int n_mine = v_begin < v_end ? cdiv(v_end - v_begin, kWaves) : 0;
+  // Effective page of the wave's i-th slot, clamped to its last page.
+  auto eff_page = [&](int i) { return v_begin + kWaves * min(i, n_mine - 1); };
+
+  if (n_mine > 0) {
+    Chunk16 kb[kPageBufs][KLD];
+    VChunk vb[kPageBufs][NB];
+    int64_t pb[kPageBufs];
 #pragma unroll
-    for (int j = 0; j < KLD; ++j) {
-      qr[j] = g_ok ? *reinterpret_cast<const Chunk16*>(qb + (4 * j + lq) * X) : Chunk16{{0u, 0u, 0u, 0u}};
+    for (int s = 0; s < kPageBufs; ++s) {
+      pb[s] = Ops::phys_page(a, bt, b, logical_page(w, eff_page(s)));
+      Ops::load_tile(a, pb[s], h, ln, lq, kb[s], vb[s]);
+    }
+    for (int i = 0; i < n_mine; i += kPageBufs) {
+#pragma unroll
+      for (int s = 0; s < kPageBufs; ++s) {
+        Ops::score(st, kb[s], vb[s], qr, w, logical_page(w, eff_page(i + s)),
+                   i + s < n_mine && pb[s] >= 0, a, lq);
+        pb[s] = Ops::phys_page(a, bt, b, logical_page(w, eff_page(i + s + kPageBufs)));
+        Ops::load_tile(a, pb[s], h, ln, lq, kb[s], vb[s]);
+      }
     }
   }
 
-  f32x4 acc[NB];
-#pragma unroll
-  for (int m = 0; m < NB; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = kNegInf;  // running max (log2 domain) of head ln
-  float l_run = 0.f;      // this lane's share of the running sum
-
-  const int v_first = part * a.part_pages + wave;
-  const int v_stop = min((part + 1) * a.part_pages, w.n_eff);
-  const E* kpool = static_cast<const E*>(a.k_pool);
-  const E* vpool = static_cast<const E*>(a.v_pool);
-  const int32_t* bt_row = a.bt + (int64_t)b * a.max_blocks;
-
-  Chunk16 kc[KLD];
-  VChunk vc[NB];
-  int64_t cur_phys = -1;
-
-  auto load_page = [&](int v, Chunk16* kd, VChunk* vd) -> int64_t {
-    const int lp = logical_page(w, v);
-    int64_t phys = lp < a.max_blocks ? (int64_t)bt_row[lp] : -1;
-    if (phys < 0 || phys >= a.num_pages) phys = -1;
-    const int64_t tile = ((phys < 0 ? 0 : phys) * a.Hkv + h) * kTile;
-    const E* kp = kpool + tile;
-    const E* vp = vpool + tile;
-#pragma unroll
-    for (int j = 0; j < KLD; ++j) kd[j] = *reinterpret_cast<const Chunk16*>(kp + ((4 * j + lq) * kBS + ln) * X);
-#pragma unroll
-    for (int m = 0; m < NB; ++m) vd[m] = *reinterpret_cast<const VChunk*>(vp + (16 * m + ln) * kBS + 4 * lq);
-    return phys;
-  };
-
-  if (v_first < v_stop) cur_phys = load_page(v_first, kc, vc);
-  for (int v = v_first; v < v_stop; v += kWaves) {
-    Chunk16 kn[KLD];
-    VChunk vn[NB];
-    int64_t next_phys = -1;
-    const bool more = v + kWaves < v_stop;
-    if (more) next_phys = load_page(v + kWaves, kn, vn);
-
-    // S^T = K . Q^T : lane holds rows 4*lq + r of head ln.
-    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < KLD; ++j) s = Tr::qk(kc[j], qr[j], s);
-
-    const int pos0 = logical_page(w, v) * kBS + 4 * lq;
-    float sl[4];
-    bool vis[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int pos = pos0 + r;
-      vis[r] = cur_phys >= 0 && pos < w.L && (pos >= w.win_start || pos < a.n_sink);
-      sl[r] = vis[r] ? s[r] * a.scale_log2 : kNegInf;
-    }
-    // Unconditional (branch-free): a branch here would separate the QK MFMAs
-    // from the first read of their accumulator by a basic-block boundary.
-#pragma unroll
-    for (int m = 0; m < NB; ++m) Tr::mask_rows(vc[m], vis);
-    float mx = fmaxf(fmaxf(sl[0], sl[1]), fmaxf(sl[2], sl[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == kNegInf ? 0.f : m_new;
-    const float alpha = exp2_fast(m_run - m_use);
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = exp2_fast(sl[r] - m_use);
-    l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    m_run = m_new;
-#pragma unroll
-    for (int m = 0; m < NB; ++m) acc[m] *= alpha;
-
-    // O^T += V^T . P^T
-    const typename Tr::PVec pv = Tr::pack_p(p);
-#pragma unroll
-    for (int m = 0; m < NB; ++m) acc[m] = Tr::pv(vc[m], pv, acc[m]);
-
-    if (more) {
-#pragma unroll
-      for (int j = 0; j < KLD; ++j) kc[j] = kn[j];
-#pragma unroll
-      for (int m = 0; m < NB; ++m) vc[m] = vn[m];
-      cur_phys = next_phys;
-    }
-  }
-
-  // Row sum of head ln over the four k-groups.
-  float l_tot = l_run + __shfl_xor(l_run, 16);
-  l_tot += __shfl_xor(l_tot, 32);
+  const float l_tot = st.total();
 
   // Merge the four waves through LDS.
   extern __shared__ float smem[];
@@ -285,7 +376,7 @@ __global__ __launch_bounds__(kThreads) void decode_partial_kernel(DecodeArgs a) 
   float* s_acc = s_fin + 32;               // [kWaves][G][D + 4]
   constexpr int kRow = D + 4;
   if (lq == 0) {
-    s_m[wave * 16 + ln] = m_run;
+    s_m[wave * 16 + ln] = st.m_run;
     s_l[wave * 16 + ln] = l_tot;
   }
   __syncthreads();
@@ -294,10 +385,10 @@ __global__ __launch_bounds__(kThreads) void decode_partial_kernel(DecodeArgs a) 
   for (int u = 0; u < kWaves; ++u) M = fmaxf(M, s_m[u * 16 + ln]);
   const float M_use = M == kNegInf ? 0.f : M;
   if (g_ok) {
-    const float f = exp2_fast(m_run - M_use);
+    const float f = exp2_fast(st.m_run - M_use);
     float* dst = s_acc + (wave * G + ln) * kRow + 4 * lq;
 #pragma unroll
-    for (int m = 0; m < NB; ++m) *reinterpret_cast<f32x4*>(dst + 16 * m) = acc[m] * f;
+    for (int m = 0; m < NB; ++m) *reinterpret_cast<f32x4*>(dst + 16 * m) = st.acc[m] * f;
     if (wave == 0 && lq == 0) {
       float L = 0.f;
 #pragma unroll
@@ -318,7 +409,7 @@ __global__ __launch_bounds__(kThreads) void decode_partial_kernel(DecodeArgs a) 
     if (direct) {
       const float L = s_fin[2 * gg + 1];
       const float r = L > 0.f ? o / L : 0.f;
-      static_cast<E*>(a.out)[((int64_t)b * Hq + h * G + gg) * D + d] = Tr::from_float(r);
+      static_cast<E*>(a.out)[((int64_t)b * Hq + h * G + gg) * D + d] = Ops::Tr::from_float(r);
     } else {
       a.ws_acc[part_base * D + idx] = o;
       if (d == 0) {
@@ -329,44 +420,293 @@ __global__ __launch_bounds__(kThreads) void decode_partial_kernel(DecodeArgs a) 
   }
 }
 
-// Log-sum-exp merge of the partitions of one (sequence, kv head).
+// Weighted sum of n partial (max, sum, acc) slots into out rows of unit (b, h):
+// slot(i) gives the workspace slot of the i-th partial.  Phase 1: wave w
+// reduces heads w, w+4, ... (lanes stride over the partials) to the global max
+// M and the total sum L.  Phase 2: every output element sums its partials'
+// accumulators weighted by exp2(m_i - M) / L, 8 partials' loads in flight.
+template <int DT, typename SlotFn>
+__device__ inline void merge_slots(const DecodeArgs& a, int b, int h, int n, int D, SlotFn slot) {
+  using E = typename Traits<DT>::E;
+  const int G = a.G;
+  const int Hq = a.Hkv * G;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ float s_M[16], s_invL[16];
+  for (int g = wave; g < G; g += 4) {
+    float m = kNegInf;
+    for (int i = lane; i < n; i += 64) m = fmaxf(m, a.ws_ml[(slot(i) * G + g) * 2]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float m_use = m == kNegInf ? 0.f : m;
+    float l = 0.f;
+    for (int i = lane; i < n; i += 64)
+      l += a.ws_ml[(slot(i) * G + g) * 2 + 1] * exp2_fast(a.ws_ml[(slot(i) * G + g) * 2] - m_use);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+    if (lane == 0) {
+      s_M[g] = m_use;
+      s_invL[g] = l > 0.f ? 1.f / l : 0.f;
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int g = idx / D;
+    const float M = s_M[g];
+    float o = 0.f;
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+      float mv[8], av[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t sl = slot(i + u);
+        mv[u] = a.ws_ml[(sl * G + g) * 2];
+        av[u] = a.ws_acc[sl * G * D + idx];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o += av[u] * exp2_fast(mv[u] - M);
+    }
+    for (; i < n; ++i) {
+      const int64_t sl = slot(i);
+      o += a.ws_acc[sl * G * D + idx] * exp2_fast(a.ws_ml[(sl * G + g) * 2] - M);
+    }
+    static_cast<E*>(a.out)[((int64_t)b * Hq + h * G) * D + idx] = Traits<DT>::from_float(o * s_invL[g]);
+  }
+}
+
+// Partitioned walk's merge: grid (kv head, sequence), 256 threads.
 template <int DT>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a, int D) {
-  using Tr = Traits<DT>;
-  using E = typename Tr::E;
-  const int b = blockIdx.y, h = blockIdx.x;
+  const int h = blockIdx.x, b = blockIdx.y;
   const PageWalk w = make_walk(a.ctx[b], a.window, a.n_sink, kBS);
   const int n_parts = num_partitions(w, a);
   if (n_parts <= 1) return;
-  const int G = a.G;
-  const int Hq = a.Hkv * G;
   const int64_t base = ((int64_t)b * a.Hkv + h) * a.n_parts_max;
-  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
-    const int gg = idx / D;
-    float M = kNegInf;
-    for (int p = 0; p < n_parts; ++p) M = fmaxf(M, a.ws_ml[((base + p) * G + gg) * 2]);
-    const float M_use = M == kNegInf ? 0.f : M;
-    float L = 0.f, o = 0.f;
-    for (int p = 0; p < n_parts; ++p) {
-      const float f = exp2_fast(a.ws_ml[((base + p) * G + gg) * 2] - M_use);
-      L += a.ws_ml[((base + p) * G + gg) * 2 + 1] * f;
-      o += a.ws_acc[(base + p) * G * D + idx] * f;
-    }
-    const float r = L > 0.f ? o / L : 0.f;
-    static_cast<E*>(a.out)[((int64_t)b * Hq + h * G) * D + idx] = Tr::from_float(r);
+  merge_slots<DT>(a, b, h, n_parts, D, [&](int i) { return base + i; });
+}
+
+// ---------------------------------------------------------------------------
+// stream walk
+// ---------------------------------------------------------------------------
+
+// Waves that share T tiles: every wave gets at least kMinTilesPerWave.
+__device__ inline int64_t stream_waves(int64_t T, int n_waves) {
+  const int64_t want = (T + kMinTilesPerWave - 1) / kMinTilesPerWave;
+  return want < n_waves ? (want > 0 ? want : 1) : n_waves;
+}
+// Wave k of W owns flat tiles [k*T/W, (k+1)*T/W); wave_of(t) inverts that.
+__device__ inline int64_t wave_start(int64_t k, int64_t T, int64_t W) { return k * T / W; }
+__device__ inline int64_t wave_of(int64_t t, int64_t T, int64_t W) { return ((t + 1) * W - 1) / T; }
+
+// Flat tile order: sequence-major, then kv head, then effective page.  Unit
+// (b, h) = tiles [Hkv*pref[b] + h*n_b, ... + n_b) with n_b = pref[b+1] - pref[b].
+// A fragment (the part of a unit inside one wave's range) is identified by
+// (wave k, unit u = b*Hkv + h); k + u increases strictly along the flat order,
+// so it is the fragment's workspace slot (< kMaxStreamWaves + B*Hkv).
+//
+// The block table and context lengths also come in as __restrict__ parameters:
+// with the workspace and output stores in the loop, that is what lets the
+// compiler read them through the scalar cache (s_load, lgkmcnt) instead of
+// vector loads whose vmcnt wait would drain the page ring.
+template <int DT, int D>
+__global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_stream_kernel(
+    DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ ctx) {
+  using Ops = TileOps<DT, D>;
+  using E = typename Ops::E;
+  using VChunk = typename Ops::VChunk;
+  constexpr int KLD = Ops::KLD, NB = Ops::NB;
+  extern __shared__ int32_t s_pref[];  // [B + 1] page prefix, then [kThreads] scan scratch
+  int32_t* s_scan = s_pref + a.batch + 1;
+
+  const int B = a.batch, Hkv = a.Hkv, G = a.G;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int ln = lane & 15;
+  const int lq = lane >> 4;
+
+  // 1. Page prefix of the batch: thread t sums a contiguous chunk of sequences,
+  //    a Hillis-Steele scan over the 256 chunk sums, then the chunk prefixes.
+  const int chunk = cdiv(B, kThreads);
+  const int c0 = min(tid * chunk, B), c1 = min(c0 + chunk, B);
+  int local = 0;
+  for (int bb = c0; bb < c1; ++bb) {
+    const int n = table_pages(make_walk(ctx[bb], a.window, a.n_sink, kBS), a.max_blocks);
+    s_pref[bb + 1] = n;
+    local += n;
   }
+  s_scan[tid] = local;
+  __syncthreads();
+  for (int off = 1; off < kThreads; off <<= 1) {
+    const int add = tid >= off ? s_scan[tid - off] : 0;
+    __syncthreads();
+    s_scan[tid] += add;
+    __syncthreads();
+  }
+  {
+    int run = s_scan[tid] - local;  // exclusive prefix of this chunk
+    if (tid == 0) s_pref[0] = 0;
+    for (int bb = c0; bb < c1; ++bb) {
+      run += s_pref[bb + 1];
+      s_pref[bb + 1] = run;
+    }
+  }
+  __syncthreads();
+  if (blockIdx.x == 0)
+    for (int bb = tid; bb <= B; bb += kThreads) a.ws_pref[bb] = s_pref[bb];
+
+  const int64_t T = (int64_t)Hkv * uni(s_pref[B]);
+  if (T == 0) return;
+  const int64_t W = stream_waves(T, a.n_waves);
+  const int64_t k = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (k >= W) return;
+  const int64_t t_begin = wave_start(k, T, W), t_end = wave_start(k + 1, T, W);
+  if (t_begin >= t_end) return;
+  const int count = (int)(t_end - t_begin);
+
+  // 2. Unit and page of the first tile: the last sequence b with
+  //    pref[b] <= t_begin / Hkv (it is non-empty), then kv head and page.
+  int lo = 0, hi = B;
+  {
+    const int key = (int)(t_begin / Hkv);
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (uni(s_pref[mid]) <= key) lo = mid;
+      else hi = mid;
+    }
+  }
+  // A cursor walks (sequence, kv head, effective page) in flat order.
+  struct Cursor {
+    int b, h, v, n;
+    PageWalk w;
+  };
+  Cursor c0r;
+  c0r.b = lo;
+  c0r.n = uni(s_pref[lo + 1]) - uni(s_pref[lo]);
+  {
+    const int64_t r = t_begin - (int64_t)Hkv * uni(s_pref[lo]);
+    c0r.h = (int)(r / c0r.n);
+    c0r.v = (int)(r - (int64_t)c0r.h * c0r.n);
+  }
+  c0r.w = make_walk(ctx[c0r.b], a.window, a.n_sink, kBS);
+  auto advance = [&](Cursor& c) {
+    if (++c.v < c.n) return;
+    c.v = 0;
+    if (++c.h < Hkv) return;
+    c.h = 0;
+    do {
+      ++c.b;
+    } while (c.b < B && uni(s_pref[c.b + 1]) == uni(s_pref[c.b]));
+    if (c.b < B) {
+      c.n = uni(s_pref[c.b + 1]) - uni(s_pref[c.b]);
+      c.w = make_walk(ctx[c.b], a.window, a.n_sink, kBS);
+    }
+  };
+
+  // 3. The ring: the load cursor runs kPageBufs tiles ahead of the compute
+  //    cursor.  Past the wave's last tile it stays there and re-loads it (an L2
+  //    hit) into padding slots that score() masks.  Every slot also loads the
+  //    query rows of its tile's unit (an L2 hit after the first): a q load only
+  //    at unit changes would sit on a branch whose join makes the compiler
+  //    drain the ring before every tile.
+  Cursor lc = c0r, cc = c0r;
+  int issued = 0;
+  Chunk16 qb[kPageBufs][KLD];
+  Chunk16 kb[kPageBufs][KLD];
+  VChunk vb[kPageBufs][NB];
+  int64_t pb[kPageBufs];
+  auto issue = [&](int s) {
+    Ops::load_q(a, lc.b, lc.h, ln, lq, qb[s]);
+    pb[s] = Ops::phys_page(a, bt, lc.b, logical_page(lc.w, lc.v));
+    Ops::load_tile(a, pb[s], lc.h, ln, lq, kb[s], vb[s]);
+    if (++issued < count) advance(lc);
+  };
+#pragma unroll
+  for (int s = 0; s < kPageBufs; ++s) issue(s);
+
+  typename Ops::State st;
+  st.reset();
+  bool fresh = true;   // next live tile starts a fragment
+  int frag_first = 0;  // first page of the current fragment
+  const int Hq = Hkv * G;
+  for (int i = 0; i < count; i += kPageBufs) {
+#pragma unroll
+    for (int s = 0; s < kPageBufs; ++s) {
+      const bool live = i + s < count;
+      if (live && fresh) {
+        st.reset();
+        frag_first = cc.v;
+        fresh = false;
+      }
+      Ops::score(st, kb[s], vb[s], qb[s], cc.w, logical_page(cc.w, cc.v), live && pb[s] >= 0, a, lq);
+      if (live) {
+        const bool unit_end = cc.v == cc.n - 1;
+        if (unit_end || i + s == count - 1) {
+          // Flush the fragment: the whole unit goes straight to `out`,
+          // a piece of it to workspace slot k + u.
+          const float l_tot = st.total();
+          if (ln < G) {
+            if (frag_first == 0 && unit_end) {
+              const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+              E* o = static_cast<E*>(a.out) + ((int64_t)cc.b * Hq + cc.h * G + ln) * D + 4 * lq;
+#pragma unroll
+              for (int m = 0; m < NB; ++m)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[16 * m + r] = Ops::Tr::from_float(st.acc[m][r] * inv);
+            } else {
+              const int64_t slot = k + (int64_t)cc.b * Hkv + cc.h;
+              float* o = a.ws_acc + (slot * G + ln) * D + 4 * lq;
+#pragma unroll
+              for (int m = 0; m < NB; ++m) *reinterpret_cast<f32x4*>(o + 16 * m) = st.acc[m];
+              if (lq == 0) {
+                a.ws_ml[(slot * G + ln) * 2] = st.m_run;
+                a.ws_ml[(slot * G + ln) * 2 + 1] = l_tot;
+              }
+            }
+          }
+          fresh = true;
+        }
+        advance(cc);
+      }
+      issue(s);
+    }
+  }
+}
+
+// Stream walk's merge: grid (kv head, sequence), 256 threads.  Writes zeros for
+// an empty unit, skips a unit one wave finished (written directly), and folds
+// the fragments of a split unit (slots k + u, k = first..last wave).
+template <int DT>
+__global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, int D) {
+  using E = typename Traits<DT>::E;
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int Hkv = a.Hkv, G = a.G;
+  const int64_t pb = a.ws_pref[b];
+  const int n = a.ws_pref[b + 1] - (int)pb;
+  if (n == 0) {
+    E* o = static_cast<E*>(a.out) + ((int64_t)b * Hkv * G + h * G) * D;
+    for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) o[idx] = Traits<DT>::from_float(0.f);
+    return;
+  }
+  const int64_t T = (int64_t)Hkv * a.ws_pref[a.batch];
+  const int64_t W = stream_waves(T, a.n_waves);
+  const int64_t first_tile = (int64_t)Hkv * pb + (int64_t)h * n;
+  const int64_t k0 = wave_of(first_tile, T, W), k1 = wave_of(first_tile + n - 1, T, W);
+  if (k0 == k1) return;
+  const int64_t base = k0 + (int64_t)b * Hkv + h;
+  merge_slots<DT>(a, b, h, (int)(k1 - k0 + 1), D, [&](int i) { return base + i; });
 }
 
 enum Stage { kFull = 0, kPartial = 1, kMerge = 2 };
 
 struct Plan {
+  bool stream;
   int G, n_parts_max, part_pages;
+  size_t acc_elems, ml_elems, pref_elems;
   size_t ws_bytes;
 };
 
-int make_plan(const char* name, int batch, int num_q_heads, int num_kv_heads, int head_dim,
-              int block_size, int max_blocks, int window, int n_sink, int partition_pages,
-              Plan* plan) {
+int make_plan(const char* name, Stage stage, int batch, int num_q_heads, int num_kv_heads,
+              int head_dim, int block_size, int max_blocks, int window, int n_sink,
+              int partition_pages, Plan* plan) {
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_blocks < 0)
     return fail(IVAKV_E_ARG, "%s: bad sizes B=%d Hq=%d Hkv=%d max_blocks=%d", name, batch,
                 num_q_heads, num_kv_heads, max_blocks);
@@ -380,25 +720,72 @@ int make_plan(const char* name, int batch, int num_q_heads, int num_kv_heads, in
   if (block_size != kBS)
     return fail(IVAKV_E_SHAPE, "%s: block_size %d != %d", name, block_size, kBS);
   if (n_sink < 0) return fail(IVAKV_E_ARG, "%s: negative n_sink", name);
+  plan->G = G;
+  plan->stream = partition_pages <= 0 && batch <= kMaxStreamBatch;
+  const size_t units = (size_t)batch * num_kv_heads;
+  if (plan->stream) {
+    plan->part_pages = 0;
+    plan->n_parts_max = 0;
+    const size_t slots = (size_t)kMaxStreamWaves + units;
+    plan->acc_elems = slots * G * (size_t)head_dim;
+    plan->ml_elems = slots * G * 2;
+    plan->pref_elems = (((size_t)batch + 1) + 3) & ~(size_t)3;
+    plan->ws_bytes = (plan->acc_elems + plan->ml_elems + plan->pref_elems) * 4;
+    return IVAKV_OK;
+  }
   const int pp = partition_pages > 0 ? partition_pages : kDefaultPartitionPages;
   const int max_eff = max_effective_pages(max_blocks, window, n_sink, kBS);
   const int n_parts_max = max_eff > 0 ? cdiv(max_eff, pp) : 1;
-  plan->G = G;
+  if (n_parts_max > 65535)
+    return fail(IVAKV_E_SHAPE, "%s: %d partitions per sequence exceed 65535; raise partition_pages",
+                name, n_parts_max);
   plan->part_pages = pp;
   plan->n_parts_max = n_parts_max;
-  plan->ws_bytes = n_parts_max > 1 ? (size_t)batch * num_kv_heads * n_parts_max * G *
-                                         ((size_t)head_dim + 2) * sizeof(float)
-                                   : 0;
+  plan->pref_elems = 0;
+  if (n_parts_max > 1) {
+    plan->acc_elems = units * n_parts_max * G * (size_t)head_dim;
+    plan->ml_elems = units * n_parts_max * G * 2;
+    plan->ws_bytes = (plan->acc_elems + plan->ml_elems) * 4;
+  } else {
+    plan->acc_elems = plan->ml_elems = 0;
+    plan->ws_bytes = 0;
+  }
   return IVAKV_OK;
 }
 
 template <int DT>
 void launch_partial(int D, dim3 grid, size_t smem, hipStream_t stream, const DecodeArgs& a) {
   switch (D) {
-    case 64: decode_partial_kernel<DT, 64><<<grid, kThreads, smem, stream>>>(a); break;
-    case 128: decode_partial_kernel<DT, 128><<<grid, kThreads, smem, stream>>>(a); break;
-    default: decode_partial_kernel<DT, 256><<<grid, kThreads, smem, stream>>>(a); break;
+    case 64: decode_partial_kernel<DT, 64><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+    case 128: decode_partial_kernel<DT, 128><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+    default: decode_partial_kernel<DT, 256><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
   }
+}
+
+template <int DT>
+void launch_stream(Stage stage, int D, dim3 grid, size_t smem, hipStream_t stream,
+                   const DecodeArgs& a) {
+  if (stage != kMerge) {
+    switch (D) {
+      case 64: decode_stream_kernel<DT, 64><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+      case 128: decode_stream_kernel<DT, 128><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+      default: decode_stream_kernel<DT, 256><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+    }
+  }
+  if (stage != kPartial)
+    decode_stream_merge_kernel<DT><<<dim3((unsigned)a.Hkv, (unsigned)a.batch), 256, 0, stream>>>(a, D);
+}
+
+// Workgroups of the stream walk on the current device: what its CUs hold at
+// once, within the workspace's wave budget.
+int stream_workgroups() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = kMaxStreamWaves / (kWaves * kStreamWGsPerCU);
+  const int wgs = cus * kStreamWGsPerCU;
+  return wgs < kMaxStreamWaves / kWaves ? wgs : kMaxStreamWaves / kWaves;
 }
 
 int decode_entry(Stage stage, const char* name, const void* q, const void* k_pool,
@@ -409,8 +796,8 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
                  hipStream_t stream) {
   if (dtype_size(dtype) == 0) return fail(IVAKV_E_DTYPE, "%s: unknown dtype code %d", name, dtype);
   Plan plan;
-  int st = make_plan(name, batch, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks,
-                     window, n_sink, partition_pages, &plan);
+  int st = make_plan(name, stage, batch, num_q_heads, num_kv_heads, head_dim, block_size,
+                     max_blocks, window, n_sink, partition_pages, &plan);
   if (st != IVAKV_OK) return st;
   if (batch == 0) return IVAKV_OK;
   // An invalid page id is read as page 0 (then masked), so the pool needs a page.
@@ -434,9 +821,11 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
   a.ctx = context_lens;
   a.out = out;
   float* ws = static_cast<float*>(workspace);
-  const size_t acc_elems = (size_t)batch * num_kv_heads * plan.n_parts_max * plan.G * head_dim;
   a.ws_acc = plan.ws_bytes ? ws : nullptr;
-  a.ws_ml = plan.ws_bytes ? ws + acc_elems : nullptr;
+  a.ws_ml = plan.ws_bytes ? ws + plan.acc_elems : nullptr;
+  a.ws_pref = plan.pref_elems ? reinterpret_cast<int32_t*>(ws + plan.acc_elems + plan.ml_elems)
+                              : nullptr;
+  a.batch = batch;
   a.Hkv = num_kv_heads;
   a.G = plan.G;
   a.max_blocks = max_blocks;
@@ -446,9 +835,24 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
   a.n_sink = n_sink;
   a.part_pages = plan.part_pages;
   a.n_parts_max = plan.n_parts_max;
+  a.n_waves = 0;
 
+  if (plan.stream) {
+    const int wgs = stream_workgroups();
+    a.n_waves = wgs * kWaves;
+    const size_t smem = sizeof(int32_t) * ((size_t)batch + 1 + kThreads);
+    switch (dtype) {
+      case IVAKV_F16: launch_stream<IVAKV_F16>(stage, head_dim, dim3((unsigned)wgs), smem, stream, a); break;
+      case IVAKV_BF16: launch_stream<IVAKV_BF16>(stage, head_dim, dim3((unsigned)wgs), smem, stream, a); break;
+      default: launch_stream<IVAKV_F32>(stage, head_dim, dim3((unsigned)wgs), smem, stream, a); break;
+    }
+    return launch_status(name);
+  }
   if (stage == kFull || stage == kPartial) {
-    dim3 grid((unsigned)plan.n_parts_max, (unsigned)num_kv_heads, (unsigned)batch);
+    // Partition slowest: consecutive workgroups (which the dispatcher deals
+    // round-robin to the 8 XCDs) are different kv heads / sequences of equal
+    // partition index, so every XCD gets an even share of the pages.
+    dim3 grid((unsigned)num_kv_heads, (unsigned)batch, (unsigned)plan.n_parts_max);
     const size_t smem = sizeof(float) * (2 * kWaves * 16 + 32 + (size_t)kWaves * plan.G * (head_dim + 4));
     switch (dtype) {
       case IVAKV_F16: launch_partial<IVAKV_F16>(head_dim, grid, smem, stream, a); break;
@@ -481,7 +885,7 @@ extern "C" int ivakv_decode_workspace_size(int batch, int num_q_heads, int num_k
                                            size_t* bytes) {
   if (!bytes) return fail(IVAKV_E_ARG, "ivakv_decode_workspace_size: null output pointer");
   Plan plan;
-  const int st = make_plan("ivakv_decode_workspace_size", batch, num_q_heads, num_kv_heads,
+  const int st = make_plan("ivakv_decode_workspace_size", kFull, batch, num_q_heads, num_kv_heads,
                            head_dim, block_size, max_blocks, window, n_sink, partition_pages,
                            &plan);
   if (st != IVAKV_OK) return st;

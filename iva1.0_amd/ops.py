@@ -154,6 +154,8 @@ _WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
 def decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
                            block_size: int, max_blocks: int, window: int = 0, n_sink: int = 0,
                            partition_pages: int = 0) -> int:
+    """Workspace bytes :func:`paged_decode_attention` needs (0 when no sequence spans more
+    than one partition).  The workspace needs no initialisation."""
     import ctypes
     out = ctypes.c_size_t(0)
     _abi.call("ivakv_decode_workspace_size", batch, num_q_heads, num_kv_heads, head_dim,

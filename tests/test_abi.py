@@ -100,13 +100,18 @@ def test_decode_argument_checks(iva):
 
 def test_workspace_size(iva):
     ws = iva.decode_workspace_bytes
-    # one partition per sequence: no workspace
+    # explicit partitions, one per sequence: no workspace
     assert ws(32, 32, 8, 128, 16, 16, partition_pages=16) == 0
-    # C2 geometry: 256 blocks / 16 = 16 partitions of G=4 heads x (128 + 2) fp32
+    # explicit partitions: 256 blocks / 16 = 16 partitions of G=4 heads x (128 + 2) fp32
     assert ws(32, 32, 8, 128, 16, 256, partition_pages=16) == 32 * 8 * 16 * 4 * 130 * 4
     # a window bounds the partitions: 4 sinks + 4096 window -> 1 + 256 + 1 pages
     assert ws(4, 32, 8, 128, 16, 8192, window=4096, n_sink=4, partition_pages=16) == \
         4 * 8 * 17 * 4 * 130 * 4
+    # default (stream walk): one slot per wave of the wave budget plus one per
+    # (sequence, kv head), then the batch's page prefix (B + 1 ints, padded to 4)
+    stream = (4096 + 32 * 8) * 4 * 130 * 4 + 36 * 4
+    assert ws(32, 32, 8, 128, 16, 256) == stream
+    assert ws(32, 32, 8, 128, 16, 16) == stream
     with pytest.raises(iva._abi.IvakvError):
         ws(1, 3, 2, 128, 16, 4)
 

@@ -110,9 +110,18 @@ def test_partial_then_merge_equals_full(iva, dev):
     lay = d["layout"]
     args = (d["q"].to(dev), d["k_pool"].to(dev), d["v_pool"].to(dev), lay.block_tables.to(dev),
             lay.context_lens.to(dev))
-    full = iva.paged_decode_attention(*args)
-    ws = torch.empty(iva.decode_workspace_bytes(3, 16, 4, 128, 16, lay.block_tables.shape[1]),
+    # the partitioned walk in one call (explicit partition size) vs its two halves
+    full = iva.paged_decode_attention(*args, partition_pages=32)
+    ws = torch.empty(max(iva.decode_workspace_bytes(3, 16, 4, 128, 16, lay.block_tables.shape[1]),
+                         iva.decode_workspace_bytes(3, 16, 4, 128, 16, lay.block_tables.shape[1],
+                                                    partition_pages=32)),
                      dtype=torch.uint8, device=dev)
+    out = torch.empty_like(full)
+    iva.paged_decode_attention_partial(*args, out=out, workspace=ws, partition_pages=32)
+    iva.paged_decode_attention_merge(*args, out=out, workspace=ws, partition_pages=32)
+    assert torch.equal(out.view(torch.int16), full.view(torch.int16))
+    # the default (stream) walk in one call vs its two halves
+    full = iva.paged_decode_attention(*args)
     out = torch.empty_like(full)
     iva.paged_decode_attention_partial(*args, out=out, workspace=ws)
     iva.paged_decode_attention_merge(*args, out=out, workspace=ws)
@@ -281,3 +290,44 @@ def test_context_beyond_block_table(iva, dev):
     out_w = run_gpu(iva, dev, d, layout=lay2, window=200, n_sink=4)
     assert_close(out_w, oracle_out(d, layout=lay2, window=200, n_sink=4), torch.float16,
                  rel_ulp=False, what="ctx > table, window")
+
+
+
+def test_workspace_reuse_across_calls(iva, dev):
+    """One workspace serves alternating batches of different shapes; results stay exact."""
+    a = iva.workloads.decode_batch([3000, 700, 16, 2500], 32, 8, 128, torch.float16, seed=21,
+                                   scale=128 ** -0.5)
+    b = iva.workloads.decode_batch([900, 4000], 32, 8, 128, torch.float16, seed=22,
+                                   scale=128 ** -0.5)
+    ws = torch.full((1 << 22,), 0x7F, dtype=torch.uint8, device=dev)  # needs no initialisation
+    for _ in range(3):
+        for d in (a, b):
+            out = run_gpu(iva, dev, d, workspace=ws, partition_pages=8)
+            assert_close(out, oracle_out(d), torch.float16, rel_ulp=False, what="workspace reuse")
+
+
+@pytest.mark.parametrize("lengths", [
+    [0, 0, 5, 0, 4097, 0, 1, 16, 17, 0],        # empty sequences between long and tiny ones
+    [1],                                        # fewer tiles than a wave minimum
+    [16] * 300,                                 # many one-page units: waves span many units
+    [3000, 2, 2, 2, 2, 2, 2, 2, 2, 2999],       # units split across many waves next to tiny ones
+])
+def test_stream_walk_unit_boundaries(iva, dev, lengths):
+    """The default (stream) walk against the oracle where wave ranges cross many unit
+    boundaries, units are empty, or the batch is smaller than one wave's share."""
+    d = iva.workloads.decode_batch(lengths, 16, 4, 128, torch.float16, seed=len(lengths),
+                                   scale=128 ** -0.5, extra_pages=2)
+    out = run_gpu(iva, dev, d)
+    assert_close(out, oracle_out(d), torch.float16, rel_ulp=False, what=f"stream {lengths[:4]}")
+
+
+def test_stream_matches_partitioned(iva, dev):
+    """Stream and partitioned walks agree on a C5-like ragged batch (fp16 tolerance)."""
+    lengths = iva.workloads.c5_lengths(seed=3, n_seqs=64)
+    d = iva.workloads.decode_batch(lengths, 32, 8, 128, torch.float16, seed=31, device=dev,
+                                   scale=128 ** -0.5)
+    lay = d["layout"]
+    args = (d["q"], d["k_pool"], d["v_pool"], lay.block_tables.to(dev), lay.context_lens.to(dev))
+    a = iva.paged_decode_attention(*args)
+    b = iva.paged_decode_attention(*args, partition_pages=24)
+    assert (a.float() - b.float()).abs().max().item() <= 2e-3
