@@ -2,28 +2,37 @@
 
 A step is one decode step of the hot path over one batch: append one new K/V row
 per sequence into its page (ivakv_append), then paged GQA decode attention over
-the whole context (ivakv_decode_attn: the paged walk + the split-K merge).
+the whole context (ivakv_decode_attn: the paged walk + the split merge).
 Workload C2: 32 sequences, 32 query / 8 KV heads, head_dim 128, fp16, block 16,
 context lengths ~ U[512, 4096] (seed 0), values N(0, 1)/sqrt(128).
 
 Inputs are resident in HBM before timing.  To keep the 256 MiB MALL from
 serving repeated reads, steps rotate over --pools independent page pools
 (>= 1 GiB in total by default).  Each pool's step is captured once as a HIP
-graph (launch overhead of the three kernels is then the graph's, as in a
-production decode loop) and the graphs are replayed --steps times between two
+graph (launch overhead of the kernels is then the graph's, as in a production
+decode loop) and the graphs are replayed --steps times between two
 synchronisations.
 
 Output: one JSON line.  `value` is algorithmic GB/s of the whole step (append
-bytes + attention bytes, formulas in DESIGN.md) / step time.  `roofline` is for
-the dominant kernel (the paged walk, decode_partial_kernel): its algorithmic
-bytes / its average duration measured here with HIP events over a graph of
-back-to-back launches on the launch stream.  `cpu_baseline` times the CPU
-restatement of the reference's torch path (contiguous cache + torch.cat append +
-AttentionTorch math, fp32) on this host's cores.
+bytes + attention bytes) / step time.  `roofline` is for the dominant kernel
+(the paged walk, decode_stream_kernel): its algorithmic bytes / its average
+duration measured here with HIP events over a graph of back-to-back launches on
+the launch stream.  `cpu_baseline` times the CPU restatement of the reference's
+torch path (contiguous cache + torch.cat append + AttentionTorch math, fp32) on
+this host's cores.
+
+Profiling helpers (no timing line):
+  --copy-calibration   also launches a plain 256 MiB device copy 10 times after
+                       the timed region: the known-size kernel that scales the
+                       rocprofv3 FETCH_SIZE / WRITE_SIZE counters.
+  --summarize-pmc F W  reads the counter CSVs of a FETCH_SIZE run (directory F)
+                       and a WRITE_SIZE run (directory W) and writes
+                       profiles/decode_attn_c2_traffic.{json,md}.
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import math
 import os
@@ -38,6 +47,8 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 METRIC = "paged decode-attn + KV append GB/s and % HBM peak; decode tokens/s at 1 GPU"
 PROFILE_TRAFFIC = ROOT / "profiles" / "decode_attn_c2_traffic.json"
+WALK_KERNEL = "decode_stream_kernel"
+COPY_BYTES = 256 << 20
 
 
 def parse_args():
@@ -46,11 +57,16 @@ def parse_args():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--pools", type=int, default=4, help="independent KV pools rotated per step")
-    p.add_argument("--partition-pages", type=int, default=0, help="0 = library default")
+    p.add_argument("--partition-pages", type=int, default=0,
+                   help="0 = default (stream) walk; > 0 = partitioned walk of that size")
     p.add_argument("--kernel-launches", type=int, default=200,
                    help="launches of the paged walk timed for the roofline figure")
     p.add_argument("--cpu-reps", type=int, default=10, help="timed CPU-baseline reps (0 = skip)")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of graphs")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="launch a plain 256 MiB copy 10x after timing (counter calibration)")
+    p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                   help="write the HBM traffic summary from two rocprofv3 --pmc runs")
     return p.parse_args()
 
 
@@ -102,8 +118,73 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def _counter_rows(directory: str):
+    """(kernel name, counter name, value) of every dispatch in a rocprofv3 --pmc CSV."""
+    files = sorted(Path(directory).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {directory}")
+    for f in files:
+        for row in csv.DictReader(f.open()):
+            yield row.get("Kernel_Name", ""), row.get("Counter_Name", ""), float(row["Counter_Value"])
+
+
+def _mean_kib(directory: str, counter: str, match) -> float:
+    vals = [v for k, c, v in _counter_rows(directory) if c == counter and match(k)]
+    if not vals:
+        raise SystemExit(f"no {counter} rows for the requested kernel in {directory}")
+    return sum(vals) / len(vals)
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str) -> None:
+    """Scales the walk's FETCH_SIZE / WRITE_SIZE (KiB per dispatch) by what the same
+    counters read for the plain copy of COPY_BYTES, and writes the traffic summary."""
+    is_walk = lambda k: WALK_KERNEL in k and "<1, 128>" in k
+    is_copy = lambda k: "copy" in k.lower() and "ivakv" not in k
+
+    def copy_kib(directory, counter):
+        """The calibration leg's 10 identical copies: the most common (to 2 significant
+        digits) large value among copy-kernel dispatches."""
+        rows = [v for k, c, v in _counter_rows(directory)
+                if c == counter and is_copy(k) and v > 0.25 * COPY_BYTES / 1024]
+        if not rows:
+            raise SystemExit(f"no calibration copy rows for {counter} in {directory}")
+        key = lambda v: float(f"{v:.2g}")
+        groups = {}
+        for v in rows:
+            groups.setdefault(key(v), []).append(v)
+        best = max(groups.values(), key=len)
+        return sum(best) / len(best)
+    fetch_walk = _mean_kib(fetch_dir, "FETCH_SIZE", is_walk)
+    write_walk = _mean_kib(write_dir, "WRITE_SIZE", is_walk)
+    fetch_copy = copy_kib(fetch_dir, "FETCH_SIZE")
+    write_copy = copy_kib(write_dir, "WRITE_SIZE")
+    f_scale = COPY_BYTES / (fetch_copy * 1024)
+    w_scale = COPY_BYTES / (write_copy * 1024)
+    read_b = fetch_walk * 1024 * f_scale
+    write_b = write_walk * 1024 * w_scale
+    summary = {
+        "kernel": "decode_stream_kernel<f16,128> (C2)",
+        "fetch_kib_per_dispatch": round(fetch_walk, 1),
+        "write_kib_per_dispatch": round(write_walk, 1),
+        "copy_calibration_bytes": COPY_BYTES,
+        "copy_fetch_kib": round(fetch_copy, 1),
+        "copy_write_kib": round(write_copy, 1),
+        "fetch_scale": round(f_scale, 4),
+        "write_scale": round(w_scale, 4),
+        "hbm_read_bytes_per_launch": int(read_b),
+        "hbm_write_bytes_per_launch": int(write_b),
+        "hbm_bytes_per_launch": int(read_b + write_b),
+    }
+    PROFILE_TRAFFIC.parent.mkdir(exist_ok=True)
+    PROFILE_TRAFFIC.write_text(json.dumps(summary, indent=1) + "\n")
+    print(json.dumps(summary))
+
+
 def main():
     args = parse_args()
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                           "(the multi-GPU sharding of the path is described in DESIGN.md)"}))
@@ -139,13 +220,16 @@ def main():
     max_blocks = sets[0]["bt"].shape[1]
     ws_bytes = iva.decode_workspace_bytes(batch, hq, hkv, d, 16, max_blocks,
                                           partition_pages=args.partition_pages)
-    workspace = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     pp = args.partition_pages or None
+
+    def attention(s):
+        iva.paged_decode_attention(s["q"], s["k_pool"], s["v_pool"], s["bt"], s["ctx"],
+                                   partition_pages=pp, out=s["out"], workspace=workspace)
 
     def step(s):
         iva.kv_append(s["k_new"], s["v_new"], s["k_pool"], s["v_pool"], s["slots"])
-        iva.paged_decode_attention(s["q"], s["k_pool"], s["v_pool"], s["bt"], s["ctx"],
-                                   partition_pages=pp, out=s["out"], workspace=workspace)
+        attention(s)
 
     def walk(s):
         iva.paged_decode_attention_partial(s["q"], s["k_pool"], s["v_pool"], s["bt"], s["ctx"],
@@ -169,6 +253,7 @@ def main():
         step_graph = None if args.eager else make_graph(step, len(sets))
         per_graph = len(sets) * max(1, 20 // len(sets))
         walk_graph = None if args.eager else make_graph(walk, per_graph)
+        attn_graph = None if args.eager else make_graph(attention, per_graph)
 
         def run_steps(n):
             if step_graph is None:
@@ -189,26 +274,37 @@ def main():
         torch.cuda.synchronize(dev)
         step_ms = e0.elapsed_time(e1) / args.steps
 
-        # dominant kernel alone: back-to-back launches of the paged walk
-        launches = 0
-        k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        if walk_graph is not None:
-            walk_graph.replay()
+        def time_launches(graph, fn):
+            """Average duration of fn's launches, back to back on the launch stream."""
+            k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            if graph is not None:
+                graph.replay()
+                torch.cuda.synchronize(dev)
+                reps = max(1, args.kernel_launches // per_graph)
+                k0.record(stream)
+                for _ in range(reps):
+                    graph.replay()
+                k1.record(stream)
+                launches = reps * per_graph
+            else:
+                k0.record(stream)
+                for i in range(args.kernel_launches):
+                    fn(sets[i % len(sets)])
+                k1.record(stream)
+                launches = args.kernel_launches
             torch.cuda.synchronize(dev)
-            reps = max(1, args.kernel_launches // per_graph)
-            k0.record(stream)
-            for _ in range(reps):
-                walk_graph.replay()
-            k1.record(stream)
-            launches = reps * per_graph
-        else:
-            k0.record(stream)
-            for i in range(args.kernel_launches):
-                walk(sets[i % len(sets)])
-            k1.record(stream)
-            launches = args.kernel_launches
-        torch.cuda.synchronize(dev)
-        walk_us = k0.elapsed_time(k1) * 1e3 / launches
+            return k0.elapsed_time(k1) * 1e3 / launches
+
+        # dominant kernel alone: back-to-back launches of the paged walk
+        walk_us = time_launches(walk_graph, walk)
+        attn_us = time_launches(attn_graph, attention)
+
+        if args.copy_calibration:
+            src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(7)
+            dst = torch.empty_like(src)
+            for _ in range(10):
+                dst.copy_(src)
+            torch.cuda.synchronize(dev)
 
     append_b, attn_b = algorithmic_bytes(lengths, hq, hkv, d, esize)
     step_s = step_ms * 1e-3
@@ -233,6 +329,8 @@ def main():
                           f"{t_cpu * 1e3:.1f} ms/step, {cpu_model()}"),
                "ms_per_step": round(t_cpu * 1e3, 2)}
 
+    walk_name = (f"{WALK_KERNEL}<f16,128>" if not args.partition_pages
+                 else "decode_partial_kernel<f16,128>")
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -251,14 +349,16 @@ def main():
                    "block_size": 16, "context": "U[512,4096] seed 0",
                    "mean_context": round(sum(lengths) / batch, 1), "pools_rotated": args.pools,
                    "pool_bytes_total": pool_bytes, "launch": "eager" if args.eager else "hip graph",
-                   "partition_pages": args.partition_pages or 16},
+                   "walk": "partitioned, %d pages" % args.partition_pages
+                   if args.partition_pages else "stream"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": "decode_partial_kernel<f16,128>",
+                     "traffic": traffic, "kernel": walk_name,
                      "kernel_us": round(walk_us, 3), "algorithmic_bytes": attn_b},
         "cpu_baseline": cpu,
         "tokens_per_s": round(batch / step_s, 1),
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "attention_us": round(attn_us, 3),
         "step_bytes": {"append": append_b, "attention": attn_b},
     }
     print(json.dumps(line), flush=True)

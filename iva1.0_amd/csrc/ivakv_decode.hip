@@ -420,56 +420,47 @@ __global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_partial_kern
   }
 }
 
-// Weighted sum of n partial (max, sum, acc) slots into out rows of unit (b, h):
-// slot(i) gives the workspace slot of the i-th partial.  Phase 1: wave w
-// reduces heads w, w+4, ... (lanes stride over the partials) to the global max
-// M and the total sum L.  Phase 2: every output element sums its partials'
-// accumulators weighted by exp2(m_i - M) / L, 8 partials' loads in flight.
+// Log-sum-exp merge of n partial (max, sum, acc) slots into the out rows of
+// unit (b, h); slot(i) gives the workspace slot of the i-th partial.  Every
+// output element runs one online pass over the partials, loading 8 partials'
+// (max, sum, acc) together, so the merge costs one memory round trip per 8
+// partials instead of separate max / sum / accumulate passes.
 template <int DT, typename SlotFn>
 __device__ inline void merge_slots(const DecodeArgs& a, int b, int h, int n, int D, SlotFn slot) {
   using E = typename Traits<DT>::E;
   const int G = a.G;
   const int Hq = a.Hkv * G;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __shared__ float s_M[16], s_invL[16];
-  for (int g = wave; g < G; g += 4) {
-    float m = kNegInf;
-    for (int i = lane; i < n; i += 64) m = fmaxf(m, a.ws_ml[(slot(i) * G + g) * 2]);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    const float m_use = m == kNegInf ? 0.f : m;
-    float l = 0.f;
-    for (int i = lane; i < n; i += 64)
-      l += a.ws_ml[(slot(i) * G + g) * 2 + 1] * exp2_fast(a.ws_ml[(slot(i) * G + g) * 2] - m_use);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o);
-    if (lane == 0) {
-      s_M[g] = m_use;
-      s_invL[g] = l > 0.f ? 1.f / l : 0.f;
-    }
-  }
-  __syncthreads();
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int g = idx / D;
-    const float M = s_M[g];
-    float o = 0.f;
-    int i = 0;
-    for (; i + 8 <= n; i += 8) {
-      float mv[8], av[8];
+    float M = kNegInf, L = 0.f, O = 0.f;
+    for (int i0 = 0; i0 < n; i0 += 8) {
+      float mv[8], lv[8], av[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int64_t sl = slot(i + u);
+        const int64_t sl = slot(min(i0 + u, n - 1));
         mv[u] = a.ws_ml[(sl * G + g) * 2];
+        lv[u] = a.ws_ml[(sl * G + g) * 2 + 1];
         av[u] = a.ws_acc[sl * G * D + idx];
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) o += av[u] * exp2_fast(mv[u] - M);
+      for (int u = 0; u < 8; ++u) mv[u] = i0 + u < n ? mv[u] : kNegInf;
+      float mc = M;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) mc = fmaxf(mc, mv[u]);
+      const float m_use = mc == kNegInf ? 0.f : mc;
+      const float f = exp2_fast(M - m_use);
+      L *= f;
+      O *= f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float w = exp2_fast(mv[u] - m_use);
+        L += lv[u] * w;
+        O += av[u] * w;
+      }
+      M = mc;
     }
-    for (; i < n; ++i) {
-      const int64_t sl = slot(i);
-      o += a.ws_acc[sl * G * D + idx] * exp2_fast(a.ws_ml[(sl * G + g) * 2] - M);
-    }
-    static_cast<E*>(a.out)[((int64_t)b * Hq + h * G) * D + idx] = Traits<DT>::from_float(o * s_invL[g]);
+    static_cast<E*>(a.out)[((int64_t)b * Hq + h * G) * D + idx] =
+        Traits<DT>::from_float(L > 0.f ? O / L : 0.f);
   }
 }
 
