@@ -7,7 +7,7 @@ include/ivakv.h (libivakv.so, bound with ctypes in ``_abi``).
 The directory name is not a Python identifier; load it with
 ``__graft_entry__.load_package()``, which registers it as ``iva_amd``.
 """
-from . import _abi, workloads
+from . import _abi, model, paged_cache, workloads
 from .ops import (
     chunk_elems,
     decode_workspace_bytes,
@@ -21,8 +21,17 @@ from .ops import (
     pool_geometry,
     pool_shapes,
 )
+from .model import PagedAttention, Transformer, TransformerConfig, get_attention
+from .paged_cache import OutOfPagesError, PagedKVCache, PagedKVPool
 
 __all__ = [
+    "OutOfPagesError",
+    "PagedAttention",
+    "PagedKVCache",
+    "PagedKVPool",
+    "Transformer",
+    "TransformerConfig",
+    "get_attention",
     "chunk_elems",
     "decode_workspace_bytes",
     "dtype_code",

@@ -1,0 +1,156 @@
+"""PagedKVPool bookkeeping on the CPU (no device storage): LIFO free list, block
+tables and slot ids, reference-counted fork, window release, exhaustion errors,
+config sizing and state round trip.  Slot ids are checked against the address
+rule slot = page * block_size + position % block_size."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+
+def pool(iva, pages=16, **kw):
+    from importlib import import_module
+    pc = import_module("iva_amd.paged_cache")
+    kw.setdefault("max_seqs", 8)
+    return pc.PagedKVPool(pages, 2, 64, 16, allocate_storage=False, device="cpu", **kw), pc
+
+
+def test_allocate_slots_follow_pages(iva):
+    p, _ = pool(iva)
+    p.add_sequence("a")
+    s = p.allocate("a", 20)                     # 2 pages
+    pages = p.pages("a")
+    assert len(pages) == 2 and p.length("a") == 20
+    pos = np.arange(20)
+    assert np.array_equal(s, np.array(pages)[pos // 16] * 16 + pos % 16)
+    s2 = p.allocate("a", 13)                    # 33 tokens -> 3 pages
+    assert len(p.pages("a")) == 3 and s2[0] == pages[1] * 16 + 4
+    bt, ctx = p.tables(["a"])
+    assert list(bt[0, :3]) == p.pages("a") and ctx[0] == 33
+
+
+def test_lifo_free_list_reuses_last_freed(iva):
+    p, _ = pool(iva)
+    for name in "abc":
+        p.add_sequence(name)
+        p.allocate(name, 16)
+    freed = p.pages("b")
+    p.free("b")
+    p.add_sequence("d")
+    p.allocate("d", 1)
+    assert p.pages("d") == freed                # most recently freed page first
+    assert p.num_free_pages == 16 - 3
+
+
+def test_exhaustion_is_atomic(iva):
+    p, pc = pool(iva, pages=4)
+    p.add_sequence("a")
+    p.allocate("a", 48)                         # 3 pages
+    p.add_sequence("b")
+    with pytest.raises(pc.OutOfPagesError):
+        p.allocate("b", 40)                     # needs 3, 1 free
+    assert p.length("b") == 0 and p.pages("b") == [] and p.num_free_pages == 1
+
+
+def test_block_table_width_limit(iva):
+    p, pc = pool(iva, max_blocks_per_seq=2)
+    p.add_sequence("a")
+    p.allocate("a", 32)
+    with pytest.raises(pc.OutOfPagesError, match="block table"):
+        p.allocate("a", 1)
+
+
+def test_fork_shares_full_pages_and_copies_partial(iva):
+    p, _ = pool(iva)
+    p.add_sequence("a")
+    p.allocate("a", 40)                         # pages 0,1 full, page 2 partial
+    pa = p.pages("a")
+    p.fork("a", "b")
+    pb = p.pages("b")
+    assert pb[:2] == pa[:2] and pb[2] != pa[2] and p.length("b") == 40
+    p.free("a")                                 # shared pages stay with b
+    assert set(pb[:2]).isdisjoint(p._free)
+    assert pa[2] in p._free
+    p.free("b")
+    assert p.num_free_pages == 16
+
+
+def test_release_outside_window_keeps_sinks_and_window(iva):
+    p, _ = pool(iva, pages=32)
+    p.add_sequence("a")
+    p.allocate("a", 300)                        # pages 0..18
+    released = p.release_outside_window("a", window=64, n_sink=4)
+    # visible: [0, 4) on page 0 and [236, 300) on pages 14..18
+    assert released == 14 - 1
+    pages = p.pages("a")
+    assert pages[0] >= 0 and all(x < 0 for x in pages[1:14]) and all(x >= 0 for x in pages[14:])
+    bt, _ = p.tables(["a"])
+    assert (bt[0, 1:14] == -1).all()
+    with pytest.raises(IndexError):
+        p.slots("a", [100])                     # released page
+    assert p.release_outside_window("a", window=64, n_sink=4) == 0
+
+
+def test_rows_and_state_round_trip(iva):
+    p, _ = pool(iva)
+    p.add_sequence(("x", 1))
+    p.allocate(("x", 1), 17)
+    p.add_sequence("y")
+    p.allocate("y", 5)
+    st = p.state_dict()
+    q, _ = pool(iva)
+    q.load_state_dict(st)
+    assert q.pages(("x", 1)) == p.pages(("x", 1)) and q.length("y") == 5
+    assert np.array_equal(q.tables(["y", ("x", 1)])[0], p.tables(["y", ("x", 1)])[0])
+    with pytest.raises(ValueError):
+        pool(iva, pages=8)[0].load_state_dict(st)
+
+
+def test_from_config_honours_quant_infer_memory_block(iva):
+    """configs/quant_infer.yaml:50-54: paged_kv_cache, kv_cache_dtype, kv_cache_size,
+    kv_cache_blocks."""
+    from importlib import import_module
+    import torch
+    pc = import_module("iva_amd.paged_cache")
+    cfg = {"paged_kv_cache": True, "kv_cache_dtype": "bf16", "kv_cache_size": 1024,
+           "kv_cache_blocks": 256}
+    p = pc.PagedKVPool.from_config(cfg, num_layers=2, num_kv_heads=8, head_dim=128, device="cpu")
+    assert p.num_pages == 256 and p.max_blocks == 64 and p.dtype == torch.bfloat16
+    assert len(p.k_pools) == 2 and p.k_pools[0].shape == (256, 8, 16, 16, 8)
+    with pytest.raises(NotImplementedError, match="fp8"):
+        pc.PagedKVPool.from_config(dict(cfg, kv_cache_dtype="fp8"), 1, 8, 128, device="cpu")
+    with pytest.raises(ValueError):
+        pc.PagedKVPool.from_config(dict(cfg, paged_kv_cache=False), 1, 8, 128, device="cpu")
+
+
+def test_churn_keeps_tables_consistent(iva):
+    """Random adds / appends / frees: every live page is owned exactly once, the free
+    list and the owned pages partition the pool, tables mirror the page lists."""
+    rng = np.random.default_rng(0)
+    p, pc = pool(iva, pages=64, max_seqs=16)
+    live = {}
+    for step in range(400):
+        op = rng.integers(3)
+        if op == 0 and len(live) < 16:
+            sid = ("s", step)
+            p.add_sequence(sid)
+            live[sid] = 0
+        elif op == 1 and live:
+            sid = list(live)[rng.integers(len(live))]
+            n = int(rng.integers(1, 40))
+            try:
+                p.allocate(sid, n)
+                live[sid] += n
+            except pc.OutOfPagesError:
+                pass
+        elif live:
+            sid = list(live)[rng.integers(len(live))]
+            p.free(sid)
+            del live[sid]
+        owned = [x for s in live for x in p.pages(s)]
+        assert len(owned) == len(set(owned))
+        assert sorted(owned + p._free) == list(range(64))
+        for s, n in live.items():
+            assert p.length(s) == n
+            bt, ctx = p.tables([s])
+            assert list(bt[0, :len(p.pages(s))]) == p.pages(s) and ctx[0] == n

@@ -1,0 +1,115 @@
+"""Model-level boundary on the CPU: TransformerConfig whitelist and GQA fields,
+get_attention dispatch, the torch backend's cache semantics (incremental decode
+equals a full recompute at absolute positions, window and sinks as a union), the
+FFN's gate/up convention, and the paged backend refusing to run without the GPU
+library."""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+
+@pytest.fixture(scope="module")
+def M(iva):
+    from importlib import import_module
+    return import_module("iva_amd.model")
+
+
+def small_cfg(M, **kw):
+    base = dict(d_model=64, n_layers=2, n_heads=4, vocab_size=97, seq_len=128, dropout=0.0,
+                n_kv_heads=2)
+    base.update(kw)
+    return M.TransformerConfig(**base)
+
+
+def test_config_whitelist_and_kv_heads(M):
+    cfg = M.TransformerConfig(attn_impl="hip_paged")
+    assert cfg.n_kv_heads == cfg.n_heads == 16 and cfg.head_dim == 64
+    with pytest.raises(ValueError, match="attn_impl"):
+        M.TransformerConfig(attn_impl="flash")
+    with pytest.raises(ValueError, match="n_kv_heads"):
+        M.TransformerConfig(n_heads=16, n_kv_heads=6)
+    with pytest.raises(ValueError, match="divisible"):
+        M.TransformerConfig(d_model=100, n_heads=16)
+
+
+def test_get_attention_dispatch(M):
+    assert isinstance(M.get_attention(small_cfg(M, attn_impl="hip_paged")), M.PagedAttention)
+    assert isinstance(M.get_attention(small_cfg(M)), M.AttentionTorch)
+    with pytest.raises(NotImplementedError):
+        M.get_attention(small_cfg(M, attn_impl="triton"))
+    with pytest.raises(NotImplementedError):
+        M.TransformerBlock(small_cfg(M, moe_enable=True))
+
+
+def test_ffn_is_silu_up_times_gate(M):
+    """ffn.py:21-24,57-60: SwiGLU(cat([gate, up])) = silu(up) * gate."""
+    torch.manual_seed(0)
+    f = M.FFN(small_cfg(M))
+    x = torch.randn(3, 64)
+    ref = f.down_proj(torch.nn.functional.silu(f.up_proj(x)) * f.gate_proj(x))
+    assert torch.allclose(f(x), ref)
+    g = f.gate_proj(x)
+    wrong = f.down_proj(torch.nn.functional.silu(g) * f.up_proj(x))
+    assert not torch.allclose(f(x), wrong, atol=1e-6)
+
+
+def test_rmsnorm_matches_formula(M):
+    n = M.RMSNorm(small_cfg(M))
+    with torch.no_grad():
+        n.weight.copy_(torch.linspace(0.5, 1.5, 64))
+    x = torch.randn(5, 64)
+    ref = x / torch.sqrt((x ** 2).mean(-1, keepdim=True) + 1e-6) * n.weight
+    assert torch.allclose(n(x), ref, atol=1e-6)
+
+
+@pytest.mark.parametrize("window,sinks", [(None, 0), (5, 0), (5, 3)])
+def test_torch_backend_incremental_equals_full(M, window, sinks):
+    """Prefill + token-by-token decode through the cache gives the logits a single
+    full forward gives (causal masks at absolute positions)."""
+    torch.manual_seed(1)
+    model = M.Transformer(small_cfg(M, sliding_window=window, sink_tokens=sinks)).eval()
+    ids = torch.randint(0, 97, (3, 20))
+    with torch.no_grad():
+        full = model(ids)["logits"]
+        cache = model.new_kv_cache(3, 20, device="cpu", dtype=torch.float32)
+        parts = [model(ids[:, :8], kv_cache=cache)["logits"]]
+        for t in range(8, 20):
+            parts.append(model(ids[:, t:t + 1], kv_cache=cache)["logits"])
+        inc = torch.cat(parts, dim=1)
+    assert cache.seq_len == 20
+    assert torch.allclose(inc, full, atol=1e-5), (inc - full).abs().max()
+
+
+def test_window_and_sinks_are_a_union(M):
+    """A decode query sees keys j with j > i - W or j < n_sink (union), at absolute
+    positions; brute force over a tiny case."""
+    q_pos = torch.tensor([9])
+    k_pos = torch.arange(10)
+    vis = M._visible(q_pos, k_pos, window=3, n_sink=2)[0]
+    assert vis.tolist() == [True, True, False, False, False, False, False, True, True, True]
+    assert M._visible(q_pos, k_pos, None, 2)[0].all()
+
+
+def test_reference_style_cache_object_still_works(M):
+    """A KVCache (rope_kv.py:71-137) passed to one attention module is replaced by a new
+    object holding the concatenated rows, as attention.py:61-75 does."""
+    torch.manual_seed(2)
+    att = M.AttentionTorch(small_cfg(M)).eval()
+    cache = M.KVCache(2, 2, 16, 0, torch.device("cpu"), torch.float32)
+    x = torch.randn(2, 4, 64)
+    _, c1 = att(x, kv_cache=cache)
+    assert c1 is not cache and c1.seq_len == 4 and c1.k.shape == (2, 2, 4, 16)
+
+
+def test_paged_backend_needs_the_gpu_library(M):
+    att = M.PagedAttention(small_cfg(M, attn_impl="hip_paged")).eval()
+    with pytest.raises(TypeError, match="PagedKVCache"):
+        att(torch.randn(1, 1, 64), kv_cache=M.KVCache(1, 2, 16, 0, torch.device("cpu")))
+    from importlib import import_module
+    pc = import_module("iva_amd.paged_cache")
+    cache = pc.PagedKVCache(1, 2, 16, 0, "cpu", torch.float32, num_layers=1, max_seq_len=32)
+    with pytest.raises(RuntimeError, match="GPU"):
+        att(torch.randn(1, 3, 64), kv_cache=cache)  # the HIP kernels run on the GPU only
