@@ -67,6 +67,10 @@ def parse_args():
                    help="launch a plain 256 MiB copy 10x after timing (counter calibration)")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="write the HBM traffic summary from two rocprofv3 --pmc runs")
+    p.add_argument("--c5-steps", type=int, default=40, help="timed churn steps of --workload c5")
+    p.add_argument("--workload", choices=("c2", "c3", "c4", "c5"), default="c2",
+                   help="c2 (default): the contract line; c3 dense-decoder tokens/s, c4 "
+                        "long-context window+sinks decode, c5 ragged churn (informational lines)")
     return p.parse_args()
 
 
@@ -180,6 +184,143 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> None:
     print(json.dumps(summary))
 
 
+def _timer(torch, dev):
+    def measure(fn, reps=1):
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        return e0.elapsed_time(e1) / reps * 1e-3
+    return measure
+
+
+def bench_c3(args, iva, torch, dev):
+    """C3: dense decoder (d 1024, 16 layers, 16 heads, head_dim 64, vocab 32000, RMSNorm +
+    SwiGLU, random init, bf16), 16 prompts of 512 uniform-random ids + 256 greedy steps
+    on the paged cache.  Decode tokens/s come from the difference of two generate()
+    calls (256 and 128 new tokens), so prefill and graph capture cancel out."""
+    M = iva.model
+    measure = _timer(torch, dev)
+    cfg = M.TransformerConfig(d_model=1024, n_layers=16, n_heads=16, vocab_size=32000,
+                              seq_len=4096, attn_impl="hip_paged", dropout=0.0)
+    torch.manual_seed(0)
+    model = M.Transformer(cfg).to(dev, torch.bfloat16).eval()
+    prompts = torch.randint(0, 32000, (16, 512), generator=torch.Generator().manual_seed(0)).to(dev)
+    gen = lambda n, graph: model.generate(prompts, max_length=n, do_sample=False,
+                                          eos_token_id=None, use_graph=graph)
+    with torch.no_grad():
+        gen(4, True)
+        gen(4, False)
+
+        def prefill():
+            cache = model.new_kv_cache(16, 512 + 256)
+            model(prompts, kv_cache=cache)
+            cache.free()
+        t_prefill = measure(prefill, 3)
+        t256 = measure(lambda: gen(256, True))
+        t128 = measure(lambda: gen(128, True))
+        e64 = measure(lambda: gen(64, False))
+        e32 = measure(lambda: gen(32, False))
+        tokens_paged = gen(256, True)
+        ref = M.Transformer(M.TransformerConfig(**{**cfg.__dict__, "attn_impl": "torch"})).to(
+            dev, torch.bfloat16).eval()
+        ref.load_state_dict(model.state_dict())
+        tokens_torch = ref.generate(prompts, max_length=256, do_sample=False, eos_token_id=None)
+    same = (tokens_paged == tokens_torch)[:, 512:]
+    first_diff = [int((~row).nonzero()[0]) if (~row).any() else 256 for row in same.cpu()]
+    weight_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
+    step_s = (t256 - t128) / 128
+    return {
+        "metric": "C3 dense-decoder greedy decode tokens/s (paged KV, bf16)", "workload": "c3",
+        "value": round(16 / step_s, 1), "unit": "tokens/s", "n_gpus": 1, "dtype": "bf16",
+        "data": "synthetic (random init, uniform-random prompt ids)",
+        "config": {"d_model": 1024, "n_layers": 16, "n_heads": 16, "head_dim": 64,
+                   "vocab": 32000, "batch": 16, "prompt": 512, "new_tokens": 256,
+                   "launch": "decode step captured as one HIP graph"},
+        "ms_per_decode_step": round(step_s * 1e3, 4),
+        "eager_tokens_per_s": round(16 * 32 / (e64 - e32), 1),
+        "prefill_ms": round(t_prefill * 1e3, 3),
+        "end_to_end_tokens_per_s": round(16 * 256 / (t256 - t_prefill), 1),
+        "weight_bytes": weight_bytes,
+        "weights_gbps_per_step": round(weight_bytes / step_s / 1e9, 1),
+        "greedy_tokens_identical_to_torch_backend": int(same.all(dim=1).sum()),
+        "first_divergence_per_seq": first_diff,
+    }
+
+
+def bench_c4(args, iva, torch, dev):
+    """C4: long-context decode, bf16, B 4 at 32k/64k/96k/128k, GQA 32/8, D 128, window
+    4096 + 4 sinks (union); GB/s on attended bytes."""
+    wl = iva.workloads
+    measure = _timer(torch, dev)
+    sets = []
+    for i in range(args.pools):
+        d = wl.c4_long_context(seed=10 + i, device=dev)
+        lay = d["layout"]
+        sets.append((d["q"], d["k_pool"], d["v_pool"], lay.block_tables.to(dev),
+                     lay.context_lens.to(dev), torch.empty_like(d["q"])))
+    w, ns = wl.C4_WINDOW, wl.C4_SINKS
+    run = lambda s, fn: fn(s[0], s[1], s[2], s[3], s[4], window=w, n_sink=ns, out=s[5])
+    for s in sets:
+        run(s, iva.paged_decode_attention)
+    reps = 50
+    t_attn = measure(lambda: [run(sets[i % len(sets)], iva.paged_decode_attention)
+                              for i in range(reps)]) / reps
+    t_walk = measure(lambda: [run(sets[i % len(sets)], iva.paged_decode_attention_partial)
+                              for i in range(reps)]) / reps
+    attended = [min(n, w) + min(ns, max(n - w, 0)) for n in wl.C4_LENGTHS]
+    byts = sum(2 * a * 8 * 128 * 2 for a in attended) + 2 * 4 * 32 * 128 * 2
+    return {"metric": "C4 long-context windowed decode attention GB/s (attended bytes)",
+            "workload": "c4", "value": round(byts / t_attn / 1e9, 1), "unit": "GB/s",
+            "dtype": "bf16", "config": {"lengths": wl.C4_LENGTHS, "window": w, "sinks": ns,
+                                        "heads": "32/8", "head_dim": 128, "launch": "eager"},
+            "attention_us": round(t_attn * 1e6, 2), "walk_us": round(t_walk * 1e6, 2),
+            "walk_gbps": round(byts / t_walk / 1e9, 1), "attended_bytes": byts}
+
+
+def bench_c5(args, iva, torch, dev):
+    """C5: ragged continuous-batching churn, fp16: 256 live sequences, LogNormal(ln 1024,
+    sigma 1) lengths capped at 16k, 512-token prefill chunks, one decode token per
+    sequence per step, completed sequences replaced (LIFO page reuse).  Reports the
+    decode attention GB/s per step on the fragmented tables."""
+    from importlib import import_module
+    pc = import_module("iva_amd.paged_cache")
+    wl = iva.workloads
+    pool = pc.PagedKVPool(48000, 8, 128, 16, 1, torch.float16, dev, max_seqs=512,
+                          max_blocks_per_seq=1024)
+    churn = wl.ChurnBatch(pool, n_seqs=256, seed=0, scale=128 ** -0.5)
+    q = (torch.randn(256, 32, 128, device=dev) * 128 ** -0.5).half()
+    out = torch.empty_like(q)
+    for _ in range(5):
+        churn.step()
+    times, byts, done = [], [], 0
+    for _ in range(args.c5_steps):
+        done += churn.step()
+        bt, ctx = churn.tables()
+        lens = churn.lengths()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        iva.paged_decode_attention(q, pool.k_pools[0], pool.v_pools[0], bt, ctx, out=out)
+        e1.record()
+        torch.cuda.synchronize(dev)
+        times.append(e0.elapsed_time(e1) * 1e-3)
+        byts.append(sum(2 * n * 8 * 128 * 2 for n in lens) + 2 * 256 * 32 * 128 * 2)
+    t = statistics.median(times)
+    gbs = statistics.median([b / x / 1e9 for b, x in zip(byts, times)])
+    return {"metric": "C5 ragged churn decode attention GB/s per step", "workload": "c5",
+            "value": round(gbs, 1), "unit": "GB/s", "dtype": "f16",
+            "config": {"live_seqs": 256, "lengths": "LogNormal(ln 1024, 1.0) cap 16384",
+                       "prefill_chunk": 512, "steps": args.c5_steps, "heads": "32/8",
+                       "launch": "eager, one attention call per step"},
+            "attention_us_median": round(t * 1e6, 2), "completed_sequences": done,
+            "mean_context": round(statistics.mean(churn.lengths()), 1),
+            "free_pages_left": pool.num_free_pages}
+
+
 def main():
     args = parse_args()
     if args.summarize_pmc:
@@ -198,6 +339,10 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     wl = iva.workloads
+    if args.workload != "c2":
+        fn = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.workload]
+        print(json.dumps(fn(args, iva, torch, dev)), flush=True)
+        return
 
     hq, hkv, d, dtype, esize = 32, 8, 128, torch.float16, 2
     lengths = wl.c2_lengths(seed=0)

@@ -452,12 +452,14 @@ class Transformer(nn.Module):
                 return_value: bool = False, **kwargs) -> Dict[str, torch.Tensor]:
         batch_size, seq_len = input_ids.shape
         device = input_ids.device
-        start = kv_cache.seq_len if kv_cache is not None else 0
-        position_ids = torch.arange(start, start + seq_len, device=device,
-                                    dtype=torch.long).unsqueeze(0).expand(batch_size, -1)
+        if isinstance(kv_cache, PagedKVCache) and kv_cache.static:
+            position_ids = kv_cache.device_positions()  # on the device: graph-replayable
+        else:
+            start = kv_cache.seq_len if kv_cache is not None else 0
+            position_ids = torch.arange(start, start + seq_len, device=device,
+                                        dtype=torch.long).unsqueeze(0).expand(batch_size, -1)
         x = self.token_embedding(input_ids) + self.position_embedding(position_ids)
-        if attention_mask is None:
-            attention_mask = torch.ones_like(input_ids, dtype=torch.bool)
+        # attention_mask None means all ones (transformer.py:212-213 builds ones_like)
         sliding_window = self.config.sliding_window
         sink_cfg = {"sink_tokens": self.config.sink_tokens} if self.config.sink_tokens else None
         for block in self.blocks:
@@ -474,33 +476,85 @@ class Transformer(nn.Module):
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_length: int = 100, temperature: float = 1.0,
                  top_p: float = 0.9, top_k: int = 50, do_sample: bool = True,
-                 pad_token_id: int = 0, eos_token_id: int = 2, **kwargs) -> torch.Tensor:
+                 pad_token_id: int = 0, eos_token_id: Optional[int] = 2, **kwargs) -> torch.Tensor:
         """src/core/transformer.py:257-320 with an incremental cache: one prefill
-        forward of the prompt, then one single-token forward per new token."""
+        forward of the prompt, then one single-token forward per new token.
+
+        With ``attn_impl="hip_paged"`` and ``use_graph=True`` (keyword) the decode
+        step is captured once as a HIP graph and replayed: the cache's pages are
+        reserved up front and its per-step bookkeeping runs on the device.  EOS
+        stopping (``eos_token_id``) needs a host read per step; pass None to run
+        all ``max_length`` steps without one.
+        """
         self.eval()
         batch_size, prompt_len = input_ids.shape
+        own_cache = kwargs.get("kv_cache") is None
         cache = kwargs.get("kv_cache") or self.new_kv_cache(batch_size, prompt_len + max_length)
-        generated = input_ids.clone()
-        step_ids = input_ids
-        finished = False
+        use_graph = bool(kwargs.get("use_graph", False))
+        if use_graph and not isinstance(cache, PagedKVCache):
+            raise ValueError("use_graph needs attn_impl='hip_paged'")
+        out = torch.empty(batch_size, prompt_len + max_length, dtype=input_ids.dtype,
+                          device=input_ids.device)
+        out[:, :prompt_len] = input_ids
+        n = 0
         try:
-            for _ in range(max_length):
-                logits = self.forward(step_ids, kv_cache=cache)["logits"][:, -1, :]
-                next_token = self._sample(logits, temperature, top_p, top_k, do_sample)
-                generated = torch.cat([generated, next_token], dim=1)
-                step_ids = next_token
-                if (next_token == eos_token_id).all():
-                    finished = True
-                    break
+            logits = self.forward(input_ids, kv_cache=cache)["logits"][:, -1, :]
+            tok = self._sample(logits, temperature, top_p, top_k, do_sample)
+            out[:, prompt_len] = tok[:, 0]
+            n = 1
+            if use_graph and max_length > 1:
+                n = self._decode_graph(cache, tok, out, prompt_len, max_length, temperature,
+                                       top_p, top_k, do_sample)
+            else:
+                while n < max_length and not (eos_token_id is not None
+                                              and bool((tok == eos_token_id).all())):
+                    logits = self.forward(tok, kv_cache=cache)["logits"][:, -1, :]
+                    tok = self._sample(logits, temperature, top_p, top_k, do_sample)
+                    out[:, prompt_len + n] = tok[:, 0]
+                    n += 1
         finally:
-            if "kv_cache" not in kwargs and isinstance(cache, PagedKVCache):
+            if own_cache and isinstance(cache, PagedKVCache):
                 cache.free()
-        del finished
-        return generated
+        return out[:, :prompt_len + n]
+
+    def _decode_graph(self, cache: PagedKVCache, tok, out, prompt_len, max_length, temperature,
+                      top_p, top_k, do_sample) -> int:
+        """Decode steps 2..max_length as replays of one captured HIP graph.  Step 2 runs
+        eagerly on the capture stream (warming every kernel and workspace), step 3 is
+        captured (capture records without executing), then the graph is replayed."""
+        cache.begin_static_decode(max_length - 1)
+        static_tok = tok.clone()
+        stream = torch.cuda.Stream(device=tok.device)
+        stream.wait_stream(torch.cuda.current_stream(tok.device))
+
+        def step():
+            logits = self.forward(static_tok, kv_cache=cache)["logits"][:, -1, :]
+            static_tok.copy_(self._sample(logits, temperature, top_p, top_k, do_sample))
+
+        n = 1
+        try:
+            with torch.cuda.stream(stream):
+                step()
+                cache.advance_host(1)
+                out[:, prompt_len + n] = static_tok[:, 0]
+                n += 1
+                if n < max_length:
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph, stream=stream):
+                        step()  # recorded, not executed: the device state does not move
+                    while n < max_length:
+                        graph.replay()
+                        cache.advance_host(1)
+                        out[:, prompt_len + n] = static_tok[:, 0]
+                        n += 1
+            torch.cuda.current_stream(tok.device).wait_stream(stream)
+        finally:
+            cache.end_static_decode()
+        return n
 
     @staticmethod
-    def _sample(logits, temperature, top_p, top_k, do_sample):
-        """Top-k / top-p / multinomial or argmax (transformer.py:292-313)."""
+    def _sample_filtered(logits, temperature, top_p, top_k):
+        """Temperature, top-k and top-p filtering, then a multinomial draw."""
         logits = logits / temperature
         if top_k > 0:
             vals, idx = torch.topk(logits, top_k)
@@ -512,6 +566,12 @@ class Transformer(nn.Module):
             remove[..., 1:] = remove[..., :-1].clone()
             remove[..., 0] = False
             logits = logits.masked_fill(remove.scatter(1, sorted_idx, remove), float("-inf"))
-        if do_sample:
-            return torch.multinomial(F.softmax(logits, dim=-1), num_samples=1)
-        return torch.argmax(logits, dim=-1, keepdim=True)
+        return torch.multinomial(F.softmax(logits, dim=-1), num_samples=1)
+
+    @staticmethod
+    def _sample(logits, temperature, top_p, top_k, do_sample):
+        """Top-k / top-p / multinomial or argmax (transformer.py:292-313).  Greedy
+        decoding takes the argmax directly: the filters always keep the maximum."""
+        if not do_sample:
+            return torch.argmax(logits, dim=-1, keepdim=True)
+        return Transformer._sample_filtered(logits, temperature, top_p, top_k)

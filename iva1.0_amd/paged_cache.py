@@ -352,6 +352,7 @@ class PagedKVCache:
         self._view: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor, int, int]] = None
         self._bt_dev: Optional[torch.Tensor] = None
         self._bt_pages = -1
+        self._static: Optional[dict] = None
         if seq_len > 0:
             z = torch.zeros(self.batch_size, self.n_heads, int(seq_len), self.head_dim,
                             dtype=dtype, device=self.device)
@@ -448,6 +449,64 @@ class PagedKVCache:
             self._bt_pages = pages
         return self._bt_dev, torch.from_numpy(ctx).to(self.device)
 
+    # ------------------------------------------------------ static decode
+    @property
+    def static(self) -> bool:
+        return self._static is not None
+
+    def begin_static_decode(self, steps: int) -> None:
+        """Switches to single-token steps whose bookkeeping runs on the device, so a
+        whole decode step can be captured in a HIP graph and replayed.  Pages for
+        ``steps`` more tokens per sequence are reserved now; each step then derives
+        the new token's slot from the (fixed) block table and the device context
+        lengths, and advances those lengths, with device ops only.  The host-side
+        ``seq_len`` is advanced by :meth:`advance_host` (once per replay);
+        :meth:`end_static_decode` writes the lengths back to the pool."""
+        if self._view is not None or self._cursor != 0:
+            raise RuntimeError("a forward is in progress on this cache")
+        self.resize(self.seq_len + int(steps))
+        bt, ctx = self.pool.tables(self.seq_ids)
+        self._static = {
+            "bt": torch.from_numpy(bt).to(self.device),
+            "ctx": torch.from_numpy(ctx).to(self.device),
+            "slot": torch.empty(self.batch_size, dtype=torch.int32, device=self.device),
+            "pos": torch.empty(self.batch_size, 1, dtype=torch.int64, device=self.device),
+            "limit": self.seq_len + int(steps),
+        }
+        self._static["pos"].copy_(self._static["ctx"].view(-1, 1))
+
+    def device_positions(self) -> torch.Tensor:
+        """int64 [B, 1] positions of the next token (static decode), on the device."""
+        st = self._static
+        st["pos"].copy_(st["ctx"].view(-1, 1))
+        return st["pos"]
+
+    def advance_host(self, steps: int = 1) -> None:
+        """Host-side length bookkeeping for ``steps`` replayed static decode steps."""
+        self.seq_len += int(steps)
+        if self.seq_len > self._static["limit"]:
+            raise RuntimeError("static decode ran past the reserved pages")
+
+    def end_static_decode(self) -> None:
+        """Leaves static decode: the pool's lengths catch up with ``seq_len``."""
+        if self._static is None:
+            return
+        for s in self.seq_ids:
+            grow = self.seq_len - self.pool.length(s)
+            if grow > 0:
+                self.pool.allocate(s, grow)
+        self._static = None
+        self._bt_pages = -1
+
+    def _static_step(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, int, int]:
+        st = self._static
+        ctx = st["ctx"]
+        page = st["bt"].gather(1, torch.div(ctx, self.block_size, rounding_mode="floor")
+                               .long().view(-1, 1)).view(-1)
+        st["slot"].copy_(page * self.block_size + ctx % self.block_size)
+        ctx.add_(1)
+        return st["slot"], st["bt"], ctx, self.seq_len, 1
+
     def layer_step(self, k_rows: torch.Tensor, v_rows: torch.Tensor) -> LayerView:
         """Appends the new tokens' K/V rows ([B, T, Hkv, D]) of the layer at the cursor and
         returns that layer's view.  The first call of a forward allocates the pages of
@@ -456,7 +515,11 @@ class PagedKVCache:
         b, t = k_rows.shape[0], k_rows.shape[1]
         if b != self.batch_size:
             raise ValueError(f"batch {b} != cache batch {self.batch_size}")
-        if self._cursor == 0:
+        if self._cursor == 0 and self._static is not None:
+            if t != 1:
+                raise ValueError("static decode appends one token per step")
+            self._view = self._static_step()
+        elif self._cursor == 0:
             start = self.seq_len
             slots = np.concatenate([self.pool.allocate(s, t) for s in self.seq_ids])
             slot_dev = torch.from_numpy(slots).to(self.device, non_blocking=True)
@@ -475,7 +538,8 @@ class PagedKVCache:
         self._cursor += 1
         if self._cursor == self.num_layers:
             self._cursor = 0
-            self.seq_len = start + t
+            if self._static is None:
+                self.seq_len = start + t
             self._view = None
         return view
 

@@ -140,3 +140,83 @@ def c5_lengths(seed: int, n_seqs: int = 256, median: int = 1024, sigma: float = 
     z = torch.randn(n_seqs, generator=gen, dtype=torch.float64)
     lens = torch.exp(math.log(median) + sigma * z).round().clamp(1, cap)
     return [int(x) for x in lens.tolist()]
+
+
+class ChurnBatch:
+    """Config C5 driver: continuous batching over a PagedKVPool (one layer, fp16,
+    GQA 32/8, head_dim 128 by default).
+
+    ``n_seqs`` sequences are live at any time, each with a target length drawn from
+    LogNormal(ln median, sigma) capped at ``cap``.  A new sequence is prefilled in
+    ``chunk``-token appends; every step appends one decode token to each live
+    sequence; a sequence that reaches its target completes, its pages go back to
+    the LIFO free list and a new sequence takes its block-table row, reusing those
+    pages, so block tables become fragmented.  K/V rows are drawn from a seeded
+    device generator; the host keeps the lengths.
+    """
+
+    def __init__(self, pool, n_seqs: int = 256, median: int = 1024, sigma: float = 1.0,
+                 cap: int = 16384, chunk: int = 512, seed: int = 0, scale: float = 1.0):
+        self.pool = pool
+        self.n_seqs, self.median, self.sigma, self.cap, self.chunk = n_seqs, median, sigma, cap, chunk
+        self.scale = scale
+        self.gen = torch.Generator().manual_seed(seed)
+        self.dev_gen = torch.Generator(device=pool.device).manual_seed(seed + 1)
+        self.ids = []
+        self.targets = {}
+        self._next = 0
+        for _ in range(n_seqs):
+            self._start()
+
+    def _draw_length(self) -> int:
+        z = torch.randn(1, generator=self.gen, dtype=torch.float64).item()
+        return int(max(1, min(self.cap, round(math.exp(math.log(self.median) + self.sigma * z)))))
+
+    def _rows(self, n: int):
+        shape = (n, self.pool.num_kv_heads, self.pool.head_dim)
+        k = torch.randn(shape, generator=self.dev_gen, device=self.pool.device) * self.scale
+        v = torch.randn(shape, generator=self.dev_gen, device=self.pool.device) * self.scale
+        return k.to(self.pool.dtype), v.to(self.pool.dtype)
+
+    def _append(self, sid, n: int) -> None:
+        from .ops import kv_append
+        slots = torch.from_numpy(self.pool.allocate(sid, n)).to(self.pool.device)
+        k, v = self._rows(n)
+        kv_append(k, v, self.pool.k_pools[0], self.pool.v_pools[0], slots)
+
+    def _start(self) -> None:
+        sid = ("c5", self._next)
+        self._next += 1
+        target = self._draw_length()
+        self.pool.add_sequence(sid)
+        self.ids.append(sid)
+        self.targets[sid] = target
+        prompt = max(1, target // 2)
+        for off in range(0, prompt, self.chunk):       # prefill-chunk appends
+            self._append(sid, min(self.chunk, prompt - off))
+
+    def step(self) -> int:
+        """One decode step: one token appended to every live sequence (a single append
+        launch), completed sequences freed and replaced by new, chunk-prefilled ones.
+        Returns how many sequences completed."""
+        import numpy as np
+        from .ops import kv_append
+        slots = np.concatenate([self.pool.allocate(sid, 1) for sid in self.ids])
+        k, v = self._rows(len(self.ids))
+        kv_append(k, v, self.pool.k_pools[0], self.pool.v_pools[0],
+                  torch.from_numpy(slots).to(self.pool.device))
+        finished = [sid for sid in self.ids if self.pool.length(sid) >= self.targets[sid]]
+        for sid in finished:
+            self.pool.free(sid)
+            self.ids.remove(sid)
+            del self.targets[sid]
+        for _ in finished:
+            self._start()
+        return len(finished)
+
+    def tables(self):
+        """Device block tables and context lengths of the live sequences."""
+        return self.pool.device_tables(self.ids)
+
+    def lengths(self):
+        return [self.pool.length(s) for s in self.ids]

@@ -121,3 +121,22 @@ def test_paged_cache_duck_type(M, iva, dev):
     n_free = cache.pool.num_free_pages
     cache.free()
     assert cache.pool.num_free_pages > n_free
+
+
+def test_graph_decode_matches_eager(M, dev):
+    """generate(use_graph=True) replays one captured decode step with device-side cache
+    bookkeeping; it must emit exactly the tokens of the eager loop."""
+    _, paged = twin_models(M, torch.bfloat16, dev)
+    ids = torch.randint(0, 512, (4, 40), device=dev)
+    with torch.no_grad():
+        a = paged.generate(ids, max_length=12, do_sample=False, eos_token_id=None, use_graph=True)
+        b = paged.generate(ids, max_length=12, do_sample=False, eos_token_id=None, use_graph=False)
+    assert a.shape == (4, 52) and torch.equal(a, b)
+    # a cache passed in keeps its length bookkeeping in step with the device
+    cache = paged.new_kv_cache(4, 60)
+    with torch.no_grad():
+        paged.generate(ids, max_length=10, do_sample=False, eos_token_id=None, use_graph=True,
+                       kv_cache=cache)
+    assert cache.seq_len == 40 + 9   # the last sampled token is not fed back
+    assert all(cache.pool.length(s) == 49 for s in cache.seq_ids)
+    cache.free()
