@@ -1,8 +1,10 @@
 """Benchmark of the paged KV hot path on one MI355X.
 
 A step is one decode step of the hot path over one batch: append one new K/V row
-per sequence into its page (ivakv_append), then paged GQA decode attention over
-the whole context (ivakv_decode_attn: the paged walk + the split merge).
+per sequence into its page, then paged GQA decode attention over the whole
+context.  By default the step is the fused op ivakv_decode_append_attn (the paged
+walk over the earlier positions + a merge that scores the new token and stores
+its rows); --unfused runs ivakv_append then ivakv_decode_attn.
 Workload C2: 32 sequences, 32 query / 8 KV heads, head_dim 128, fp16, block 16,
 context lengths ~ U[512, 4096] (seed 0), values N(0, 1)/sqrt(128).
 
@@ -63,6 +65,8 @@ def parse_args():
                    help="launches of the paged walk timed for the roofline figure")
     p.add_argument("--cpu-reps", type=int, default=10, help="timed CPU-baseline reps (0 = skip)")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of graphs")
+    p.add_argument("--unfused", action="store_true",
+                   help="step = ivakv_append + ivakv_decode_attn instead of the fused op")
     p.add_argument("--copy-calibration", action="store_true",
                    help="launch a plain 256 MiB copy 10x after timing (counter calibration)")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -373,8 +377,13 @@ def main():
                                    partition_pages=pp, out=s["out"], workspace=workspace)
 
     def step(s):
-        iva.kv_append(s["k_new"], s["v_new"], s["k_pool"], s["v_pool"], s["slots"])
-        attention(s)
+        if args.unfused or args.partition_pages:
+            iva.kv_append(s["k_new"], s["v_new"], s["k_pool"], s["v_pool"], s["slots"])
+            attention(s)
+        else:  # append + attend in one op (ivakv_decode_append_attn)
+            iva.paged_decode_append_attention(s["q"], s["k_new"], s["v_new"], s["k_pool"],
+                                              s["v_pool"], s["bt"], s["ctx"], out=s["out"],
+                                              workspace=workspace)
 
     def walk(s):
         iva.paged_decode_attention_partial(s["q"], s["k_pool"], s["v_pool"], s["bt"], s["ctx"],
@@ -495,7 +504,9 @@ def main():
                    "mean_context": round(sum(lengths) / batch, 1), "pools_rotated": args.pools,
                    "pool_bytes_total": pool_bytes, "launch": "eager" if args.eager else "hip graph",
                    "walk": "partitioned, %d pages" % args.partition_pages
-                   if args.partition_pages else "stream"},
+                   if args.partition_pages else "stream",
+                   "step_ops": "ivakv_append + ivakv_decode_attn" if args.unfused or
+                   args.partition_pages else "ivakv_decode_append_attn (fused)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "kernel": walk_name,

@@ -162,6 +162,28 @@ int ivakv_decode_attn_merge(const void* q, const void* k_pool, const void* v_poo
                             hipStream_t stream);
 
 /*
+ * Fused decode step: append, then attend.  Position L-1 = context_lens[b]-1 of every
+ * sequence is the new token; its rows k_new / v_new ([batch][Hkv][D] dense, pool
+ * dtype) are written to that position's slot (block_tables[b][(L-1)/BS]*BS +
+ * (L-1)%BS; skipped when that page id is outside the table or the pool) and
+ * attended together with positions < L-1 read from the pools.  Same result as
+ * ivakv_append of those rows followed by ivakv_decode_attn, in two launches
+ * instead of three: the pool walk skips position L-1 and the merge scores the new
+ * token straight from k_new.  Workspace: ivakv_decode_workspace_size with
+ * partition_pages <= 0.  Supported geometry as ivakv_decode_attn, batch <= 8192.
+ * Replaces: the append + score sequence of AttentionTorch.forward with a cache
+ * (src/core/attention.py:61-102): torch.cat of the new K/V, then the attention
+ * math over the extended cache.
+ */
+int ivakv_decode_append_attn(const void* q, const void* k_new, const void* v_new,
+                             void* k_pool, void* v_pool, const int32_t* block_tables,
+                             const int32_t* context_lens, void* out, void* workspace,
+                             size_t workspace_bytes, int batch, int num_q_heads,
+                             int num_kv_heads, int head_dim, int block_size, int max_blocks,
+                             int num_pages, float scale, int window, int n_sink, int dtype,
+                             hipStream_t stream);
+
+/*
  * Index gather on a contiguous-layout cache kv = [batch][n_heads][seq_len][D]
  * with element strides (s_b, s_h, s_s, s_d):
  *   out[b, h, j, :] = kv[b, h, indices[j], :]      out = [B][H][n_idx][D] dense

@@ -15,6 +15,7 @@ from .ops import (
     kv_append,
     kv_gather,
     kv_ops,
+    paged_decode_append_attention,
     paged_decode_attention,
     paged_decode_attention_merge,
     paged_decode_attention_partial,
@@ -38,6 +39,7 @@ __all__ = [
     "kv_append",
     "kv_gather",
     "kv_ops",
+    "paged_decode_append_attention",
     "paged_decode_attention",
     "paged_decode_attention_merge",
     "paged_decode_attention_partial",

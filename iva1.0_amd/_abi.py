@@ -64,6 +64,15 @@ SIGNATURES = {
     "ivakv_decode_attn": (c_int, _DECODE_ARGS),
     "ivakv_decode_attn_partial": (c_int, _DECODE_ARGS),
     "ivakv_decode_attn_merge": (c_int, _DECODE_ARGS),
+    "ivakv_decode_append_attn": (c_int, [
+        c_void_p, c_void_p, c_void_p,          # q, k_new, v_new
+        c_void_p, c_void_p, c_void_p, c_void_p,  # k_pool, v_pool, block_tables, context_lens
+        c_void_p, c_void_p, c_size_t,          # out, workspace, workspace_bytes
+        c_int, c_int, c_int, c_int,            # batch, num_q_heads, num_kv_heads, head_dim
+        c_int, c_int, c_int, c_float,          # block_size, max_blocks, num_pages, scale
+        c_int, c_int, c_int,                   # window, n_sink, dtype
+        c_void_p,                              # stream
+    ]),
     "ivakv_index_gather": (c_int, [
         c_void_p, c_int64, c_int64, c_int64, c_int64,  # kv + strides
         c_void_p, c_int,                             # indices, n_idx

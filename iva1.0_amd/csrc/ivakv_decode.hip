@@ -49,12 +49,27 @@ constexpr int kBS = 16;       // rows per page == MFMA tile edge
 constexpr int kWaves = 4;     // wavefronts per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kDefaultPartitionPages = 32;
-constexpr int kPageBufs = 2;  // register page buffers per wave (ring)
+#ifndef IVAKV_PAGE_BUFS
+#define IVAKV_PAGE_BUFS 2
+#endif
+#ifndef IVAKV_STREAM_WGS_PER_CU
+#define IVAKV_STREAM_WGS_PER_CU 2
+#endif
+constexpr int kPageBufs = IVAKV_PAGE_BUFS;  // register page buffers per wave (ring)
 // Workgroups per CU both walks are built for (two 4-wave groups: 2 waves per
 // SIMD, up to 256 registers each), and for the stream walk the wave
 // budget the workspace is sized for, the fewest tiles worth giving a wave, and
 // the largest batch whose page prefix fits the workgroup's LDS.
-constexpr int kStreamWGsPerCU = 2;
+constexpr int kStreamWGsPerCU = IVAKV_STREAM_WGS_PER_CU;
+#ifndef IVAKV_STREAM_WAVES
+#define IVAKV_STREAM_WAVES 8
+#endif
+// Stream walk workgroup: kStreamWaves independent waves (one per SIMD pair per CU
+// at two waves per SIMD).  Fewer, larger workgroups dispatch faster and run the
+// page-prefix scan fewer times per launch.
+constexpr int kStreamWaves = IVAKV_STREAM_WAVES;
+constexpr int kStreamThreads = 64 * kStreamWaves;
+constexpr int kStreamWGs = kStreamWGsPerCU * kWaves / kStreamWaves;  // per CU
 constexpr int kMaxStreamWaves = 4096;
 constexpr int kMinTilesPerWave = 4;
 constexpr int kMaxStreamBatch = 8192;
@@ -74,6 +89,11 @@ struct DecodeArgs {
   float scale_log2;
   int window, n_sink, part_pages, n_parts_max;
   int n_waves;         // stream: waves launched
+  // Fused append (ivakv_decode_append_attn): position L-1 of every sequence is the new
+  // token, whose rows come from k_new / v_new ([B][Hkv][D] dense) instead of the pool.
+  const void* k_new;
+  const void* v_new;
+  int fused;
 };
 
 // Zeroes the 16-bit V elements of rows that are not attended.  A row outside
@@ -181,6 +201,19 @@ __device__ inline int table_pages(const PageWalk& w, int max_blocks) {
   const int sink = min(w.sink_pages, max_blocks);
   const int win = min(cdiv(w.L, kBS), max_blocks) - w.win_first;
   return sink + (win > 0 ? win : 0);
+}
+
+// Page walk of a sequence of context length L as the stream walk reads it: with the
+// fused append the pool covers positions < L - 1 only (the window and sinks are
+// still those of length L); the new token at L - 1 is folded in by the merge.
+__device__ inline PageWalk seq_walk(const DecodeArgs& a, int L) {
+  PageWalk w = make_walk(L, a.window, a.n_sink, kBS);
+  if (a.fused && w.L > 0) {
+    w.L -= 1;
+    const int n_log = cdiv(w.L, kBS);
+    w.n_eff = w.sink_pages + (n_log > w.win_first ? n_log - w.win_first : 0);
+  }
+  return w;
 }
 
 // Partitions of one sequence, capped at the grid's partition count.  The cap only
@@ -420,45 +453,55 @@ __global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_partial_kern
   }
 }
 
-// Log-sum-exp merge of n partial (max, sum, acc) slots into the out rows of
-// unit (b, h); slot(i) gives the workspace slot of the i-th partial.  Every
-// output element runs one online pass over the partials, loading 8 partials'
-// (max, sum, acc) together, so the merge costs one memory round trip per 8
-// partials instead of separate max / sum / accumulate passes.
+// Log-sum-exp fold of n partial (max, sum, acc) slots into one running state
+// (M, L, O) of output element idx (query head g); slot(i) gives the workspace slot
+// of the i-th partial.  One online pass loads 16 partials' (max, sum, acc)
+// together, so the merge costs one memory round trip per 16 partials instead of
+// separate max / sum / accumulate passes.
+template <typename SlotFn>
+__device__ inline void fold_slots(const DecodeArgs& a, int g, int idx, int D, int n, SlotFn slot,
+                                  float& M, float& L, float& O) {
+  const int G = a.G;
+  constexpr int U = 16;
+  for (int i0 = 0; i0 < n; i0 += U) {
+    float mv[U], lv[U], av[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t sl = slot(min(i0 + u, n - 1));
+      mv[u] = a.ws_ml[(sl * G + g) * 2];
+      lv[u] = a.ws_ml[(sl * G + g) * 2 + 1];
+      av[u] = a.ws_acc[sl * G * D + idx];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) mv[u] = i0 + u < n ? mv[u] : kNegInf;
+    float mc = M;
+#pragma unroll
+    for (int u = 0; u < U; ++u) mc = fmaxf(mc, mv[u]);
+    const float m_use = mc == kNegInf ? 0.f : mc;
+    const float f = exp2_fast(M - m_use);
+    L *= f;
+    O *= f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float w = exp2_fast(mv[u] - m_use);
+      L += lv[u] * w;
+      O += av[u] * w;
+    }
+    M = mc;
+  }
+}
+
+// Merge of n partial slots into the out rows of unit (b, h).  Output elements are
+// spread over the workgroup and over grid z (a unit split across workgroups when
+// units are fewer than CUs).
 template <int DT, typename SlotFn>
 __device__ inline void merge_slots(const DecodeArgs& a, int b, int h, int n, int D, SlotFn slot) {
   using E = typename Traits<DT>::E;
   const int G = a.G;
   const int Hq = a.Hkv * G;
-  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
-    const int g = idx / D;
+  for (int idx = threadIdx.x + blockIdx.z * blockDim.x; idx < G * D; idx += blockDim.x * gridDim.z) {
     float M = kNegInf, L = 0.f, O = 0.f;
-    for (int i0 = 0; i0 < n; i0 += 8) {
-      float mv[8], lv[8], av[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int64_t sl = slot(min(i0 + u, n - 1));
-        mv[u] = a.ws_ml[(sl * G + g) * 2];
-        lv[u] = a.ws_ml[(sl * G + g) * 2 + 1];
-        av[u] = a.ws_acc[sl * G * D + idx];
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) mv[u] = i0 + u < n ? mv[u] : kNegInf;
-      float mc = M;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) mc = fmaxf(mc, mv[u]);
-      const float m_use = mc == kNegInf ? 0.f : mc;
-      const float f = exp2_fast(M - m_use);
-      L *= f;
-      O *= f;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float w = exp2_fast(mv[u] - m_use);
-        L += lv[u] * w;
-        O += av[u] * w;
-      }
-      M = mc;
-    }
+    fold_slots(a, idx / D, idx, D, n, slot, M, L, O);
     static_cast<E*>(a.out)[((int64_t)b * Hq + h * G) * D + idx] =
         Traits<DT>::from_float(L > 0.f ? O / L : 0.f);
   }
@@ -499,13 +542,13 @@ __device__ inline int64_t wave_of(int64_t t, int64_t T, int64_t W) { return ((t 
 // compiler read them through the scalar cache (s_load, lgkmcnt) instead of
 // vector loads whose vmcnt wait would drain the page ring.
 template <int DT, int D>
-__global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_stream_kernel(
+__global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kernel(
     DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ ctx) {
   using Ops = TileOps<DT, D>;
   using E = typename Ops::E;
   using VChunk = typename Ops::VChunk;
   constexpr int KLD = Ops::KLD, NB = Ops::NB;
-  extern __shared__ int32_t s_pref[];  // [B + 1] page prefix, then [kThreads] scan scratch
+  extern __shared__ int32_t s_pref[];  // [B + 1] page prefix, then [kStreamThreads] scan scratch
   int32_t* s_scan = s_pref + a.batch + 1;
 
   const int B = a.batch, Hkv = a.Hkv, G = a.G;
@@ -516,17 +559,17 @@ __global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_stream_kerne
 
   // 1. Page prefix of the batch: thread t sums a contiguous chunk of sequences,
   //    a Hillis-Steele scan over the 256 chunk sums, then the chunk prefixes.
-  const int chunk = cdiv(B, kThreads);
+  const int chunk = cdiv(B, kStreamThreads);
   const int c0 = min(tid * chunk, B), c1 = min(c0 + chunk, B);
   int local = 0;
   for (int bb = c0; bb < c1; ++bb) {
-    const int n = table_pages(make_walk(ctx[bb], a.window, a.n_sink, kBS), a.max_blocks);
+    const int n = table_pages(seq_walk(a, ctx[bb]), a.max_blocks);
     s_pref[bb + 1] = n;
     local += n;
   }
   s_scan[tid] = local;
   __syncthreads();
-  for (int off = 1; off < kThreads; off <<= 1) {
+  for (int off = 1; off < kStreamThreads; off <<= 1) {
     const int add = tid >= off ? s_scan[tid - off] : 0;
     __syncthreads();
     s_scan[tid] += add;
@@ -542,12 +585,12 @@ __global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_stream_kerne
   }
   __syncthreads();
   if (blockIdx.x == 0)
-    for (int bb = tid; bb <= B; bb += kThreads) a.ws_pref[bb] = s_pref[bb];
+    for (int bb = tid; bb <= B; bb += kStreamThreads) a.ws_pref[bb] = s_pref[bb];
 
   const int64_t T = (int64_t)Hkv * uni(s_pref[B]);
   if (T == 0) return;
   const int64_t W = stream_waves(T, a.n_waves);
-  const int64_t k = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t k = (int64_t)blockIdx.x * kStreamWaves + __builtin_amdgcn_readfirstlane(tid >> 6);
   if (k >= W) return;
   const int64_t t_begin = wave_start(k, T, W), t_end = wave_start(k + 1, T, W);
   if (t_begin >= t_end) return;
@@ -577,7 +620,7 @@ __global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_stream_kerne
     c0r.h = (int)(r / c0r.n);
     c0r.v = (int)(r - (int64_t)c0r.h * c0r.n);
   }
-  c0r.w = make_walk(ctx[c0r.b], a.window, a.n_sink, kBS);
+  c0r.w = seq_walk(a, ctx[c0r.b]);
   auto advance = [&](Cursor& c) {
     if (++c.v < c.n) return;
     c.v = 0;
@@ -588,7 +631,7 @@ __global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_stream_kerne
     } while (c.b < B && uni(s_pref[c.b + 1]) == uni(s_pref[c.b]));
     if (c.b < B) {
       c.n = uni(s_pref[c.b + 1]) - uni(s_pref[c.b]);
-      c.w = make_walk(ctx[c.b], a.window, a.n_sink, kBS);
+      c.w = seq_walk(a, ctx[c.b]);
     }
   };
 
@@ -635,7 +678,7 @@ __global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_stream_kerne
           // a piece of it to workspace slot k + u.
           const float l_tot = st.total();
           if (ln < G) {
-            if (frag_first == 0 && unit_end) {
+            if (frag_first == 0 && unit_end && !a.fused) {
               const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
               E* o = static_cast<E*>(a.out) + ((int64_t)cc.b * Hq + cc.h * G + ln) * D + 4 * lq;
 #pragma unroll
@@ -662,7 +705,7 @@ __global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_stream_kerne
   }
 }
 
-// Stream walk's merge: grid (kv head, sequence), 256 threads.  Writes zeros for
+// Stream walk's merge: grid (kv head, sequence, column split), 256 or 64 threads.  Writes zeros for
 // an empty unit, skips a unit one wave finished (written directly), and folds
 // the fragments of a split unit (slots k + u, k = first..last wave).
 template <int DT>
@@ -674,7 +717,8 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, 
   const int n = a.ws_pref[b + 1] - (int)pb;
   if (n == 0) {
     E* o = static_cast<E*>(a.out) + ((int64_t)b * Hkv * G + h * G) * D;
-    for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) o[idx] = Traits<DT>::from_float(0.f);
+    for (int idx = threadIdx.x + blockIdx.z * blockDim.x; idx < G * D; idx += blockDim.x * gridDim.z)
+      o[idx] = Traits<DT>::from_float(0.f);
     return;
   }
   const int64_t T = (int64_t)Hkv * a.ws_pref[a.batch];
@@ -686,7 +730,82 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, 
   merge_slots<DT>(a, b, h, (int)(k1 - k0 + 1), D, [&](int i) { return base + i; });
 }
 
-enum Stage { kFull = 0, kPartial = 1, kMerge = 2 };
+// Fused append's merge: grid (kv head, sequence, column split), 256 or 64 threads.  Scores the new
+// token (position L-1) of every query head of the unit from k_new, folds it as one
+// more log-sum-exp term (weight exp2(s - M), value row v_new) with the pool walk's
+// partials of positions < L-1, writes `out`, and stores the new K/V rows into the
+// token's slot for later steps.  Every unit is merged here (the fused walk never
+// writes `out` directly).
+template <int DT>
+__global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a, int D) {
+  using Tr = Traits<DT>;
+  using E = typename Tr::E;
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int Hkv = a.Hkv, G = a.G, Hq = Hkv * G;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int L = a.ctx[b];
+  E* out = static_cast<E*>(a.out) + ((int64_t)b * Hq + h * G) * D;
+  const int nwaves = blockDim.x >> 6;
+  const int idx0 = threadIdx.x + blockIdx.z * blockDim.x, stride = blockDim.x * gridDim.z;
+  if (L <= 0) {
+    for (int idx = idx0; idx < G * D; idx += stride) out[idx] = Tr::from_float(0.f);
+    return;
+  }
+  // The new token's slot; an invalid page id there means it is neither stored nor
+  // attended (as ivakv_append skips the slot and the walk masks the row).
+  const int pos = L - 1, lp = pos / kBS, row = pos % kBS;
+  int64_t page = lp < a.max_blocks ? (int64_t)a.bt[(int64_t)b * a.max_blocks + lp] : -1;
+  const bool new_ok = page >= 0 && page < a.num_pages;
+  const E* kn = static_cast<const E*>(a.k_new) + ((int64_t)b * Hkv + h) * D;
+  const E* vn = static_cast<const E*>(a.v_new) + ((int64_t)b * Hkv + h) * D;
+  const E* qb = static_cast<const E*>(a.q) + ((int64_t)b * Hq + h * G) * D;
+  __shared__ float s_new[16];
+  for (int g = wave; g < G; g += nwaves) {
+    float dot = 0.f;
+    for (int d = lane; d < D; d += 64) dot += (float)qb[g * D + d] * (float)kn[d];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o);
+    if (lane == 0) s_new[g] = dot * a.scale_log2;
+  }
+  __syncthreads();
+
+  // Partials of the pool walk (positions < L-1): fragments k0..k1 of the unit.
+  const int64_t pb = a.ws_pref[b];
+  const int n = a.ws_pref[b + 1] - (int)pb;
+  int64_t k0 = 0, nf = 0;
+  if (n > 0) {
+    const int64_t T = (int64_t)Hkv * a.ws_pref[a.batch];
+    const int64_t W = stream_waves(T, a.n_waves);
+    const int64_t first_tile = (int64_t)Hkv * pb + (int64_t)h * n;
+    k0 = wave_of(first_tile, T, W);
+    nf = wave_of(first_tile + n - 1, T, W) - k0 + 1;
+  }
+  const int64_t base = k0 + (int64_t)b * Hkv + h;
+  for (int idx = idx0; idx < G * D; idx += stride) {
+    const int g = idx / D;
+    float M = new_ok ? s_new[g] : kNegInf;
+    float L_sum = new_ok ? 1.f : 0.f;
+    float O = new_ok ? (float)vn[idx - g * D] : 0.f;
+    fold_slots(a, g, idx, D, (int)nf, [&](int i) { return base + i; }, M, L_sum, O);
+    out[idx] = Tr::from_float(L_sum > 0.f ? O / L_sum : 0.f);
+  }
+
+  // Append: the new rows go to the slot of position L-1.
+  {
+    if (new_ok && blockIdx.z == 0) {
+      constexpr int X = 16 / (int)sizeof(E);
+      const int64_t tile = (page * Hkv + h) * (int64_t)D * kBS;
+      E* kp = static_cast<E*>(const_cast<void*>(a.k_pool)) + tile;
+      E* vp = static_cast<E*>(const_cast<void*>(a.v_pool)) + tile;
+      for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        kp[((d / X) * kBS + row) * X + d % X] = kn[d];
+        vp[d * kBS + row] = vn[d];
+      }
+    }
+  }
+}
+
+enum Stage { kFull = 0, kPartial = 1, kMerge = 2, kFused = 3 };
 
 struct Plan {
   bool stream;
@@ -713,6 +832,9 @@ int make_plan(const char* name, Stage stage, int batch, int num_q_heads, int num
   if (n_sink < 0) return fail(IVAKV_E_ARG, "%s: negative n_sink", name);
   plan->G = G;
   plan->stream = partition_pages <= 0 && batch <= kMaxStreamBatch;
+  if (stage == kFused && !plan->stream)
+    return fail(IVAKV_E_SHAPE, "%s: the fused append runs on the default walk: partition_pages "
+                "must be <= 0 and batch <= %d", name, kMaxStreamBatch);
   const size_t units = (size_t)batch * num_kv_heads;
   if (plan->stream) {
     plan->part_pages = 0;
@@ -758,13 +880,22 @@ void launch_stream(Stage stage, int D, dim3 grid, size_t smem, hipStream_t strea
                    const DecodeArgs& a) {
   if (stage != kMerge) {
     switch (D) {
-      case 64: decode_stream_kernel<DT, 64><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
-      case 128: decode_stream_kernel<DT, 128><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
-      default: decode_stream_kernel<DT, 256><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+      case 64: decode_stream_kernel<DT, 64><<<grid, kStreamThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+      case 128: decode_stream_kernel<DT, 128><<<grid, kStreamThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+      default: decode_stream_kernel<DT, 256><<<grid, kStreamThreads, smem, stream>>>(a, a.bt, a.ctx); break;
     }
   }
-  if (stage != kPartial)
-    decode_stream_merge_kernel<DT><<<dim3((unsigned)a.Hkv, (unsigned)a.batch), 256, 0, stream>>>(a, D);
+  // Merge grid: one workgroup per (kv head, sequence) when there are enough of them
+  // to fill the CUs; otherwise smaller workgroups split each unit's output columns
+  // (grid z), so a batch of few, long sequences still merges on many CUs.
+  const int units = a.Hkv * a.batch;
+  const int threads = units >= 256 ? 256 : 64;
+  const int zsplit = units >= 256 ? 1 : cdiv(a.G * D, threads);
+  const dim3 mgrid((unsigned)a.Hkv, (unsigned)a.batch, (unsigned)zsplit);
+  if (stage == kFused)
+    decode_fused_merge_kernel<DT><<<mgrid, threads, 0, stream>>>(a, D);
+  else if (stage != kPartial)
+    decode_stream_merge_kernel<DT><<<mgrid, threads, 0, stream>>>(a, D);
 }
 
 // Workgroups of the stream walk on the current device: what its CUs hold at
@@ -774,9 +905,9 @@ int stream_workgroups() {
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       cus <= 0)
-    cus = kMaxStreamWaves / (kWaves * kStreamWGsPerCU);
-  const int wgs = cus * kStreamWGsPerCU;
-  return wgs < kMaxStreamWaves / kWaves ? wgs : kMaxStreamWaves / kWaves;
+    cus = kMaxStreamWaves / (kStreamWaves * kStreamWGs);
+  const int wgs = cus * kStreamWGs;
+  return wgs < kMaxStreamWaves / kStreamWaves ? wgs : kMaxStreamWaves / kStreamWaves;
 }
 
 int decode_entry(Stage stage, const char* name, const void* q, const void* k_pool,
@@ -784,7 +915,7 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
                  void* out, void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
                  int num_kv_heads, int head_dim, int block_size, int max_blocks, int num_pages,
                  float scale, int window, int n_sink, int partition_pages, int dtype,
-                 hipStream_t stream) {
+                 hipStream_t stream, const void* k_new = nullptr, const void* v_new = nullptr) {
   if (dtype_size(dtype) == 0) return fail(IVAKV_E_DTYPE, "%s: unknown dtype code %d", name, dtype);
   Plan plan;
   int st = make_plan(name, stage, batch, num_q_heads, num_kv_heads, head_dim, block_size,
@@ -795,6 +926,8 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
   if (num_pages < 1) return fail(IVAKV_E_ARG, "%s: num_pages must be >= 1", name);
   if (!q || !k_pool || !v_pool || !context_lens || !out || (max_blocks > 0 && !block_tables))
     return fail(IVAKV_E_ARG, "%s: null pointer argument", name);
+  if (stage == kFused && (!k_new || !v_new))
+    return fail(IVAKV_E_ARG, "%s: null k_new / v_new", name);
   if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out))
     return fail(IVAKV_E_ARG, "%s: q, pools and out must be 16-byte aligned", name);
   if (plan.ws_bytes > 0 && (!workspace || workspace_bytes < plan.ws_bytes || !aligned16(workspace)))
@@ -827,11 +960,14 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
   a.part_pages = plan.part_pages;
   a.n_parts_max = plan.n_parts_max;
   a.n_waves = 0;
+  a.k_new = k_new;
+  a.v_new = v_new;
+  a.fused = stage == kFused;
 
   if (plan.stream) {
     const int wgs = stream_workgroups();
-    a.n_waves = wgs * kWaves;
-    const size_t smem = sizeof(int32_t) * ((size_t)batch + 1 + kThreads);
+    a.n_waves = wgs * kStreamWaves;
+    const size_t smem = sizeof(int32_t) * ((size_t)batch + 1 + kStreamThreads);
     switch (dtype) {
       case IVAKV_F16: launch_stream<IVAKV_F16>(stage, head_dim, dim3((unsigned)wgs), smem, stream, a); break;
       case IVAKV_BF16: launch_stream<IVAKV_BF16>(stage, head_dim, dim3((unsigned)wgs), smem, stream, a); break;
@@ -900,3 +1036,16 @@ extern "C" int ivakv_decode_workspace_size(int batch, int num_q_heads, int num_k
 IVAKV_DECODE_ENTRY(ivakv_decode_attn, kFull)
 IVAKV_DECODE_ENTRY(ivakv_decode_attn_partial, kPartial)
 IVAKV_DECODE_ENTRY(ivakv_decode_attn_merge, kMerge)
+
+extern "C" int ivakv_decode_append_attn(const void* q, const void* k_new, const void* v_new,
+                                        void* k_pool, void* v_pool, const int32_t* block_tables,
+                                        const int32_t* context_lens, void* out, void* workspace,
+                                        size_t workspace_bytes, int batch, int num_q_heads,
+                                        int num_kv_heads, int head_dim, int block_size,
+                                        int max_blocks, int num_pages, float scale, int window,
+                                        int n_sink, int dtype, hipStream_t stream) {
+  return decode_entry(kFused, "ivakv_decode_append_attn", q, k_pool, v_pool, block_tables,
+                      context_lens, out, workspace, workspace_bytes, batch, num_q_heads,
+                      num_kv_heads, head_dim, block_size, max_blocks, num_pages, scale, window,
+                      n_sink, 0, dtype, stream, k_new, v_new);
+}

@@ -13,9 +13,10 @@ meaning, return contracts, errors) for the path ``Transformer.forward(kv_cache=.
   AttentionTorch      src/core/attention.py:17-148 on a contiguous KVCache (torch.cat
                       append), the reference's default backend.
   PagedAttention      same constructor/forward contract (:37-45,110) on a PagedKVCache:
-                      append with ivakv_append, single-token decode with
-                      ivakv_decode_attn, multi-token (prefill) steps by gathering the
-                      context (ivakv_gather) and evaluating the masked attention.
+                      single-token decode appends and attends in one op
+                      (ivakv_decode_append_attn); multi-token (prefill) steps append
+                      with ivakv_append, gather the context (ivakv_gather) and evaluate
+                      the masked attention.
   KVCache             src/core/rope_kv.py:71-137 (contiguous cache of AttentionTorch).
   RMSNorm / FFN       src/core/norms.py:14-36, src/core/ffn.py:16-64 (needed by the
                       dense decoder of config C3; not part of the paged hot path).
@@ -48,7 +49,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .ops import kv_gather, paged_decode_attention
+from .ops import kv_gather, paged_decode_append_attention
 from .paged_cache import PagedKVCache
 
 
@@ -283,10 +284,11 @@ class PagedAttention(_AttentionBase):
 
     forward(x, attention_mask, kv_cache, rope_state, sliding_window, sink_cfg)
     -> (out, kv_cache), as AttentionTorch (src/core/attention.py:37-45,110); the
-    cache is mutated in place and returned.  New K/V rows are appended with
-    ivakv_append.  A single-token step (decode) runs ivakv_decode_attn over the
-    pages; a multi-token step (prefill / chunked prefill) gathers the context with
-    ivakv_gather and evaluates the causal attention of the new tokens on it.
+    cache is mutated in place and returned.  A single-token step (decode) appends the
+    new row and attends over the pages in one op (ivakv_decode_append_attn); a
+    multi-token step (prefill / chunked prefill) appends with ivakv_append, gathers
+    the context with ivakv_gather and evaluates the causal attention of the new
+    tokens on it.
     Without a cache the new tokens attend to themselves (causal).
     """
 
@@ -312,12 +314,16 @@ class PagedAttention(_AttentionBase):
                           allowed[None, None])
             out = out.transpose(1, 2)
         else:
-            view = kv_cache.layer_step(k.contiguous(), v.contiguous())
-            if s == 1 and self.causal:
-                o = paged_decode_attention(q.view(b, self.n_heads, self.head_dim).contiguous(),
-                                           view.k_pool, view.v_pool, view.block_tables,
-                                           view.context_lens, scale=self.scale,
-                                           window=window or 0, n_sink=n_sink if window else 0)
+            decode = s == 1 and self.causal
+            view = kv_cache.layer_step(k.contiguous(), v.contiguous(), append=not decode)
+            if decode:
+                # append + attend in one op: the new row lands at position L-1 of each page
+                # table and is scored straight from k / v (ivakv_decode_append_attn)
+                o = paged_decode_append_attention(
+                    q.view(b, self.n_heads, self.head_dim), k.view(b, self.n_kv_heads, self.head_dim),
+                    v.view(b, self.n_kv_heads, self.head_dim), view.k_pool, view.v_pool,
+                    view.block_tables, view.context_lens, scale=self.scale, window=window or 0,
+                    n_sink=n_sink if window else 0)
                 out = o.view(b, 1, self.n_heads, self.head_dim)
             else:
                 total = view.start + s

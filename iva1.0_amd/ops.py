@@ -246,6 +246,61 @@ def paged_decode_attention_merge(q, k_pool, v_pool, block_tables, context_lens, 
                    scale, window, n_sink, partition_pages, out, workspace)
 
 
+def paged_decode_append_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                                  k_pool: torch.Tensor, v_pool: torch.Tensor,
+                                  block_tables: torch.Tensor, context_lens: torch.Tensor,
+                                  scale: Optional[float] = None, window: Optional[int] = None,
+                                  n_sink: int = 0, out: Optional[torch.Tensor] = None,
+                                  workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One decode step in one op: the new token of sequence b sits at position
+    ``context_lens[b] - 1``; its rows ``k_new[b], v_new[b]`` ([B, Hkv, D]) are written to
+    that position's slot and attended together with the earlier positions in the pages.
+    Same result as :func:`kv_append` of those rows followed by
+    :func:`paged_decode_attention`, in two launches (no separate append kernel).
+
+    Fuses the append and the scoring of ``AttentionTorch.forward`` with a cache
+    (src/core/attention.py:61-102).
+    """
+    dev = _require_gpu(q, k_new, v_new, k_pool, v_pool, block_tables, context_lens)
+    num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
+    if q.dim() != 3 or q.shape[2] != head_dim:
+        raise ValueError(f"q must be [B, Hq, {head_dim}]; got {tuple(q.shape)}")
+    batch, hq, _ = q.shape
+    for name, t in (("k_new", k_new), ("v_new", v_new)):
+        if tuple(t.shape) != (batch, hkv, head_dim):
+            raise ValueError(f"{name} must be [{batch}, {hkv}, {head_dim}]; got {tuple(t.shape)}")
+    for t in (q, k_new, v_new):
+        if t.dtype != k_pool.dtype:
+            raise TypeError(f"dtype {t.dtype} != pool dtype {k_pool.dtype}")
+    block_tables = _i32(block_tables, "block_tables")
+    context_lens = _i32(context_lens, "context_lens").reshape(-1)
+    if block_tables.dim() != 2 or block_tables.shape[0] != batch or context_lens.numel() != batch:
+        raise ValueError("block_tables must be [B, max_blocks] and context_lens [B]")
+    max_blocks = block_tables.shape[1]
+    q, k_new, v_new = q.contiguous(), k_new.contiguous(), v_new.contiguous()
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    window = int(window) if window else 0
+    n_sink = int(n_sink) if n_sink else 0
+    if out is None:
+        out = torch.empty_like(q)
+    elif tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped and typed like q")
+    nbytes = decode_workspace_bytes(batch, hq, hkv, head_dim, bs, max_blocks, window, n_sink)
+    if workspace is None:
+        workspace = _workspace(dev, nbytes)
+    elif workspace.numel() * workspace.element_size() < nbytes:
+        raise ValueError(f"workspace has {workspace.numel() * workspace.element_size()} bytes, "
+                         f"{nbytes} needed")
+    _abi.call("ivakv_decode_append_attn", q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
+              k_pool.data_ptr(), v_pool.data_ptr(), block_tables.data_ptr(),
+              context_lens.data_ptr(), out.data_ptr(), workspace.data_ptr(),
+              workspace.numel() * workspace.element_size(), batch, hq, hkv, head_dim, bs,
+              max_blocks, num_pages, float(scale), window, n_sink, dtype_code(q.dtype),
+              _stream(dev))
+    return out
+
+
 def kv_ops(kv_cache: torch.Tensor, indices: torch.Tensor, values: Optional[torch.Tensor] = None,
            operation: str = "gather") -> torch.Tensor:
     """Index gather / scatter along the sequence axis of a contiguous ``[B, H, S, D]`` cache.

@@ -507,11 +507,14 @@ class PagedKVCache:
         ctx.add_(1)
         return st["slot"], st["bt"], ctx, self.seq_len, 1
 
-    def layer_step(self, k_rows: torch.Tensor, v_rows: torch.Tensor) -> LayerView:
+    def layer_step(self, k_rows: torch.Tensor, v_rows: torch.Tensor,
+                   append: bool = True) -> LayerView:
         """Appends the new tokens' K/V rows ([B, T, Hkv, D]) of the layer at the cursor and
         returns that layer's view.  The first call of a forward allocates the pages of
         the T new tokens of every sequence; the call of the last layer advances
-        ``seq_len`` by T and rewinds the cursor."""
+        ``seq_len`` by T and rewinds the cursor.  ``append=False`` allocates and
+        advances the same way but leaves writing the rows to the caller (the fused
+        decode op writes them itself)."""
         b, t = k_rows.shape[0], k_rows.shape[1]
         if b != self.batch_size:
             raise ValueError(f"batch {b} != cache batch {self.batch_size}")
@@ -530,9 +533,10 @@ class PagedKVCache:
                                "the same tokens")
         slot_dev, bt, ctx, start, t = self._view
         layer = self._cursor
-        kv_append(k_rows.reshape(b * t, self.n_heads, self.head_dim),
-                  v_rows.reshape(b * t, self.n_heads, self.head_dim),
-                  self.pool.k_pools[layer], self.pool.v_pools[layer], slot_dev)
+        if append:
+            kv_append(k_rows.reshape(b * t, self.n_heads, self.head_dim),
+                      v_rows.reshape(b * t, self.n_heads, self.head_dim),
+                      self.pool.k_pools[layer], self.pool.v_pools[layer], slot_dev)
         view = LayerView(layer, self.pool.k_pools[layer], self.pool.v_pools[layer], slot_dev, bt,
                          ctx, start, t)
         self._cursor += 1

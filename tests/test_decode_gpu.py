@@ -331,3 +331,42 @@ def test_stream_matches_partitioned(iva, dev):
     a = iva.paged_decode_attention(*args)
     b = iva.paged_decode_attention(*args, partition_pages=24)
     assert (a.float() - b.float()).abs().max().item() <= 2e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("window,n_sink", [(0, 0), (40, 4)])
+def test_fused_append_attention(iva, dev, dtype, window, n_sink):
+    """ivakv_decode_append_attn == ivakv_append of the new rows + ivakv_decode_attn: the
+    pools afterwards are bit-identical, the output matches the fp64 oracle (tolerance of
+    the dtype).  Lengths cover a new token alone (L=1), an empty sequence (L=0), a new
+    token opening a page (L=17) and closing one (L=16), and an invalid page id under
+    the new token (neither stored nor attended)."""
+    lengths = [1, 0, 17, 16, 300, 1000, 2]
+    hkv, g, d = 2, 4, 128
+    base = iva.workloads.decode_batch(lengths, hkv * g, hkv, d, dtype, seed=40 + window,
+                                      scale=0.5, extra_pages=4)
+    lay = base["layout"]
+    bt = lay.block_tables.clone()
+    bt[6, 0] = -3                      # the new token of sequence 6 sits on an invalid page
+    lay = iva.workloads.PagedLayout(lay.lengths, bt, lay.num_pages)
+    gen = torch.Generator().manual_seed(7)
+    k_new = (torch.randn(len(lengths), hkv, d, generator=gen) * 0.5).to(dtype)
+    v_new = (torch.randn(len(lengths), hkv, d, generator=gen) * 0.5).to(dtype)
+    # reference: append then decode
+    kp_a, vp_a = base["k_pool"].clone().to(dev), base["v_pool"].clone().to(dev)
+    slots = torch.tensor([int(bt[b, (n - 1) // 16]) * 16 + (n - 1) % 16 if n > 0 and bt[b, (n - 1) // 16] >= 0
+                          else -1 for b, n in enumerate(lengths)], dtype=torch.int32)
+    iva.kv_append(k_new.to(dev), v_new.to(dev), kp_a, vp_a, slots.to(dev))
+    # fused
+    kp_f, vp_f = base["k_pool"].clone().to(dev), base["v_pool"].clone().to(dev)
+    out = iva.paged_decode_append_attention(base["q"].to(dev), k_new.to(dev), v_new.to(dev), kp_f,
+                                            vp_f, lay.block_tables.to(dev), lay.context_lens.to(dev),
+                                            window=window, n_sink=n_sink)
+    ti = {torch.float32: torch.int32}.get(dtype, torch.int16)
+    assert torch.equal(kp_a.view(ti), kp_f.view(ti)) and torch.equal(vp_a.view(ti), vp_f.view(ti))
+    d_after = dict(base, k_pool=kp_a.cpu(), v_pool=vp_a.cpu())
+    ref = oracle_out(d_after, window=window, n_sink=n_sink, layout=lay)
+    assert_close(out, ref, dtype, what=f"fused {dtype} w{window}")
+    unfused = iva.paged_decode_attention(base["q"].to(dev), kp_a, vp_a, lay.block_tables.to(dev),
+                                         lay.context_lens.to(dev), window=window, n_sink=n_sink)
+    assert_close(unfused, ref, dtype, what="append + decode")
