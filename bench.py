@@ -404,8 +404,8 @@ def main():
                     fn(sets[r % len(sets)])
             return g
 
-        step_graph = None if args.eager else make_graph(step, len(sets))
         per_graph = len(sets) * max(1, 20 // len(sets))
+        step_graph = None if args.eager else make_graph(step, per_graph)
         walk_graph = None if args.eager else make_graph(walk, per_graph)
         attn_graph = None if args.eager else make_graph(attention, per_graph)
 
@@ -414,10 +414,10 @@ def main():
                 for i in range(n):
                     step(sets[i % len(sets)])
             else:
-                for _ in range(n // len(sets)):
+                for _ in range(n // per_graph):
                     step_graph.replay()
-                for i in range(n % len(sets)):
-                    step(sets[i])
+                for i in range(n % per_graph):
+                    step(sets[i % len(sets)])
 
         run_steps(args.warmup)
         torch.cuda.synchronize(dev)

@@ -62,7 +62,7 @@ constexpr int kPageBufs = IVAKV_PAGE_BUFS;  // register page buffers per wave (r
 // the largest batch whose page prefix fits the workgroup's LDS.
 constexpr int kStreamWGsPerCU = IVAKV_STREAM_WGS_PER_CU;
 #ifndef IVAKV_STREAM_WAVES
-#define IVAKV_STREAM_WAVES 8
+#define IVAKV_STREAM_WAVES 4
 #endif
 // Stream walk workgroup: kStreamWaves independent waves (one per SIMD pair per CU
 // at two waves per SIMD).  Fewer, larger workgroups dispatch faster and run the
@@ -527,9 +527,16 @@ __device__ inline int64_t stream_waves(int64_t T, int n_waves) {
   const int64_t want = (T + kMinTilesPerWave - 1) / kMinTilesPerWave;
   return want < n_waves ? (want > 0 ? want : 1) : n_waves;
 }
-// Wave k of W owns flat tiles [k*T/W, (k+1)*T/W); wave_of(t) inverts that.
-__device__ inline int64_t wave_start(int64_t k, int64_t T, int64_t W) { return k * T / W; }
-__device__ inline int64_t wave_of(int64_t t, int64_t T, int64_t W) { return ((t + 1) * W - 1) / T; }
+
+// Split of T flat tiles over W waves: wave k owns tiles [start(k), start(k + 1))
+// with start(k) = k * T / W; owner(t) inverts it (the k with start(k) <= t <
+// start(k + 1)).
+struct WaveSplit {
+  int64_t T, W;
+  __device__ WaveSplit(int64_t T_, const DecodeArgs& a) : T(T_), W(stream_waves(T_, a.n_waves)) {}
+  __device__ int64_t start(int64_t k) const { return k * T / W; }
+  __device__ int64_t owner(int64_t t) const { return ((t + 1) * W - 1) / T; }
+};
 
 // Flat tile order: sequence-major, then kv head, then effective page.  Unit
 // (b, h) = tiles [Hkv*pref[b] + h*n_b, ... + n_b) with n_b = pref[b+1] - pref[b].
@@ -589,10 +596,10 @@ __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kern
 
   const int64_t T = (int64_t)Hkv * uni(s_pref[B]);
   if (T == 0) return;
-  const int64_t W = stream_waves(T, a.n_waves);
+  const WaveSplit split(T, a);
   const int64_t k = (int64_t)blockIdx.x * kStreamWaves + __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (k >= W) return;
-  const int64_t t_begin = wave_start(k, T, W), t_end = wave_start(k + 1, T, W);
+  if (k >= split.W) return;
+  const int64_t t_begin = split.start(k), t_end = split.start(k + 1);
   if (t_begin >= t_end) return;
   const int count = (int)(t_end - t_begin);
 
@@ -722,9 +729,9 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, 
     return;
   }
   const int64_t T = (int64_t)Hkv * a.ws_pref[a.batch];
-  const int64_t W = stream_waves(T, a.n_waves);
+  const WaveSplit split(T, a);
   const int64_t first_tile = (int64_t)Hkv * pb + (int64_t)h * n;
-  const int64_t k0 = wave_of(first_tile, T, W), k1 = wave_of(first_tile + n - 1, T, W);
+  const int64_t k0 = split.owner(first_tile), k1 = split.owner(first_tile + n - 1);
   if (k0 == k1) return;
   const int64_t base = k0 + (int64_t)b * Hkv + h;
   merge_slots<DT>(a, b, h, (int)(k1 - k0 + 1), D, [&](int i) { return base + i; });
@@ -742,10 +749,9 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a, i
   using E = typename Tr::E;
   const int h = blockIdx.x, b = blockIdx.y;
   const int Hkv = a.Hkv, G = a.G, Hq = Hkv * G;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int L = a.ctx[b];
   E* out = static_cast<E*>(a.out) + ((int64_t)b * Hq + h * G) * D;
-  const int nwaves = blockDim.x >> 6;
   const int idx0 = threadIdx.x + blockIdx.z * blockDim.x, stride = blockDim.x * gridDim.z;
   if (L <= 0) {
     for (int idx = idx0; idx < G * D; idx += stride) out[idx] = Tr::from_float(0.f);
@@ -759,15 +765,6 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a, i
   const E* kn = static_cast<const E*>(a.k_new) + ((int64_t)b * Hkv + h) * D;
   const E* vn = static_cast<const E*>(a.v_new) + ((int64_t)b * Hkv + h) * D;
   const E* qb = static_cast<const E*>(a.q) + ((int64_t)b * Hq + h * G) * D;
-  __shared__ float s_new[16];
-  for (int g = wave; g < G; g += nwaves) {
-    float dot = 0.f;
-    for (int d = lane; d < D; d += 64) dot += (float)qb[g * D + d] * (float)kn[d];
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o);
-    if (lane == 0) s_new[g] = dot * a.scale_log2;
-  }
-  __syncthreads();
 
   // Partials of the pool walk (positions < L-1): fragments k0..k1 of the unit.
   const int64_t pb = a.ws_pref[b];
@@ -775,18 +772,31 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a, i
   int64_t k0 = 0, nf = 0;
   if (n > 0) {
     const int64_t T = (int64_t)Hkv * a.ws_pref[a.batch];
-    const int64_t W = stream_waves(T, a.n_waves);
+    const WaveSplit split(T, a);
     const int64_t first_tile = (int64_t)Hkv * pb + (int64_t)h * n;
-    k0 = wave_of(first_tile, T, W);
-    nf = wave_of(first_tile + n - 1, T, W) - k0 + 1;
+    k0 = split.owner(first_tile);
+    nf = split.owner(first_tile + n - 1) - k0 + 1;
   }
   const int64_t base = k0 + (int64_t)b * Hkv + h;
+  // The partials are folded first (their loads wait only on the prefix), then
+  // the new token.  D is a multiple of 64, so the 64 outputs of a wave share one
+  // query head g, and the wave scores the new token for g with a lane-strided
+  // dot product.
   for (int idx = idx0; idx < G * D; idx += stride) {
     const int g = idx / D;
-    float M = new_ok ? s_new[g] : kNegInf;
-    float L_sum = new_ok ? 1.f : 0.f;
-    float O = new_ok ? (float)vn[idx - g * D] : 0.f;
+    float M = kNegInf, L_sum = 0.f, O = 0.f;
     fold_slots(a, g, idx, D, (int)nf, [&](int i) { return base + i; }, M, L_sum, O);
+    float dot = 0.f;
+    for (int d = lane; d < D; d += 64) dot += (float)qb[g * D + d] * (float)kn[d];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o);
+    if (new_ok) {
+      const float sc = dot * a.scale_log2;
+      const float mn = fmaxf(M, sc);
+      const float f = exp2_fast(M - mn), w = exp2_fast(sc - mn);
+      L_sum = L_sum * f + w;
+      O = O * f + (float)vn[idx - g * D] * w;
+    }
     out[idx] = Tr::from_float(L_sum > 0.f ? O / L_sum : 0.f);
   }
 
@@ -885,12 +895,13 @@ void launch_stream(Stage stage, int D, dim3 grid, size_t smem, hipStream_t strea
       default: decode_stream_kernel<DT, 256><<<grid, kStreamThreads, smem, stream>>>(a, a.bt, a.ctx); break;
     }
   }
-  // Merge grid: one workgroup per (kv head, sequence) when there are enough of them
-  // to fill the CUs; otherwise smaller workgroups split each unit's output columns
-  // (grid z), so a batch of few, long sequences still merges on many CUs.
+  // Merge grid: (kv head, sequence, column split) with one output element per
+  // thread, so every partial load of a unit is in flight at once; 64-thread
+  // workgroups when units are fewer than CUs, so few, long sequences still merge
+  // on many CUs.
   const int units = a.Hkv * a.batch;
   const int threads = units >= 256 ? 256 : 64;
-  const int zsplit = units >= 256 ? 1 : cdiv(a.G * D, threads);
+  const int zsplit = cdiv(a.G * D, threads);
   const dim3 mgrid((unsigned)a.Hkv, (unsigned)a.batch, (unsigned)zsplit);
   if (stage == kFused)
     decode_fused_merge_kernel<DT><<<mgrid, threads, 0, stream>>>(a, D);
