@@ -184,6 +184,28 @@ int ivakv_decode_append_attn(const void* q, const void* k_new, const void* v_new
                              hipStream_t stream);
 
 /*
+ * Paged multi-query causal attention (prefill / chunked prefill).  Sequence b owns
+ * query rows query_start[b] .. query_start[b+1]-1 of q ([n_tok][Hq][D] dense, pool
+ * dtype); with n_b rows and context length L = context_lens[b], row i sits at
+ * absolute position p = L - n_b + i and its K/V must already be in the pages
+ * (ivakv_append first).  Row i of query head h attends to the keys j <= p of
+ * kv head h / (Hq/Hkv) with j > p - window (all when window <= 0) or j < n_sink,
+ * over valid page ids; out has q's shape.  A row at a negative position (n_b > L)
+ * and a row that sees no key are written as zeros.  max_query_len must be >= every
+ * n_b (rows past it are not computed).  query_start is int32 [batch+1], non-
+ * decreasing.  Geometry: head_dim in {64, 128, 256}, block_size 16, any GQA group.
+ * Replaces: AttentionTorch.forward with a cache and seq_len > 1
+ * (src/core/attention.py:61-102): torch.cat of the chunk's K/V, scores, causal /
+ * window / sink masks (attention.py:79-93,115-148) at absolute positions, softmax, PV.
+ */
+int ivakv_prefill_attn(const void* q, const void* k_pool, const void* v_pool,
+                       const int32_t* block_tables, const int32_t* context_lens,
+                       const int32_t* query_start, void* out, int batch, int num_q_heads,
+                       int num_kv_heads, int head_dim, int block_size, int max_blocks,
+                       int num_pages, int max_query_len, float scale, int window, int n_sink,
+                       int dtype, hipStream_t stream);
+
+/*
  * Index gather on a contiguous-layout cache kv = [batch][n_heads][seq_len][D]
  * with element strides (s_b, s_h, s_s, s_d):
  *   out[b, h, j, :] = kv[b, h, indices[j], :]      out = [B][H][n_idx][D] dense

@@ -19,6 +19,7 @@ from .ops import (
     paged_decode_attention,
     paged_decode_attention_merge,
     paged_decode_attention_partial,
+    paged_prefill_attention,
     pool_geometry,
     pool_shapes,
 )
@@ -43,6 +44,7 @@ __all__ = [
     "paged_decode_attention",
     "paged_decode_attention_merge",
     "paged_decode_attention_partial",
+    "paged_prefill_attention",
     "pool_geometry",
     "pool_shapes",
 ]

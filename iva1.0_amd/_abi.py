@@ -73,6 +73,15 @@ SIGNATURES = {
         c_int, c_int, c_int,                   # window, n_sink, dtype
         c_void_p,                              # stream
     ]),
+    "ivakv_prefill_attn": (c_int, [
+        c_void_p, c_void_p, c_void_p,          # q, k_pool, v_pool
+        c_void_p, c_void_p, c_void_p,          # block_tables, context_lens, query_start
+        c_void_p,                              # out
+        c_int, c_int, c_int, c_int,            # batch, num_q_heads, num_kv_heads, head_dim
+        c_int, c_int, c_int, c_int, c_float,   # block_size, max_blocks, num_pages, max_query_len, scale
+        c_int, c_int, c_int,                   # window, n_sink, dtype
+        c_void_p,                              # stream
+    ]),
     "ivakv_index_gather": (c_int, [
         c_void_p, c_int64, c_int64, c_int64, c_int64,  # kv + strides
         c_void_p, c_int,                             # indices, n_idx

@@ -26,26 +26,11 @@
 //     stream walk's page prefix in LDS): grid (kv head, sequence, partition) of 4-wave
 //     workgroups; a partition of part_pages pages is split over the 4 waves
 //     and merged through LDS, then across partitions by decode_merge_kernel.
-#include "ivakv_internal.h"
+#include "ivakv_tile.h"
 
 namespace ivakv {
 namespace {
 
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-struct alignas(16) Chunk16 {
-  uint32_t w[4];
-};
-struct alignas(8) Chunk8 {
-  uint32_t w[2];
-};
-
-constexpr int kBS = 16;       // rows per page == MFMA tile edge
 constexpr int kWaves = 4;     // wavefronts per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kDefaultPartitionPages = 32;
@@ -73,7 +58,6 @@ constexpr int kStreamWGs = kStreamWGsPerCU * kWaves / kStreamWaves;  // per CU
 constexpr int kMaxStreamWaves = 4096;
 constexpr int kMinTilesPerWave = 4;
 constexpr int kMaxStreamBatch = 8192;
-constexpr float kNegInf = -__builtin_huge_valf();
 
 struct DecodeArgs {
   const void* q;
@@ -96,112 +80,7 @@ struct DecodeArgs {
   int fused;
 };
 
-// Zeroes the 16-bit V elements of rows that are not attended.  A row outside
-// the context (tail of the last page, an invalid page) may hold any bits, and
-// 0 * NaN would poison the PV accumulator even though its weight is zero.
-__device__ inline void mask_rows16(Chunk8& v, const bool vis[4]) {
-  v.w[0] &= (vis[0] ? 0x0000FFFFu : 0u) | (vis[1] ? 0xFFFF0000u : 0u);
-  v.w[1] &= (vis[2] ? 0x0000FFFFu : 0u) | (vis[3] ? 0xFFFF0000u : 0u);
-}
 
-template <int DT>
-struct Traits;
-
-template <>
-struct Traits<IVAKV_F16> {
-  using E = _Float16;
-  using VChunk = Chunk8;  // 4 consecutive rows of one dim
-  using PVec = f16x4;
-  static __device__ inline f32x4 qk(const Chunk16& k, const Chunk16& q, f32x4 s) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, k),
-                                                  __builtin_bit_cast(f16x8, q), s, 0, 0, 0);
-  }
-  static __device__ inline PVec pack_p(const float p[4]) {
-    return PVec{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
-  }
-  static __device__ inline f32x4 pv(const VChunk& v, const PVec& p, f32x4 acc) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, v), p, acc, 0, 0, 0);
-  }
-  static __device__ inline E from_float(float x) { return (E)x; }
-  static __device__ inline void mask_rows(VChunk& v, const bool vis[4]) { mask_rows16(v, vis); }
-};
-
-// bf16 keeps only 8 significant bits, so P is carried as a hi + lo pair of bf16
-// values (p = hi + lo to ~16 bits) and the PV product takes two MFMAs.
-struct BF16Pair {
-  i16x4 hi, lo;
-};
-
-template <>
-struct Traits<IVAKV_BF16> {
-  using E = __bf16;
-  using VChunk = Chunk8;
-  using PVec = BF16Pair;
-  static __device__ inline f32x4 qk(const Chunk16& k, const Chunk16& q, f32x4 s) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, k),
-                                                   __builtin_bit_cast(bf16x8, q), s, 0, 0, 0);
-  }
-  static __device__ inline PVec pack_p(const float p[4]) {
-    bf16x4 hi{(__bf16)p[0], (__bf16)p[1], (__bf16)p[2], (__bf16)p[3]};
-    bf16x4 lo{(__bf16)(p[0] - (float)hi[0]), (__bf16)(p[1] - (float)hi[1]),
-              (__bf16)(p[2] - (float)hi[2]), (__bf16)(p[3] - (float)hi[3])};
-    return PVec{__builtin_bit_cast(i16x4, hi), __builtin_bit_cast(i16x4, lo)};
-  }
-  static __device__ inline f32x4 pv(const VChunk& v, const PVec& p, f32x4 acc) {
-    const i16x4 va = __builtin_bit_cast(i16x4, v);
-    acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, p.hi, acc, 0, 0, 0);
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, p.lo, acc, 0, 0, 0);
-  }
-  static __device__ inline E from_float(float x) { return (E)x; }
-  static __device__ inline void mask_rows(VChunk& v, const bool vis[4]) { mask_rows16(v, vis); }
-};
-
-template <>
-struct Traits<IVAKV_F32> {
-  using E = float;
-  using VChunk = Chunk16;
-  using PVec = f32x4;
-  static __device__ inline f32x4 qk(const Chunk16& k, const Chunk16& q, f32x4 s) {
-    const f32x4 kf = __builtin_bit_cast(f32x4, k);
-    const f32x4 qf = __builtin_bit_cast(f32x4, q);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[i], qf[i], s, 0, 0, 0);
-    return s;
-  }
-  static __device__ inline PVec pack_p(const float p[4]) { return PVec{p[0], p[1], p[2], p[3]}; }
-  static __device__ inline f32x4 pv(const VChunk& v, const PVec& p, f32x4 acc) {
-    const f32x4 vf = __builtin_bit_cast(f32x4, v);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[r], p[r], acc, 0, 0, 0);
-    return acc;
-  }
-  static __device__ inline E from_float(float x) { return x; }
-  static __device__ inline void mask_rows(VChunk& v, const bool vis[4]) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) v.w[r] = vis[r] ? v.w[r] : 0u;
-  }
-};
-
-__device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// A value every lane of the wave holds (e.g. read from LDS at a uniform
-// address), made visibly uniform so addresses built from it stay scalar: block
-// table and context reads then use the scalar cache and lgkmcnt, and never make
-// the wave wait for its outstanding page loads.
-__device__ inline int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
-
-__device__ inline int logical_page(const PageWalk& w, int v) {
-  return v < w.sink_pages ? v : w.win_first + (v - w.sink_pages);
-}
-
-// Effective pages of a walk whose logical page lies inside the block table
-// (logical_page is increasing, so these are the first ones).  Positions on the
-// pages past the table are never attended, so the walks stop there.
-__device__ inline int table_pages(const PageWalk& w, int max_blocks) {
-  const int sink = min(w.sink_pages, max_blocks);
-  const int win = min(cdiv(w.L, kBS), max_blocks) - w.win_first;
-  return sink + (win > 0 ? win : 0);
-}
 
 // Page walk of a sequence of context length L as the stream walk reads it: with the
 // fused append the pool covers positions < L - 1 only (the window and sinks are

@@ -58,6 +58,21 @@ __host__ __device__ inline PageWalk make_walk(int L, int window, int n_sink, int
   return w;
 }
 
+// Logical page of effective page v.
+__host__ __device__ inline int logical_page(const PageWalk& w, int v) {
+  return v < w.sink_pages ? v : w.win_first + (v - w.sink_pages);
+}
+
+// Effective pages of a walk whose logical page lies inside the block table
+// (logical_page is increasing, so these are the first ones).  Positions on the
+// pages past the table are never attended, so the walks stop there.
+__host__ __device__ inline int table_pages(const PageWalk& w, int max_blocks, int bs = 16) {
+  const int sink = w.sink_pages < max_blocks ? w.sink_pages : max_blocks;
+  const int n_log = cdiv(w.L, bs);
+  const int win = (n_log < max_blocks ? n_log : max_blocks) - w.win_first;
+  return sink + (win > 0 ? win : 0);
+}
+
 // Largest n_eff any sequence can have for a block table of max_blocks columns.
 inline int max_effective_pages(int max_blocks, int window, int n_sink, int bs) {
   if (window <= 0) return max_blocks;

@@ -1,0 +1,162 @@
+// Register-level tile types shared by the attention kernels (gfx950): 16-byte
+// and 8-byte load chunks, MFMA operand vectors, and per-dtype MFMA wrappers.
+// Internal to libivakv; every translation unit gets its own copy.
+#pragma once
+
+#include "ivakv_internal.h"
+
+namespace ivakv {
+namespace {
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct alignas(16) Chunk16 {
+  uint32_t w[4];
+};
+struct alignas(8) Chunk8 {
+  uint32_t w[2];
+};
+
+constexpr int kBS = 16;       // rows per page == MFMA tile edge
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// Zeroes the 16-bit V elements of rows that are not attended.  A row outside
+// the context (tail of the last page, an invalid page) may hold any bits, and
+// 0 * NaN would poison the PV accumulator even though its weight is zero.
+__device__ inline void mask_rows16(Chunk8& v, const bool vis[4]) {
+  v.w[0] &= (vis[0] ? 0x0000FFFFu : 0u) | (vis[1] ? 0xFFFF0000u : 0u);
+  v.w[1] &= (vis[2] ? 0x0000FFFFu : 0u) | (vis[3] ? 0xFFFF0000u : 0u);
+}
+
+template <int DT>
+struct Traits;
+
+template <>
+struct Traits<IVAKV_F16> {
+  using E = _Float16;
+  using VChunk = Chunk8;  // 4 consecutive rows of one dim
+  using PVec = f16x4;
+  static __device__ inline f32x4 qk(const Chunk16& k, const Chunk16& q, f32x4 s) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, k),
+                                                  __builtin_bit_cast(f16x8, q), s, 0, 0, 0);
+  }
+  static __device__ inline PVec pack_p(const float p[4]) {
+    return PVec{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+  }
+  static __device__ inline f32x4 pv(const VChunk& v, const PVec& p, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, v), p, acc, 0, 0, 0);
+  }
+  // 32-key PV: k-slot 8*lq + r is row 4*lq + r of page A (r < 4) or of page B.
+  using P8 = f16x8;
+  static __device__ inline P8 pack_p8(const float pa[4], const float pb[4]) {
+    return P8{(_Float16)pa[0], (_Float16)pa[1], (_Float16)pa[2], (_Float16)pa[3],
+              (_Float16)pb[0], (_Float16)pb[1], (_Float16)pb[2], (_Float16)pb[3]};
+  }
+  static __device__ inline f32x4 pv32(const VChunk& va, const VChunk& vb, const P8& p, f32x4 acc) {
+    const Chunk16 v{{va.w[0], va.w[1], vb.w[0], vb.w[1]}};
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, v), p, acc, 0, 0, 0);
+  }
+  static __device__ inline E from_float(float x) { return (E)x; }
+  static __device__ inline void mask_rows(VChunk& v, const bool vis[4]) { mask_rows16(v, vis); }
+};
+
+// bf16 keeps only 8 significant bits, so P is carried as a hi + lo pair of bf16
+// values (p = hi + lo to ~16 bits) and the PV product takes two MFMAs.
+struct BF16Pair {
+  i16x4 hi, lo;
+};
+
+template <>
+struct Traits<IVAKV_BF16> {
+  using E = __bf16;
+  using VChunk = Chunk8;
+  using PVec = BF16Pair;
+  static __device__ inline f32x4 qk(const Chunk16& k, const Chunk16& q, f32x4 s) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, k),
+                                                   __builtin_bit_cast(bf16x8, q), s, 0, 0, 0);
+  }
+  static __device__ inline PVec pack_p(const float p[4]) {
+    bf16x4 hi{(__bf16)p[0], (__bf16)p[1], (__bf16)p[2], (__bf16)p[3]};
+    bf16x4 lo{(__bf16)(p[0] - (float)hi[0]), (__bf16)(p[1] - (float)hi[1]),
+              (__bf16)(p[2] - (float)hi[2]), (__bf16)(p[3] - (float)hi[3])};
+    return PVec{__builtin_bit_cast(i16x4, hi), __builtin_bit_cast(i16x4, lo)};
+  }
+  static __device__ inline f32x4 pv(const VChunk& v, const PVec& p, f32x4 acc) {
+    const i16x4 va = __builtin_bit_cast(i16x4, v);
+    acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, p.hi, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, p.lo, acc, 0, 0, 0);
+  }
+  struct P8 {
+    bf16x8 hi, lo;
+  };
+  static __device__ inline P8 pack_p8(const float pa[4], const float pb[4]) {
+    P8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r.hi[i] = (__bf16)pa[i];
+      r.hi[4 + i] = (__bf16)pb[i];
+      r.lo[i] = (__bf16)(pa[i] - (float)r.hi[i]);
+      r.lo[4 + i] = (__bf16)(pb[i] - (float)r.hi[4 + i]);
+    }
+    return r;
+  }
+  static __device__ inline f32x4 pv32(const VChunk& va, const VChunk& vb, const P8& p, f32x4 acc) {
+    const Chunk16 v{{va.w[0], va.w[1], vb.w[0], vb.w[1]}};
+    const bf16x8 vv = __builtin_bit_cast(bf16x8, v);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, p.hi, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, p.lo, acc, 0, 0, 0);
+  }
+  static __device__ inline E from_float(float x) { return (E)x; }
+  static __device__ inline void mask_rows(VChunk& v, const bool vis[4]) { mask_rows16(v, vis); }
+};
+
+template <>
+struct Traits<IVAKV_F32> {
+  using E = float;
+  using VChunk = Chunk16;
+  using PVec = f32x4;
+  static __device__ inline f32x4 qk(const Chunk16& k, const Chunk16& q, f32x4 s) {
+    const f32x4 kf = __builtin_bit_cast(f32x4, k);
+    const f32x4 qf = __builtin_bit_cast(f32x4, q);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[i], qf[i], s, 0, 0, 0);
+    return s;
+  }
+  static __device__ inline PVec pack_p(const float p[4]) { return PVec{p[0], p[1], p[2], p[3]}; }
+  static __device__ inline f32x4 pv(const VChunk& v, const PVec& p, f32x4 acc) {
+    const f32x4 vf = __builtin_bit_cast(f32x4, v);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[r], p[r], acc, 0, 0, 0);
+    return acc;
+  }
+  struct P8 {
+    f32x4 a, b;
+  };
+  static __device__ inline P8 pack_p8(const float pa[4], const float pb[4]) {
+    return P8{pack_p(pa), pack_p(pb)};
+  }
+  static __device__ inline f32x4 pv32(const VChunk& va, const VChunk& vb, const P8& p, f32x4 acc) {
+    return pv(vb, p.b, pv(va, p.a, acc));
+  }
+  static __device__ inline E from_float(float x) { return x; }
+  static __device__ inline void mask_rows(VChunk& v, const bool vis[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v.w[r] = vis[r] ? v.w[r] : 0u;
+  }
+};
+
+__device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// A value every lane of the wave holds (e.g. read from LDS at a uniform
+// address), made visibly uniform so addresses built from it stay scalar: block
+// table and context reads then use the scalar cache and lgkmcnt, and never make
+// the wave wait for its outstanding page loads.
+__device__ inline int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+}  // namespace
+}  // namespace ivakv

@@ -301,6 +301,60 @@ def paged_decode_append_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: t
     return out
 
 
+def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                            block_tables: torch.Tensor, context_lens: torch.Tensor,
+                            query_start: torch.Tensor, scale: Optional[float] = None,
+                            window: Optional[int] = None, n_sink: int = 0,
+                            max_query_len: Optional[int] = None,
+                            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal multi-query attention of chunks of new tokens over paged K/V.
+
+    ``q`` is ``[n_tok, Hq, D]``; the rows of sequence b are
+    ``query_start[b] .. query_start[b+1]-1`` (int32 ``[B+1]``) and sit at absolute
+    positions ``L - n_b .. L - 1`` with ``L = context_lens[b]``.  Their K/V must already
+    be in the pages (:func:`kv_append`).  Row at position p attends to keys ``j <= p``
+    within the window (``j > p - window``) or among the first ``n_sink`` positions.
+    Returns ``[n_tok, Hq, D]``.  ``max_query_len`` (>= every chunk length) sizes the
+    launch; when omitted it is read back from ``query_start`` (a device sync).
+
+    Replaces ``AttentionTorch.forward`` with a cache and ``seq_len > 1``
+    (src/core/attention.py:61-102), with the causal, window and sink masks
+    (attention.py:79-93,115-148) taken at absolute positions.
+    """
+    dev = _require_gpu(q, k_pool, v_pool, block_tables, context_lens, query_start)
+    num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
+    if q.dim() != 3 or q.shape[2] != head_dim:
+        raise ValueError(f"q must be [n_tok, Hq, {head_dim}]; got {tuple(q.shape)}")
+    if q.dtype != k_pool.dtype:
+        raise TypeError(f"q dtype {q.dtype} != pool dtype {k_pool.dtype}")
+    hq = q.shape[1]
+    block_tables = _i32(block_tables, "block_tables")
+    context_lens = _i32(context_lens, "context_lens").reshape(-1)
+    query_start = _i32(query_start, "query_start").reshape(-1)
+    batch = context_lens.numel()
+    if block_tables.dim() != 2 or block_tables.shape[0] != batch:
+        raise ValueError("block_tables must be [B, max_blocks] with B == len(context_lens)")
+    if query_start.numel() != batch + 1:
+        raise ValueError(f"query_start must have B+1 = {batch + 1} entries")
+    if max_query_len is None:
+        max_query_len = int((query_start[1:] - query_start[:-1]).max().item()) if batch else 0
+    q = q.contiguous()
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    window = int(window) if window else 0
+    n_sink = int(n_sink) if n_sink else 0
+    if out is None:
+        out = torch.empty_like(q)
+    elif tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor shaped and typed like q")
+    _abi.call("ivakv_prefill_attn", q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+              block_tables.data_ptr(), context_lens.data_ptr(), query_start.data_ptr(),
+              out.data_ptr(), batch, hq, hkv, head_dim, bs, block_tables.shape[1], num_pages,
+              int(max_query_len), float(scale), window, n_sink, dtype_code(q.dtype),
+              _stream(dev))
+    return out
+
+
 def kv_ops(kv_cache: torch.Tensor, indices: torch.Tensor, values: Optional[torch.Tensor] = None,
            operation: str = "gather") -> torch.Tensor:
     """Index gather / scatter along the sequence axis of a contiguous ``[B, H, S, D]`` cache.

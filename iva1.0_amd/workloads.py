@@ -110,6 +110,22 @@ def decode_batch(lengths: List[int], num_q_heads: int, num_kv_heads: int, head_d
                 num_q_heads=num_q_heads, num_kv_heads=num_kv_heads, head_dim=head_dim)
 
 
+def prefill_batch(lengths: List[int], chunks: List[int], num_q_heads: int, num_kv_heads: int,
+                  head_dim: int, dtype: torch.dtype, seed: int, device=None,
+                  scale: float = 1.0) -> dict:
+    """Prefill inputs: pools holding ``lengths[b]`` positions of sequence b (the chunk
+    already appended) and query rows for its last ``chunks[b]`` positions, packed as
+    ``q [sum(chunks), Hq, D]`` with ``query_start`` (int32 ``[B+1]``)."""
+    d = decode_batch(lengths, num_q_heads, num_kv_heads, head_dim, dtype, seed, device, scale)
+    qs = [0]
+    for n in chunks:
+        qs.append(qs[-1] + int(n))
+    d["q"] = _randn((qs[-1], num_q_heads, head_dim), seed * 1000 + 14, device, dtype, scale)
+    d["query_start"] = torch.tensor(qs, dtype=torch.int32)
+    d["chunks"] = [int(n) for n in chunks]
+    return d
+
+
 def c2_lengths(seed: int, batch: int = 32, lo: int = 512, hi: int = 4096) -> List[int]:
     gen = torch.Generator().manual_seed(seed)
     return torch.randint(lo, hi + 1, (batch,), generator=gen).tolist()

@@ -5,7 +5,7 @@ Restates, on the paged layout, the semantics of the reference's
   - AttentionTorch cache append (torch.cat) src/core/attention.py:61-63
   - KVCache.get_slice                      src/core/rope_kv.py:136-137
   - AttentionTorch math                    src/core/attention.py:77-102
-  - masks (window / sink)                  src/core/attention.py:115-148
+  - masks (causal / window / sink)         src/core/attention.py:79-93,115-148
   - kv_gather / kv_scatter kernels         src/kernels_t/kv_ops_triton.py:18-65,129
 
 Layout (X = 16 // itemsize, BS = block size):
@@ -208,6 +208,70 @@ def decode_attention_loops(q, k_rows, v_rows, ctx_lens, scale: float, window: in
             z = sum(e)
             for i in range(d):
                 out[b][h][i] = sum(e[n] * float(v_rows[b][kh][j][i]) for n, j in enumerate(keys)) / z
+    return out
+
+
+def visible_at(pos: int, length: int, window: int = 0, n_sink: int = 0) -> np.ndarray:
+    """Keys 0..length-1 a query at absolute position ``pos`` attends to: causal
+    (``j <= pos``, attention.py:79-81 at absolute positions), within the sliding window
+    ``j > pos - window`` (attention.py:124-127) or an attention sink ``j < n_sink``
+    (attention.py:131-148, as a union).  For ``pos = length - 1`` this is
+    :func:`visible`."""
+    j = np.arange(max(length, 0))
+    vis = j <= pos
+    if window and window > 0:
+        vis &= (j > pos - window) | (j < n_sink)
+    return vis
+
+
+def prefill_attention(q: np.ndarray, k_pool: np.ndarray, v_pool: np.ndarray,
+                      block_tables: np.ndarray, ctx_lens: np.ndarray, query_start: np.ndarray,
+                      scale: Optional[float] = None, window: int = 0,
+                      n_sink: int = 0) -> np.ndarray:
+    """fp64 causal multi-query attention over paged K/V (prefill / chunked prefill).
+
+    ``q`` is ``[n_tok, Hq, D]``; sequence b owns rows ``query_start[b] ..
+    query_start[b+1]-1``, which sit at absolute positions ``L - n_b .. L - 1``
+    (``L = ctx_lens[b]``, the chunk already appended: attention.py:61-63 then
+    :77-102).  Each row is ``softmax(q k^T * scale) v`` over :func:`visible_at` keys
+    on valid page ids; rows at negative positions or with no visible key are zero."""
+    q = np.asarray(q, dtype=np.float64)
+    n_tok, hq, d = q.shape
+    hkv = k_pool.shape[1]
+    g = hq // hkv
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    ctx = np.asarray(ctx_lens, dtype=np.int64).reshape(-1)
+    qs = np.asarray(query_start, dtype=np.int64).reshape(-1)
+    bt = np.asarray(block_tables, dtype=np.int64)
+    num_pages, bs = k_pool.shape[0], k_pool.shape[3]
+    max_len = int(max(ctx.max(initial=0), 0))
+    k_all, v_all = gather(k_pool, v_pool, bt, ctx, out_len=max_len)
+    out = np.zeros((n_tok, hq, d), dtype=np.float64)
+    for b in range(len(ctx)):
+        length, s0, s1 = int(ctx[b]), int(qs[b]), int(qs[b + 1])
+        n = s1 - s0
+        if length <= 0 or n <= 0:
+            continue
+        page_idx = np.arange(length) // bs
+        pid = np.full(length, -1, dtype=np.int64)
+        in_table = page_idx < bt.shape[1]
+        pid[in_table] = bt[b, page_idx[in_table]]
+        valid = (pid >= 0) & (pid < num_pages)
+        k = expand_gqa(k_all[b, :, :length].astype(np.float64), g)  # [Hq, L, D]
+        v = expand_gqa(v_all[b, :, :length].astype(np.float64), g)
+        for i in range(n):
+            pos = length - n + i
+            if pos < 0:
+                continue
+            vis = visible_at(pos, length, window, n_sink) & valid
+            if not vis.any():
+                continue
+            scores = np.einsum("hd,had->ha", q[s0 + i], k[:, vis]) * scale
+            scores -= scores.max(axis=1, keepdims=True)
+            p = np.exp(scores)
+            p /= p.sum(axis=1, keepdims=True)
+            out[s0 + i] = np.einsum("ha,had->hd", p, v[:, vis])
     return out
 
 

@@ -323,3 +323,121 @@ def test_index_ops_vs_torch():
     ref[:, :, torch.from_numpy(uniq)] = torch.from_numpy(vals)
     assert np.array_equal(out, ref.numpy())
     assert not np.shares_memory(out, kv)
+
+
+# ------------------------------------------------------------------ prefill attention
+
+def prefill_case(seed, lengths, chunks, hq, hkv, d, bs=16):
+    """Pools holding `lengths` tokens per sequence; query rows for the last chunks[b]
+    positions of each sequence (chunks[b] may exceed the length: negative positions)."""
+    c = attn_case(seed, lengths, hq, hkv, d, bs)
+    rng = np.random.default_rng(seed + 2000)
+    qs = np.concatenate([[0], np.cumsum(chunks)]).astype(np.int64)
+    c.update(qp=rng.standard_normal((int(qs[-1]), hq, d)), qs=qs, chunks=list(chunks))
+    return c
+
+
+def _call_pf(fn, c, **kw):
+    return fn(c["qp"], c["kp"], c["vp"], c["bt"], c["ctx"], c["qs"], **kw)
+
+
+def check_pf_rows_are_decodes(fn):
+    """Row i of sequence b at position p equals the (separately pinned) decode oracle
+    with context length p + 1 on the same pages; negative positions give zero rows."""
+    ok = True
+    for lengths, chunks, hq, hkv, d, window, sink in (
+            ([20, 37, 5], [20, 9, 1], 4, 2, 8, 0, 0),
+            ([50, 33], [17, 33], 6, 2, 8, 7, 3),
+            ([3, 40], [5, 0], 2, 2, 4, 0, 0),
+            ([64], [64], 4, 1, 8, 16, 1)):
+        c = prefill_case(31, lengths, chunks, hq, hkv, d)
+        c["bt"][-1, 1] = -1 if c["bt"].shape[1] > 1 else c["bt"][-1, 1]  # an invalid page
+        got = _call_pf(fn, c, window=window, n_sink=sink)
+        for b, (length, n) in enumerate(zip(lengths, chunks)):
+            for i in range(n):
+                row = int(c["qs"][b]) + i
+                pos = length - n + i
+                if pos < 0:
+                    ok &= not got[row].any()
+                    continue
+                exp = orc.decode_attention(c["qp"][row][None], c["kp"], c["vp"], c["bt"][b:b + 1],
+                                           np.array([pos + 1]), window=window, n_sink=sink)
+                ok &= np.allclose(got[row], exp[0], atol=1e-12)
+    return ok
+
+
+def check_pf_sdpa_causal(fn):
+    """Full prefill (chunk = whole sequence) vs torch SDPA in fp64: is_causal for plain
+    causal attention; otherwise an explicit mask, the reference's window loop
+    (attention.py:120-127) united with the first n_sink positions."""
+    ok = True
+    for length, hq, hkv, d, window, sink in ((45, 4, 2, 8, 0, 0), (60, 6, 3, 8, 9, 2),
+                                             (33, 2, 1, 16, 1, 1)):
+        c = prefill_case(37, [length], [length], hq, hkv, d)
+        got = _call_pf(fn, c, window=window, n_sink=sink)
+        ko, vo = orc.gather(c["kp"], c["vp"], c["bt"], c["ctx"])
+        g = hq // hkv
+        k = torch.from_numpy(ko[0, :, :length]).double().repeat_interleave(g, 0)
+        v = torch.from_numpy(vo[0, :, :length]).double().repeat_interleave(g, 0)
+        q = torch.from_numpy(c["qp"]).double().transpose(0, 1)  # [Hq, L, D]
+        if not window:
+            o = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        else:
+            mask = torch.zeros(length, length, dtype=torch.bool)
+            for i in range(length):                          # attention.py:120-127
+                mask[i, max(0, i - window + 1):i + 1] = True
+                mask[i, :min(sink, i + 1)] = True            # sinks, never past i
+            o = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+        ok &= np.allclose(got, o.transpose(0, 1).numpy(), atol=1e-10)
+    return ok
+
+
+def check_pf_chunking(fn):
+    """A sequence prefilled in two chunks gives the rows of one full prefill."""
+    c = prefill_case(41, [70], [70], 4, 2, 8)
+    full = _call_pf(fn, c, window=20, n_sink=2)
+    c1 = dict(c, ctx=np.array([33]), qs=np.array([0, 33]), qp=c["qp"][:33])
+    c2 = dict(c, ctx=np.array([70]), qs=np.array([0, 37]), qp=c["qp"][33:])
+    parts = np.concatenate([_call_pf(fn, c1, window=20, n_sink=2),
+                            _call_pf(fn, c2, window=20, n_sink=2)])
+    return np.allclose(full, parts, atol=1e-12)
+
+
+PF_CHECKS = [check_pf_rows_are_decodes, check_pf_sdpa_causal, check_pf_chunking]
+
+
+@pytest.mark.parametrize("check", PF_CHECKS, ids=lambda f: f.__name__)
+def test_prefill_oracle_pins(check):
+    assert check(orc.prefill_attention)
+
+
+def _pf_mutant_relative(q, kp, vp, bt, ctx, qs, scale=None, window=0, n_sink=0):
+    # the reference's literal torch.tril over [S, S_cache + S] (attention.py:79-81):
+    # chunk row i sees keys 0..i, ignoring the cached prefix
+    ctx = np.asarray(ctx)
+    out = np.zeros(q.shape)
+    for b in range(len(ctx)):
+        for i in range(int(qs[b + 1] - qs[b])):
+            out[qs[b] + i] = orc.decode_attention(q[qs[b] + i][None], kp, vp, bt[b:b + 1],
+                                                  np.array([i + 1]), scale, window, n_sink)[0]
+    return out
+
+
+@pytest.mark.parametrize("mutant", ["relative_positions", "window_off_by_one", "sinks_dropped",
+                                    "gqa_tile", "causal_inclusive_off"])
+def test_prefill_planted_mistakes_are_caught(monkeypatch, mutant):
+    fn = orc.prefill_attention
+    real = orc.visible_at
+    if mutant == "relative_positions":
+        fn = _pf_mutant_relative
+    elif mutant == "window_off_by_one":
+        monkeypatch.setattr(orc, "visible_at",
+                            lambda p, n, w=0, s=0: real(p, n, w + 1 if w else w, s))
+    elif mutant == "sinks_dropped":
+        monkeypatch.setattr(orc, "visible_at", lambda p, n, w=0, s=0: real(p, n, w, 0))
+    elif mutant == "gqa_tile":
+        monkeypatch.setattr(orc, "expand_gqa", lambda x, g: np.concatenate([x] * g, axis=0))
+    elif mutant == "causal_inclusive_off":
+        monkeypatch.setattr(orc, "visible_at", lambda p, n, w=0, s=0: real(p - 1, n, w, s))
+    results = [check(fn) for check in PF_CHECKS]
+    assert not all(results), f"planted mistake {mutant} passed every prefill pin check"

@@ -1,0 +1,139 @@
+"""Paged prefill / chunked-prefill attention on the GPU vs the fp64 CPU oracle.
+
+Tolerance (north star): max |out - exact| <= 2e-3 for fp16/bf16 and 1e-5 for fp32,
+plus one half-ulp of the output dtype times |exact| (output rounding), as for decode.
+Cases cover full prefill (chunk = whole sequence), chunks after a cached prefix,
+single-row chunks, empty chunks, chunks longer than the context (rows at negative
+positions are zero), invalid page ids, NaN bits past the context, GQA groups 1, 3, 4
+and 8, windows with sinks, and head_dim 64 / 128 / 256.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_kv as orc
+
+pytestmark = pytest.mark.gpu
+
+ATOL = {torch.float16: 2e-3, torch.bfloat16: 2e-3, torch.float32: 1e-5}
+OUT_ULP = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8, torch.float32: 2.0 ** -23}
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def assert_close(out, ref, dtype, what=""):
+    err = np.abs(to_np(out) - ref)
+    bound = ATOL[dtype] + OUT_ULP[dtype] * np.abs(ref)
+    worst = float((err - bound).max()) if err.size else -1.0
+    assert worst <= 0.0, f"{what}: max abs err {err.max():.3e} exceeds bound (excess {worst:.3e})"
+
+
+def make(iva, lengths, chunks, hq, hkv, d, dtype, seed=0):
+    return iva.workloads.prefill_batch(lengths, chunks, hq, hkv, d, dtype, seed=seed,
+                                       scale=d ** -0.5)
+
+
+def oracle(c, bt=None, window=0, n_sink=0):
+    lay = c["layout"]
+    return orc.prefill_attention(to_np(c["q"]), to_np(c["k_pool"]), to_np(c["v_pool"]),
+                                 (lay.block_tables if bt is None else bt).numpy(),
+                                 lay.context_lens.numpy(), c["query_start"].numpy(),
+                                 window=window, n_sink=n_sink)
+
+
+def run(iva, dev, c, bt=None, **kw):
+    lay = c["layout"]
+    return iva.paged_prefill_attention(c["q"].to(dev), c["k_pool"].to(dev), c["v_pool"].to(dev),
+                                       (lay.block_tables if bt is None else bt).to(dev),
+                                       lay.context_lens.to(dev), c["query_start"].to(dev), **kw)
+
+
+CASES = {
+    "full": ([16, 100], [16, 100]),
+    "chunk_after_prefix": ([257, 70, 33], [64, 70, 1]),
+    "ragged": ([1, 17, 300, 45], [1, 17, 37, 0]),
+    "longer_than_context": ([5, 40], [9, 40]),
+}
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("case", list(CASES))
+@pytest.mark.parametrize("heads", [(8, 2), (4, 4), (12, 4), (16, 2)], ids=lambda h: f"{h[0]}q{h[1]}kv")
+def test_prefill_vs_oracle(iva, dev, dtype, case, heads):
+    lengths, chunks = CASES[case]
+    c = make(iva, lengths, chunks, heads[0], heads[1], 64, dtype, seed=3)
+    out = run(iva, dev, c)
+    assert_close(out, oracle(c), dtype, f"{case} {heads} {dtype}")
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("window,sink", [(0, 0), (50, 4), (16, 0), (1, 1)])
+def test_prefill_head_dims_windows(iva, dev, d, dtype, window, sink):
+    c = make(iva, [190, 77], [120, 77], 8, 2, d, dtype, seed=5)
+    out = run(iva, dev, c, window=window, n_sink=sink)
+    assert_close(out, oracle(c, window=window, n_sink=sink), dtype, f"D={d} w={window} s={sink}")
+
+
+def test_prefill_invalid_pages_and_nan_tail(iva, dev):
+    """Keys on an invalid page id are not attended; NaN bits past the context (the
+    tail of the last page) never reach the output."""
+    c = make(iva, [70, 41], [30, 41], 8, 2, 128, torch.float16, seed=7)
+    bt = c["layout"].block_tables.clone()
+    bt[0, 1] = -1
+    bt[1, 0] = c["layout"].num_pages + 5
+    last = int(c["layout"].block_tables[1, 2])  # length 41: rows 9..15 of page 2 are past it
+    c["k_pool"][last, :, :, 9:] = float("nan")
+    c["v_pool"][last, :, :, 9:] = float("nan")
+    out = run(iva, dev, c, bt=bt, window=24, n_sink=2)
+    assert torch.isfinite(out).all()
+    assert_close(out, oracle(c, bt=bt, window=24, n_sink=2), torch.float16, "invalid pages")
+
+
+def test_chunked_equals_full_and_last_row_equals_decode(iva, dev):
+    """Prefill in three chunks == one full prefill (both vs the oracle), and the last
+    row equals the decode kernel's output for that position."""
+    length, hq, hkv, d = 300, 8, 2, 128
+    c = make(iva, [length], [length], hq, hkv, d, torch.bfloat16, seed=9)
+    full = run(iva, dev, c, window=100, n_sink=4)
+    parts = []
+    for lo, hi in ((0, 45), (45, 200), (200, 300)):
+        cc = dict(c, q=c["q"][lo:hi], query_start=torch.tensor([0, hi - lo], dtype=torch.int32))
+        cc["layout"] = type(c["layout"])([hi], c["layout"].block_tables, c["layout"].num_pages)
+        parts.append(run(iva, dev, cc, window=100, n_sink=4))
+    chunked = torch.cat(parts)
+    ref = oracle(c, window=100, n_sink=4)
+    assert_close(full, ref, torch.bfloat16, "full")
+    assert_close(chunked, ref, torch.bfloat16, "chunked")
+    dec = iva.paged_decode_attention(c["q"][-1:].to(dev), c["k_pool"].to(dev), c["v_pool"].to(dev),
+                                     c["layout"].block_tables.to(dev),
+                                     c["layout"].context_lens.to(dev), window=100, n_sink=4)
+    assert (full[-1].float() - dec[0].float()).abs().max().item() <= 2e-3
+
+
+def test_prefill_c5_chunk_size(iva, dev):
+    """A 512-token chunk on top of a 1536-token prefix, 4 sequences, GQA 32/8, D 128, fp16."""
+    c = make(iva, [2048, 1700, 900, 512], [512, 512, 512, 512], 32, 8, 128, torch.float16, seed=11)
+    out = run(iva, dev, c)
+    ref = oracle(c)
+    err = np.abs(to_np(out) - ref).max()
+    assert err <= 2e-3, err
+
+
+def test_prefill_argument_errors(iva, dev):
+    c = make(iva, [20], [20], 4, 2, 64, torch.float16)
+    lay = c["layout"]
+    args = (c["q"].to(dev), c["k_pool"].to(dev), c["v_pool"].to(dev), lay.block_tables.to(dev),
+            lay.context_lens.to(dev))
+    with pytest.raises(TypeError, match="query_start"):
+        iva.paged_prefill_attention(*args, c["query_start"].to(dev).long())
+    with pytest.raises(ValueError, match="B\\+1"):
+        iva.paged_prefill_attention(*args, c["query_start"][:1].to(dev))
+    with pytest.raises(TypeError, match="dtype"):
+        iva.paged_prefill_attention(args[0].float(), *args[1:], c["query_start"].to(dev))
+    out = iva.paged_prefill_attention(*args, c["query_start"].to(dev), max_query_len=0)
+    assert out.shape == c["q"].shape  # nothing computed, no error
