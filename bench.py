@@ -72,9 +72,10 @@ def parse_args():
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="write the HBM traffic summary from two rocprofv3 --pmc runs")
     p.add_argument("--c5-steps", type=int, default=40, help="timed churn steps of --workload c5")
-    p.add_argument("--workload", choices=("c2", "c3", "c4", "c5"), default="c2",
+    p.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "prefill"), default="c2",
                    help="c2 (default): the contract line; c3 dense-decoder tokens/s, c4 "
-                        "long-context window+sinks decode, c5 ragged churn (informational lines)")
+                        "long-context window+sinks decode, c5 ragged churn, prefill: 512-token "
+                        "chunks over paged context (informational lines)")
     return p.parse_args()
 
 
@@ -325,6 +326,37 @@ def bench_c5(args, iva, torch, dev):
             "free_pages_left": pool.num_free_pages}
 
 
+def bench_prefill(args, iva, torch, dev):
+    """Chunked prefill at C5's chunk size: 16 sequences each appending a 512-token chunk
+    on top of 1536 cached positions (context 2048), GQA 32/8, D 128, fp16.  TFLOP/s on
+    algorithmic causal FLOPs: 4 * D * Hq * (visible keys) summed over query rows."""
+    wl = iva.workloads
+    measure = _timer(torch, dev)
+    lengths, chunks, hq, hkv, d = [2048] * 16, [512] * 16, 32, 8, 128
+    sets = []
+    for i in range(args.pools):
+        c = wl.prefill_batch(lengths, chunks, hq, hkv, d, torch.float16, seed=20 + i,
+                             device=dev, scale=d ** -0.5)
+        lay = c["layout"]
+        sets.append((c["q"], c["k_pool"], c["v_pool"], lay.block_tables.to(dev),
+                     lay.context_lens.to(dev), c["query_start"].to(dev), torch.empty_like(c["q"])))
+    run = lambda s: iva.paged_prefill_attention(s[0], s[1], s[2], s[3], s[4], s[5],
+                                                max_query_len=512, out=s[6])
+    for s in sets:
+        run(s)
+    reps = 40
+    t = measure(lambda: [run(sets[i % len(sets)]) for i in range(reps)]) / reps
+    flops = sum(4 * d * hq * (L - n + i + 1) for L, n in zip(lengths, chunks) for i in range(n))
+    tf = flops / t / 1e12
+    return {"metric": "paged chunked-prefill attention TFLOP/s", "workload": "prefill",
+            "value": round(tf, 1), "unit": "TFLOP/s", "dtype": "f16",
+            "config": {"sequences": 16, "chunk": 512, "context": 2048, "heads": "32/8",
+                       "head_dim": 128, "launch": "eager"},
+            "kernel_us": round(t * 1e6, 2), "algorithmic_flops": flops,
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0,
+                         "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4)}}
+
+
 def main():
     args = parse_args()
     if args.summarize_pmc:
@@ -344,7 +376,8 @@ def main():
     torch.cuda.set_device(dev)
     wl = iva.workloads
     if args.workload != "c2":
-        fn = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.workload]
+        fn = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
+              "prefill": bench_prefill}[args.workload]
         print(json.dumps(fn(args, iva, torch, dev)), flush=True)
         return
 

@@ -49,7 +49,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .ops import kv_gather, paged_decode_append_attention
+from .ops import kv_gather, paged_decode_append_attention, paged_prefill_attention
 from .paged_cache import PagedKVCache
 
 
@@ -286,9 +286,8 @@ class PagedAttention(_AttentionBase):
     -> (out, kv_cache), as AttentionTorch (src/core/attention.py:37-45,110); the
     cache is mutated in place and returned.  A single-token step (decode) appends the
     new row and attends over the pages in one op (ivakv_decode_append_attn); a
-    multi-token step (prefill / chunked prefill) appends with ivakv_append, gathers
-    the context with ivakv_gather and evaluates the causal attention of the new
-    tokens on it.
+    multi-token step (prefill / chunked prefill) appends with ivakv_append and runs
+    the causal attention of the new tokens over the pages (ivakv_prefill_attn).
     Without a cache the new tokens attend to themselves (causal).
     """
 
@@ -325,14 +324,19 @@ class PagedAttention(_AttentionBase):
                     view.block_tables, view.context_lens, scale=self.scale, window=window or 0,
                     n_sink=n_sink if window else 0)
                 out = o.view(b, 1, self.n_heads, self.head_dim)
+            elif self.causal:
+                # the chunk's rows sit at positions start .. start+s-1 of every sequence
+                qs = torch.arange(0, (b + 1) * s, s, dtype=torch.int32, device=x.device)
+                o = paged_prefill_attention(
+                    q.reshape(b * s, self.n_heads, self.head_dim), view.k_pool, view.v_pool,
+                    view.block_tables, view.context_lens, qs, scale=self.scale,
+                    window=window or 0, n_sink=n_sink if window else 0, max_query_len=s)
+                out = o.view(b, s, self.n_heads, self.head_dim)
             else:
                 total = view.start + s
                 kc, vc = kv_gather(view.k_pool, view.v_pool, view.block_tables,
                                    view.context_lens, out_len=total)
-                q_pos = torch.arange(view.start, total, device=x.device)
-                k_pos = torch.arange(total, device=x.device)
-                allowed = _visible(q_pos, k_pos, window, n_sink) if self.causal else \
-                    torch.ones(s, total, dtype=torch.bool, device=x.device)
+                allowed = torch.ones(s, total, dtype=torch.bool, device=x.device)
                 out = _attend(q.transpose(1, 2), kc, vc, self.scale, allowed[None, None])
                 out = out.transpose(1, 2)
         out = out.reshape(b, s, self.d_model)
