@@ -9,9 +9,11 @@
 // Work split: the query rows of one (sequence, kv head) are flattened
 // position-major over the G heads of the group, r = i*G + g, so a block of 16
 // rows spans as few positions as possible (tight causal ranges).  A workgroup
-// of 4 waves takes 4*16*NR consecutive rows; each wave walks the pages its own
-// rows can see, two pages (32 keys) at a time, through a 2-deep ring of
-// register buffers:
+// of W waves takes 32*W consecutive rows (two 16-row blocks per wave) and walks
+// the pages its rows can see two at a time (32 keys):
+// the pair's K and V tiles move HBM -> registers -> an LDS ring of two buffers
+// once per workgroup, and every wave reads them from LDS in MFMA operand order
+// (the pools' tile layout is kept in LDS):
 //   S^T[key][row]  = K_page(16 x D) . Q^T(D x 16)        v_mfma 16x16x32, per page
 //   O^T[dim][row] += V^T_pair(D x 32) . P^T(32 x 16)     v_mfma 16x16x32, per pair
 // The QK accumulator of lane l holds keys 4*(l/16)+r of row l%16 for each page
@@ -19,13 +21,15 @@
 // operand (slot 8*(l/16)+r = page A key 4*(l/16)+r, slot +4 = page B key), and
 // the V chunks of the two pages are paired the same way, so P never leaves
 // registers.  Online softmax in fp32, log2 domain, as in the decode kernel.
+// A wave skips pairs that lie entirely after its last row.
 #include "ivakv_tile.h"
 
 namespace ivakv {
 namespace {
 
-constexpr int kPfWaves = 4;
-constexpr int kPfThreads = 64 * kPfWaves;
+// Log2-domain headroom of the lazy row max: p = exp2(s - m) stays <= 2^8, well
+// inside fp16 / bf16 range.
+constexpr float kLazyMax = 8.f;
 
 struct PrefillArgs {
   const void* q;  // [n_tok, Hq, D], rows of sequence b at query_start[b] ..
@@ -35,53 +39,78 @@ struct PrefillArgs {
   int batch, Hkv, G, max_blocks, num_pages;
   float scale_log2;
   int window, n_sink;
+  int blocks_x;  // row-block workgroups per (sequence, kv head)
 };
 
-// Rows per workgroup of the kernel instance for head_dim D.
-template <int D>
+// Shape of the kernel instance.  fp16 / bf16 up to head_dim 128: 8 waves of
+// two 16-row blocks (two waves per SIMD, under 256 registers each, so one
+// wave's softmax overlaps the other's MFMAs) and two pairs in flight in
+// registers; fp32 and head_dim 256: 4 waves (one per SIMD, the accumulator in
+// AGPRs) and one pair in flight.
+template <int DT, int D>
 struct PrefillShape {
-  static constexpr int NR = D <= 128 ? 2 : 1;  // 16-row blocks per wave
+  static constexpr int kESize = DT == IVAKV_F32 ? 4 : 2;
+  static constexpr int kWaves = (DT == IVAKV_F32 || D == 256) ? 4 : 8;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int NR = 2;
+  static constexpr int kStages = kWaves == 8 ? 2 : 1;  // pairs in flight in registers
   static constexpr int kRowsWave = 16 * NR;
-  static constexpr int kRowsWG = kRowsWave * kPfWaves;
+  static constexpr int kRowsWG = kRowsWave * kWaves;
+  static constexpr int kPageElems = kBS * D;          // one K or V page tile
+  static constexpr int kPairElems = 4 * kPageElems;   // K_A, K_B, V_A, V_B
+  static constexpr size_t kLdsBytes = 2 * (size_t)kPairElems * kESize;
 };
 
 template <int DT, int D>
-__global__ __launch_bounds__(kPfThreads) void prefill_kernel(PrefillArgs a,
+__global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kernel(PrefillArgs a,
                                                              const int32_t* __restrict__ bt,
                                                              const int32_t* __restrict__ ctx,
                                                              const int32_t* __restrict__ qstart) {
   using Tr = Traits<DT>;
   using E = typename Tr::E;
   using VChunk = typename Tr::VChunk;
+  using S = PrefillShape<DT, D>;
   constexpr int X = 16 / (int)sizeof(E);
-  constexpr int KLD = D / X / 4;  // 16-byte K loads per lane per page
+  constexpr int KLD = D / X / 4;  // 16-byte K reads per lane per page
   constexpr int NB = D / 16;      // 16-dim blocks
-  constexpr int NR = PrefillShape<D>::NR;
+  constexpr int NR = S::NR;
   constexpr int64_t kTile = (int64_t)D * kBS;
+  extern __shared__ Chunk16 lds[];  // 2 x [K_A | K_B | V_A | V_B], global tile layout
 
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int lane = threadIdx.x & 63, ln = lane & 15, lq = lane >> 4;
-  const int wave = uni(threadIdx.x >> 6);
+  // XCD-aware order: the dispatcher deals workgroup ids round-robin to the 8
+  // XCDs, so unit u = (sequence, kv head) gets ids == u % 8 (mod 8) and all its
+  // row blocks run on one XCD, close in time: its pages come from HBM once per
+  // XCD and are L2 hits for the other row blocks.
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int unit = (slot / a.blocks_x) * 8 + xcd;
+  if (unit >= a.batch * a.Hkv) return;
+  const int b = unit / a.Hkv, h = unit % a.Hkv;
+  const int xb = slot % a.blocks_x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, ln = lane & 15, lq = lane >> 4;
+  const int wave = uni(tid >> 6);
   const int G = a.G, Hkv = a.Hkv, Hq = Hkv * G;
   const int q0 = qstart[b];
   const int n = qstart[b + 1] - q0;
   const int L = ctx[b];
   const int rows = n * G;
-  const int r_w = blockIdx.x * PrefillShape<D>::kRowsWG + wave * PrefillShape<D>::kRowsWave;
-  if (n <= 0 || r_w >= rows) return;
+  const int r_wg = xb * S::kRowsWG;
+  if (n <= 0 || r_wg >= rows) return;  // uniform over the workgroup
   const int first_pos = L - n;  // position of query row 0 of the chunk
-  const int r_last = min(r_w + PrefillShape<D>::kRowsWave, rows) - 1;
-  const int p_lo = max(first_pos + r_w / G, 0);
-  const int p_hi = first_pos + r_last / G;
 
-  // Keys any row of the wave can see: positions <= p_hi, from p_lo - window + 1
-  // on, plus the sinks.  (All rows before position 0: nothing to walk.)
+  // Keys any row of the workgroup can see: positions <= p_hi, from p_lo - window
+  // + 1 on, plus the sinks.  (All rows before position 0: nothing to walk.)
+  const int p_lo = max(first_pos + r_wg / G, 0);
+  const int p_hi = first_pos + (min(r_wg + S::kRowsWG, rows) - 1) / G;
   const PageWalk w = make_walk(p_hi >= 0 ? p_hi + 1 : 0, a.window > 0 ? a.window + (p_hi - p_lo) : 0,
                                a.n_sink, kBS);
   const int n_eff = table_pages(w, a.max_blocks, kBS);
+  const int n_pairs = (n_eff + 1) / 2;
 
-  // Query rows of the lane (column ln of each row block).  Rows past the chunk
-  // or before position 0 see no key; their loads are clamped to row 0.
+  // This wave's rows: the last position any of them has (pairs entirely past it
+  // are skipped) and, per lane, the position of row ln of each block.
+  const int r_w = r_wg + wave * S::kRowsWave;
+  const int wave_p_hi = r_w < rows ? first_pos + (min(r_w + S::kRowsWave, rows) - 1) / G : -1;
   int qpos[NR];
   Chunk16 qr[NR][KLD];
 #pragma unroll
@@ -105,97 +134,205 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(PrefillArgs a,
     l_run[rb] = 0.f;
   }
 
-  // Ring of two page pairs.  Effective pages past n_eff are clamped to the last
-  // one (an L2 hit) and fully masked, so the loop body carries no branch around
-  // the loads.
-  Chunk16 kb[2][2][KLD];
-  VChunk vb[2][2][NB];
-  int lp_buf[2][2];
-  bool ok_buf[2][2];
-  auto issue = [&](int s, int pair) {
+  // Pair staging, HBM -> registers -> LDS.  An LDS buffer holds
+  //   [K_A | K_B]  the two K tiles in the pools' layout (16-byte chunks), and
+  //   V pair       row d (32 keys) = granules A0 B0 A1 B1 A2 B2 A3 B3, granule
+  //                Pg = keys 4g..4g+3 of page P (4 elements),
+  // so a lane's PV operand (granule lq of page A and of page B for dim d) is one
+  // contiguous 2-granule read and a wave's V reads are conflict-free.  Thread
+  // tid moves 16-byte LDS chunks tid + T*c of each part.  Pages past n_eff are
+  // clamped to the last one (masked later); invalid ids read page 0.
+  constexpr int kPageChunks = S::kPageElems * (int)sizeof(E) / 16;
+  constexpr int kGran = 4 * (int)sizeof(E);  // bytes of one V granule
+  constexpr int kKPer = (2 * kPageChunks + S::kThreads - 1) / S::kThreads;
+  constexpr int kVPer = kKPer;               // the V pair has as many 16-byte chunks
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 stK[S::kStages][kKPer], stV[S::kStages][kVPer];  // vector types: kept in registers
+  auto page_of = [&](int v, int& lp, bool& ok) -> int64_t {
+    const int vc = v < n_eff ? v : n_eff - 1;
+    lp = logical_page(w, vc);
+    const int64_t pp = bt[(int64_t)b * a.max_blocks + lp];
+    ok = v < n_eff && pp >= 0 && pp < a.num_pages;
+    return (pp >= 0 && pp < a.num_pages) ? pp : 0;
+  };
+  auto load_pair = [&](int pair, int set) {
+    int lp;
+    bool ok;
+    const int64_t pa = page_of(2 * pair, lp, ok), pb = page_of(2 * pair + 1, lp, ok);
+    const E* kpa = static_cast<const E*>(a.k_pool) + (pa * Hkv + h) * kTile;
+    const E* kpb = static_cast<const E*>(a.k_pool) + (pb * Hkv + h) * kTile;
+    const E* vpa = static_cast<const E*>(a.v_pool) + (pa * Hkv + h) * kTile;
+    const E* vpb = static_cast<const E*>(a.v_pool) + (pb * Hkv + h) * kTile;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int v = 2 * pair + half;
-      const int vc = v < n_eff ? v : n_eff - 1;
-      const int lp = logical_page(w, vc);
-      const int64_t pp = bt[(int64_t)b * a.max_blocks + lp];
-      const bool ok = v < n_eff && pp >= 0 && pp < a.num_pages;
-      lp_buf[s][half] = lp;
-      ok_buf[s][half] = ok;
-      const int64_t tile = (((pp >= 0 && pp < a.num_pages) ? pp : 0) * Hkv + h) * kTile;
-      const E* kp = static_cast<const E*>(a.k_pool) + tile;
-      const E* vp = static_cast<const E*>(a.v_pool) + tile;
-#pragma unroll
-      for (int j = 0; j < KLD; ++j)
-        kb[s][half][j] = *reinterpret_cast<const Chunk16*>(kp + ((4 * j + lq) * kBS + ln) * X);
-#pragma unroll
-      for (int m = 0; m < NB; ++m)
-        vb[s][half][m] = *reinterpret_cast<const VChunk*>(vp + (16 * m + ln) * kBS + 4 * lq);
+    for (int c = 0; c < kKPer; ++c) {
+      const int idx = min(tid + S::kThreads * c, 2 * kPageChunks - 1);
+      const E* src = idx < kPageChunks ? kpa : kpb;
+      stK[set][c] = *reinterpret_cast<const u32x4*>(src + (idx % kPageChunks) * (16 / (int)sizeof(E)));
     }
-    __asm__ volatile("" ::: "memory");
+#pragma unroll
+    for (int c = 0; c < kVPer; ++c) {
+      const int v = min(tid + S::kThreads * c, 2 * kPageChunks - 1);
+      if constexpr (kGran == 8) {  // 16-bit: chunk v = row v/4, granule v%4 of A and B
+        const int off = (v >> 2) * kBS + 4 * (v & 3);
+        const u32x2 ga = *reinterpret_cast<const u32x2*>(vpa + off);
+        const u32x2 gb = *reinterpret_cast<const u32x2*>(vpb + off);
+        stV[set][c] = u32x4{ga[0], ga[1], gb[0], gb[1]};
+      } else {  // fp32: chunk v = row v/8, granule (v%8)/2 of page v%2
+        const int off = (v >> 3) * kBS + 4 * ((v & 7) >> 1);
+        stV[set][c] = *reinterpret_cast<const u32x4*>(((v & 1) ? vpb : vpa) + off);
+      }
+    }
+  };
+  auto store_pair = [&](int buf, int set) {
+    u32x4* dk = reinterpret_cast<u32x4*>(lds + buf * (4 * kPageChunks));
+    u32x4* dv = dk + 2 * kPageChunks;
+#pragma unroll
+    for (int c = 0; c < kKPer; ++c)
+      if ((2 * kPageChunks) % S::kThreads == 0 || tid + S::kThreads * c < 2 * kPageChunks)
+        dk[tid + S::kThreads * c] = stK[set][c];
+#pragma unroll
+    for (int c = 0; c < kVPer; ++c)
+      if ((2 * kPageChunks) % S::kThreads == 0 || tid + S::kThreads * c < 2 * kPageChunks)
+        dv[tid + S::kThreads * c] = stV[set][c];
   };
 
-  auto compute = [&](int s) {
-    // V rows outside the context (tail of the last page, invalid pages) may hold
-    // any bits; zero them (0 * NaN would poison the accumulator).
+  // Interior pairs (every key inside every row's causal window, all keys inside
+  // the context on valid pages) skip the per-key masks; that needs every row of
+  // the wave to be a real row.
+  const bool rows_all_valid = r_w + S::kRowsWave <= rows && first_pos + r_w / G >= 0;
+  const int wave_p_lo = first_pos + r_w / G;
+
+  auto compute = [&](int buf, int pair) {
+    int lpa, lpb;
+    bool oka, okb;
+    page_of(2 * pair, lpa, oka);
+    page_of(2 * pair + 1, lpb, okb);
+    // Skip a pair past the walk or entirely after every row of the wave.
+    if (pair < n_pairs && lpa * kBS <= wave_p_hi) {
+    const bool interior = rows_all_valid && oka && okb && lpb * kBS + kBS - 1 <= wave_p_lo &&
+                          (a.window <= 0 || lpa * kBS > wave_p_hi - a.window);
+    const E* kA = reinterpret_cast<const E*>(lds + buf * (4 * kPageChunks));
+    const E* kB = kA + S::kPageElems;
+    const char* vP = reinterpret_cast<const char*>(kB + S::kPageElems);
+    Chunk16 ka[KLD], kb[KLD];
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      bool vrow[4];
+    for (int j = 0; j < KLD; ++j) {
+      ka[j] = *reinterpret_cast<const Chunk16*>(kA + ((4 * j + lq) * kBS + ln) * X);
+      kb[j] = *reinterpret_cast<const Chunk16*>(kB + ((4 * j + lq) * kBS + ln) * X);
+    }
+    VChunk va[NB], vb[NB];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) vrow[r] = ok_buf[s][half] && lp_buf[s][half] * kBS + 4 * lq + r < L;
+    for (int m = 0; m < NB; ++m) {
+      const VChunk* g = reinterpret_cast<const VChunk*>(vP + (16 * m + ln) * (8 * kGran) + lq * (2 * kGran));
+      va[m] = g[0];
+      vb[m] = g[1];
+    }
+    if (!interior) {
+      // V rows outside the context (tail of the last page, invalid pages) may hold
+      // any bits; zero them (0 * NaN would poison the accumulator).
+      bool vra[4], vrb[4];
 #pragma unroll
-      for (int m = 0; m < NB; ++m) Tr::mask_rows(vb[s][half][m], vrow);
+      for (int r = 0; r < 4; ++r) {
+        vra[r] = oka && lpa * kBS + 4 * lq + r < L;
+        vrb[r] = okb && lpb * kBS + 4 * lq + r < L;
+      }
+#pragma unroll
+      for (int m = 0; m < NB; ++m) {
+        Tr::mask_rows(va[m], vra);
+        Tr::mask_rows(vb[m], vrb);
+      }
     }
 #pragma unroll
     for (int rb = 0; rb < NR; ++rb) {
       f32x4 sa = f32x4{0.f, 0.f, 0.f, 0.f}, sb = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < KLD; ++j) {
-        sa = Tr::qk(kb[s][0][j], qr[rb][j], sa);
-        sb = Tr::qk(kb[s][1][j], qr[rb][j], sb);
+        sa = Tr::qk(ka[j], qr[rb][j], sa);
+        sb = Tr::qk(kb[j], qr[rb][j], sb);
       }
-      const int qp = qpos[rb];
-      float pa[4], pb[4], sl[8];
+      float sl[8];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int ka = lp_buf[s][0] * kBS + 4 * lq + r;
-        const int kb_ = lp_buf[s][1] * kBS + 4 * lq + r;
-        const bool va = ok_buf[s][0] && ka <= qp && (a.window <= 0 || ka > qp - a.window || ka < a.n_sink);
-        const bool vb_ = ok_buf[s][1] && kb_ <= qp && (a.window <= 0 || kb_ > qp - a.window || kb_ < a.n_sink);
-        sl[r] = va ? sa[r] * a.scale_log2 : kNegInf;
-        sl[4 + r] = vb_ ? sb[r] * a.scale_log2 : kNegInf;
+        sl[r] = sa[r] * a.scale_log2;
+        sl[4 + r] = sb[r] * a.scale_log2;
       }
-      float mx = sl[0];
+      if (!interior) {
+        const int qp = qpos[rb];
 #pragma unroll
-      for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sl[i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run[rb], mx);
-      const float m_use = m_new == kNegInf ? 0.f : m_new;
-      const float alpha = exp2_fast(m_run[rb] - m_use);
+        for (int r = 0; r < 4; ++r) {
+          const int ka_ = lpa * kBS + 4 * lq + r;
+          const int kb_ = lpb * kBS + 4 * lq + r;
+          const bool visa = oka && ka_ <= qp && (a.window <= 0 || ka_ > qp - a.window || ka_ < a.n_sink);
+          const bool visb = okb && kb_ <= qp && (a.window <= 0 || kb_ > qp - a.window || kb_ < a.n_sink);
+          sl[r] = visa ? sl[r] : kNegInf;
+          sl[4 + r] = visb ? sl[4 + r] : kNegInf;
+        }
+      }
+      // Lazy rescaling: the reference max m_run of a row only moves (with a
+      // cross-lane max and a rescale of acc and l) when a score exceeds it by
+      // more than kLazyMax; otherwise p = exp2(s - m_run) <= 2^kLazyMax and the
+      // final O = acc / l is unchanged.
+      float lmx = sl[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) lmx = fmaxf(lmx, sl[i]);
+      if (__builtin_amdgcn_ballot_w64(lmx > m_run[rb] + kLazyMax) != 0) {
+        float mx = fmaxf(lmx, __shfl_xor(lmx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run[rb], mx);
+        const float alpha = m_new == kNegInf ? 1.f : exp2_fast(m_run[rb] - m_new);
+        l_run[rb] *= alpha;
+#pragma unroll
+        for (int m = 0; m < NB; ++m) acc[rb][m] *= alpha;
+        m_run[rb] = m_new;
+      }
+      const float m_use = m_run[rb] == kNegInf ? 0.f : m_run[rb];
+      float pa[4], pb[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         pa[r] = exp2_fast(sl[r] - m_use);
         pb[r] = exp2_fast(sl[4 + r] - m_use);
       }
-      l_run[rb] = l_run[rb] * alpha + (((pa[0] + pa[1]) + (pa[2] + pa[3])) +
-                                       ((pb[0] + pb[1]) + (pb[2] + pb[3])));
-      m_run[rb] = m_new;
+      l_run[rb] += ((pa[0] + pa[1]) + (pa[2] + pa[3])) + ((pb[0] + pb[1]) + (pb[2] + pb[3]));
       const typename Tr::P8 p8 = Tr::pack_p8(pa, pb);
 #pragma unroll
-      for (int m = 0; m < NB; ++m) acc[rb][m] = Tr::pv32(vb[s][0][m], vb[s][1][m], p8, acc[rb][m] * alpha);
+      for (int m = 0; m < NB; ++m) acc[rb][m] = Tr::pv32(va[m], vb[m], p8, acc[rb][m]);
+    }
     }
   };
 
-  if (n_eff > 0) {
-    const int n_pairs = (n_eff + 1) / 2;
-    issue(0, 0);
-    issue(1, 1);
-    for (int pi = 0; pi < n_pairs; pi += 2) {
-      compute(0);
-      issue(0, pi + 2);
-      compute(1);
-      issue(1, pi + 3);
+  // Ring: pair i is in LDS buffer i % 2 while pair i + 1 travels from HBM / L2
+  // into the staging registers; one barrier per pair.
+  if (n_pairs > 0) {
+    if constexpr (S::kStages == 2) {
+      // Two stage sets: pair i + 2 is loaded while pair i is computed and pair
+      // i + 1 waits in registers for its LDS buffer.  Loads past the last pair
+      // repeat the last page (an L2 hit) into buffers nobody reads; being
+      // unconditional keeps the stage in registers.
+      load_pair(0, 0);
+      load_pair(1, 1);
+      store_pair(0, 0);
+      __syncthreads();
+      for (int i = 0; i < n_pairs; i += 2) {
+        load_pair(i + 2, 0);
+        compute(0, i);
+        store_pair(1, 1);
+        __syncthreads();
+        load_pair(i + 3, 1);
+        compute(1, i + 1);
+        store_pair(0, 0);
+        __syncthreads();
+      }
+    } else {
+      load_pair(0, 0);
+      store_pair(0, 0);
+      __syncthreads();
+      for (int i = 0; i < n_pairs; ++i) {
+        load_pair(i + 1, 0);
+        compute(i & 1, i);
+        store_pair((i + 1) & 1, 0);
+        __syncthreads();
+      }
     }
   }
 
@@ -216,21 +353,41 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(PrefillArgs a,
   }
 }
 
+template <int DT, int D>
+void launch_prefill_d(dim3 grid, hipStream_t stream, const PrefillArgs& a, const int32_t* bt,
+                      const int32_t* ctx, const int32_t* qs) {
+  // LDS beyond 64 KiB (fp32 with head_dim 256) must be allowed per kernel once.
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&prefill_kernel<DT, D>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)PrefillShape<DT, D>::kLdsBytes);
+  (void)attr;
+  prefill_kernel<DT, D><<<grid, PrefillShape<DT, D>::kThreads, PrefillShape<DT, D>::kLdsBytes, stream>>>(a, bt, ctx, qs);
+}
+
 template <int DT>
 void launch_prefill(int head_dim, dim3 grid, hipStream_t stream, const PrefillArgs& a,
                     const int32_t* bt, const int32_t* ctx, const int32_t* qs) {
   switch (head_dim) {
-    case 64: prefill_kernel<DT, 64><<<grid, kPfThreads, 0, stream>>>(a, bt, ctx, qs); break;
-    case 128: prefill_kernel<DT, 128><<<grid, kPfThreads, 0, stream>>>(a, bt, ctx, qs); break;
-    default: prefill_kernel<DT, 256><<<grid, kPfThreads, 0, stream>>>(a, bt, ctx, qs); break;
+    case 64: launch_prefill_d<DT, 64>(grid, stream, a, bt, ctx, qs); break;
+    case 128: launch_prefill_d<DT, 128>(grid, stream, a, bt, ctx, qs); break;
+    default: launch_prefill_d<DT, 256>(grid, stream, a, bt, ctx, qs); break;
   }
 }
 
-int rows_per_workgroup(int head_dim) {
+template <int DT>
+int rows_per_workgroup_t(int head_dim) {
   switch (head_dim) {
-    case 64: return PrefillShape<64>::kRowsWG;
-    case 128: return PrefillShape<128>::kRowsWG;
-    default: return PrefillShape<256>::kRowsWG;
+    case 64: return PrefillShape<DT, 64>::kRowsWG;
+    case 128: return PrefillShape<DT, 128>::kRowsWG;
+    default: return PrefillShape<DT, 256>::kRowsWG;
+  }
+}
+
+int rows_per_workgroup(int dtype, int head_dim) {
+  switch (dtype) {
+    case IVAKV_F16: return rows_per_workgroup_t<IVAKV_F16>(head_dim);
+    case IVAKV_BF16: return rows_per_workgroup_t<IVAKV_BF16>(head_dim);
+    default: return rows_per_workgroup_t<IVAKV_F32>(head_dim);
   }
 }
 
@@ -265,12 +422,11 @@ extern "C" int ivakv_prefill_attn(const void* q, const void* k_pool, const void*
     return fail(IVAKV_E_ARG, "%s: null pointer argument", name);
   if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out))
     return fail(IVAKV_E_ARG, "%s: q, pools and out must be 16-byte aligned", name);
-  if (batch > 65535 || num_kv_heads > 65535)
-    return fail(IVAKV_E_SHAPE, "%s: batch and num_kv_heads must be <= 65535", name);
   if (!(scale == scale)) return fail(IVAKV_E_ARG, "%s: scale is NaN", name);
   const int G = num_q_heads / num_kv_heads;
   const int64_t rows = (int64_t)max_query_len * G;
-  const int64_t blocks_x = (rows + rows_per_workgroup(head_dim) - 1) / rows_per_workgroup(head_dim);
+  const int rows_wg = rows_per_workgroup(dtype, head_dim);
+  const int64_t blocks_x = (rows + rows_wg - 1) / rows_wg;
   if (blocks_x > 0x7fffffff) return fail(IVAKV_E_SHAPE, "%s: max_query_len too large", name);
 
   PrefillArgs a;
@@ -286,7 +442,12 @@ extern "C" int ivakv_prefill_attn(const void* q, const void* k_pool, const void*
   a.scale_log2 = (float)((double)scale * 1.4426950408889634);
   a.window = window > 0 ? window : 0;
   a.n_sink = n_sink;
-  const dim3 grid((unsigned)blocks_x, (unsigned)num_kv_heads, (unsigned)batch);
+  a.blocks_x = (int)blocks_x;
+  // 1-D grid in XCD-aware order (see prefill_kernel): 8 interleaved unit streams.
+  const int64_t units_per_xcd = ((int64_t)batch * num_kv_heads + 7) / 8;
+  const int64_t n_wg = units_per_xcd * blocks_x * 8;
+  if (n_wg > 0x7fffffff) return fail(IVAKV_E_SHAPE, "%s: launch too large", name);
+  const dim3 grid((unsigned)n_wg);
   switch (dtype) {
     case IVAKV_F16: launch_prefill<IVAKV_F16>(head_dim, grid, stream, a, block_tables, context_lens, query_start); break;
     case IVAKV_BF16: launch_prefill<IVAKV_BF16>(head_dim, grid, stream, a, block_tables, context_lens, query_start); break;
