@@ -123,6 +123,19 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
 #pragma unroll
     for (int j = 0; j < KLD; ++j) qr[rb][j] = *reinterpret_cast<const Chunk16*>(qb + (4 * j + lq) * X);
   }
+  // Scores are kept raw (q.k) and scaled inside the exponent, exp2(s*c - m), with
+  // c = |scale * log2(e)| > 0; a negative scale negates q instead (exact), so
+  // max(s*c) = c*max(s) always holds.  (A zero scale uses the smallest normal c.)
+  const float c_log2 = fmaxf(fabsf(a.scale_log2), 1.17549435e-38f);
+  if (a.scale_log2 < 0.f) {
+    const uint32_t sign = sizeof(E) == 2 ? 0x80008000u : 0x80000000u;
+#pragma unroll
+    for (int rb = 0; rb < NR; ++rb)
+#pragma unroll
+      for (int j = 0; j < KLD; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qr[rb][j].w[i] ^= sign;
+  }
 
   f32x4 acc[NR][NB];
   float m_run[NR], l_run[NR];
@@ -243,19 +256,26 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
         Tr::mask_rows(vb[m], vrb);
       }
     }
+    // All QK products first: the MFMAs of block rb + 1 run while block rb's
+    // softmax is on the VALU.
+    f32x4 sa[NR], sb[NR];
 #pragma unroll
     for (int rb = 0; rb < NR; ++rb) {
-      f32x4 sa = f32x4{0.f, 0.f, 0.f, 0.f}, sb = f32x4{0.f, 0.f, 0.f, 0.f};
+      sa[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      sb[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < KLD; ++j) {
-        sa = Tr::qk(ka[j], qr[rb][j], sa);
-        sb = Tr::qk(kb[j], qr[rb][j], sb);
+        sa[rb] = Tr::qk(ka[j], qr[rb][j], sa[rb]);
+        sb[rb] = Tr::qk(kb[j], qr[rb][j], sb[rb]);
       }
+    }
+#pragma unroll
+    for (int rb = 0; rb < NR; ++rb) {
       float sl[8];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sl[r] = sa[r] * a.scale_log2;
-        sl[4 + r] = sb[r] * a.scale_log2;
+        sl[r] = sa[rb][r];
+        sl[4 + r] = sb[rb][r];
       }
       if (!interior) {
         const int qp = qpos[rb];
@@ -269,13 +289,14 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
           sl[4 + r] = visb ? sl[4 + r] : kNegInf;
         }
       }
-      // Lazy rescaling: the reference max m_run of a row only moves (with a
-      // cross-lane max and a rescale of acc and l) when a score exceeds it by
-      // more than kLazyMax; otherwise p = exp2(s - m_run) <= 2^kLazyMax and the
-      // final O = acc / l is unchanged.
+      // Lazy rescaling: the reference max m_run of a row (log2 units) only moves
+      // (with a cross-lane max and a rescale of acc and l) when a scaled score
+      // exceeds it by more than kLazyMax; otherwise p = exp2(s*c - m_run) <=
+      // 2^kLazyMax and the final O = acc / l is unchanged.
       float lmx = sl[0];
 #pragma unroll
       for (int i = 1; i < 8; ++i) lmx = fmaxf(lmx, sl[i]);
+      lmx *= c_log2;
       if (__builtin_amdgcn_ballot_w64(lmx > m_run[rb] + kLazyMax) != 0) {
         float mx = fmaxf(lmx, __shfl_xor(lmx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -290,8 +311,8 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
       float pa[4], pb[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        pa[r] = exp2_fast(sl[r] - m_use);
-        pb[r] = exp2_fast(sl[4 + r] - m_use);
+        pa[r] = exp2_fast(__builtin_fmaf(sl[r], c_log2, -m_use));
+        pb[r] = exp2_fast(__builtin_fmaf(sl[4 + r], c_log2, -m_use));
       }
       l_run[rb] += ((pa[0] + pa[1]) + (pa[2] + pa[3])) + ((pb[0] + pb[1]) + (pb[2] + pb[3]));
       const typename Tr::P8 p8 = Tr::pack_p8(pa, pb);

@@ -137,3 +137,17 @@ def test_prefill_argument_errors(iva, dev):
         iva.paged_prefill_attention(args[0].float(), *args[1:], c["query_start"].to(dev))
     out = iva.paged_prefill_attention(*args, c["query_start"].to(dev), max_query_len=0)
     assert out.shape == c["q"].shape  # nothing computed, no error
+
+
+@pytest.mark.parametrize("scale", [-0.2, 0.0, 0.35])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=str)
+def test_prefill_explicit_scales(iva, dev, scale, dtype):
+    """Non-default scales, including negative (the kernel negates q) and zero (uniform
+    weights over the visible keys)."""
+    c = make(iva, [90, 33], [40, 33], 8, 2, 64, dtype, seed=13)
+    lay = c["layout"]
+    out = run(iva, dev, c, scale=scale, window=20, n_sink=2)
+    ref = orc.prefill_attention(to_np(c["q"]), to_np(c["k_pool"]), to_np(c["v_pool"]),
+                                lay.block_tables.numpy(), lay.context_lens.numpy(),
+                                c["query_start"].numpy(), scale=scale, window=20, n_sink=2)
+    assert_close(out, ref, dtype, f"scale {scale}")
