@@ -184,6 +184,50 @@ int ivakv_decode_append_attn(const void* q, const void* k_new, const void* v_new
                              hipStream_t stream);
 
 /*
+ * FP8 KV pages (OCP e4m3fn codes, one byte per element) with one fp32 scaling factor
+ * per (slot, kv head):
+ *   k_pool  [num_pages][Hkv][D/16][BS][16] bytes (16-byte chunks of 16 dims)
+ *   v_pool  [num_pages][Hkv][D][BS] bytes
+ *   k_scale, v_scale [num_pages][Hkv][BS] fp32
+ * A row x of one (token, kv head) is stored as e4m3(x * sf), sf = 448 / max|x|
+ * (1 for an all-zero row), clamped to [1e-8, 1e8], rounded to nearest even and
+ * saturated at +-448; it reads back as code / sf.  BS = 16, head_dim in {64,128,256}.
+ * Replaces: the reference's kv_cache_dtype "fp8" (configs/quant_infer.yaml:22,52),
+ * with its scaling rule (src/quant/fp8_runtime.py:66-76) applied per row.
+ *
+ * ivakv_append_fp8: ivakv_append for FP8 pools; k_new / v_new rows of dtype f32 / f16 /
+ * bf16 with element strides as in ivakv_append.  Skips slots outside the pool.
+ */
+int ivakv_append_fp8(const void* k_new, const void* v_new, int64_t k_tok_stride,
+                     int64_t k_head_stride, int64_t v_tok_stride, int64_t v_head_stride,
+                     void* k_pool, void* v_pool, float* k_scale, float* v_scale,
+                     const int32_t* slot_mapping, int n_tok, int num_kv_heads, int head_dim,
+                     int block_size, int num_pages, int dtype, hipStream_t stream);
+/*
+ * ivakv_gather_fp8: ivakv_gather for FP8 pools, dequantized (code / sf) into outputs of
+ * dtype `dtype` (f32 / f16 / bf16, [batch][Hkv][out_len][D] dense); zero past the
+ * context or on an invalid page id.
+ */
+int ivakv_gather_fp8(const void* k_pool, const void* v_pool, const float* k_scale,
+                     const float* v_scale, const int32_t* block_tables,
+                     const int32_t* context_lens, int batch, int max_blocks, int num_kv_heads,
+                     int head_dim, int block_size, int num_pages, int out_len, void* k_out,
+                     void* v_out, int dtype, hipStream_t stream);
+/*
+ * ivakv_decode_attn_fp8: ivakv_decode_attn over FP8 pools (stream walk); q and out of
+ * dtype f16 or bf16 (`dtype`), scores and softmax in fp32 on the dequantized keys and
+ * values.  Workspace: ivakv_decode_workspace_size with partition_pages <= 0;
+ * batch <= 8192.  k_scale / v_scale 16-byte aligned.
+ */
+int ivakv_decode_attn_fp8(const void* q, const void* k_pool, const void* v_pool,
+                          const float* k_scale, const float* v_scale,
+                          const int32_t* block_tables, const int32_t* context_lens, void* out,
+                          void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
+                          int num_kv_heads, int head_dim, int block_size, int max_blocks,
+                          int num_pages, float scale, int window, int n_sink, int dtype,
+                          hipStream_t stream);
+
+/*
  * Paged multi-query causal attention (prefill / chunked prefill).  Sequence b owns
  * query rows query_start[b] .. query_start[b+1]-1 of q ([n_tok][Hq][D] dense, pool
  * dtype); with n_b rows and context length L = context_lens[b], row i sits at

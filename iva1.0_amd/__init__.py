@@ -12,6 +12,7 @@ from .ops import (
     chunk_elems,
     decode_workspace_bytes,
     dtype_code,
+    is_fp8,
     kv_append,
     kv_gather,
     kv_ops,
@@ -22,6 +23,7 @@ from .ops import (
     paged_prefill_attention,
     pool_geometry,
     pool_shapes,
+    scale_shape,
 )
 from .model import PagedAttention, Transformer, TransformerConfig, get_attention
 from .paged_cache import OutOfPagesError, PagedKVCache, PagedKVPool
@@ -37,6 +39,7 @@ __all__ = [
     "chunk_elems",
     "decode_workspace_bytes",
     "dtype_code",
+    "is_fp8",
     "kv_append",
     "kv_gather",
     "kv_ops",
@@ -47,4 +50,5 @@ __all__ = [
     "paged_prefill_attention",
     "pool_geometry",
     "pool_shapes",
+    "scale_shape",
 ]

@@ -73,6 +73,28 @@ SIGNATURES = {
         c_int, c_int, c_int,                   # window, n_sink, dtype
         c_void_p,                              # stream
     ]),
+    "ivakv_append_fp8": (c_int, [
+        c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,  # k_new, v_new, strides
+        c_void_p, c_void_p, c_void_p, c_void_p,  # k_pool, v_pool, k_scale, v_scale
+        c_void_p, c_int, c_int, c_int, c_int, c_int,  # slots, n_tok, Hkv, D, bs, num_pages
+        c_int, c_void_p,                         # dtype, stream
+    ]),
+    "ivakv_gather_fp8": (c_int, [
+        c_void_p, c_void_p, c_void_p, c_void_p,  # k_pool, v_pool, k_scale, v_scale
+        c_void_p, c_void_p,                      # block_tables, context_lens
+        c_int, c_int, c_int, c_int, c_int, c_int, c_int,  # B, max_blocks, Hkv, D, bs, pages, out_len
+        c_void_p, c_void_p, c_int, c_void_p,     # k_out, v_out, dtype, stream
+    ]),
+    "ivakv_decode_attn_fp8": (c_int, [
+        c_void_p, c_void_p, c_void_p,          # q, k_pool, v_pool
+        c_void_p, c_void_p,                    # k_scale, v_scale
+        c_void_p, c_void_p,                    # block_tables, context_lens
+        c_void_p, c_void_p, c_size_t,          # out, workspace, workspace_bytes
+        c_int, c_int, c_int, c_int,            # batch, num_q_heads, num_kv_heads, head_dim
+        c_int, c_int, c_int, c_float,          # block_size, max_blocks, num_pages, scale
+        c_int, c_int, c_int,                   # window, n_sink, dtype
+        c_void_p,                              # stream
+    ]),
     "ivakv_prefill_attn": (c_int, [
         c_void_p, c_void_p, c_void_p,          # q, k_pool, v_pool
         c_void_p, c_void_p, c_void_p,          # block_tables, context_lens, query_start

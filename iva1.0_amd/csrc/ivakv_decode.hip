@@ -26,6 +26,8 @@
 //     stream walk's page prefix in LDS): grid (kv head, sequence, partition) of 4-wave
 //     workgroups; a partition of part_pages pages is split over the 4 waves
 //     and merged through LDS, then across partitions by decode_merge_kernel.
+#include <type_traits>
+
 #include "ivakv_tile.h"
 
 namespace ivakv {
@@ -78,6 +80,9 @@ struct DecodeArgs {
   const void* k_new;
   const void* v_new;
   int fused;
+  // FP8 pools: per-(slot, kv head) scaling factors, [num_pages][Hkv][16] fp32.
+  const float* k_scale;
+  const float* v_scale;
 };
 
 
@@ -103,110 +108,228 @@ __device__ inline int num_partitions(const PageWalk& w, const DecodeArgs& a) {
   return n < a.n_parts_max ? n : a.n_parts_max;
 }
 
-// Register-level tile machinery of one wave (lane = 16 * lq + ln).
+// Online-softmax state of one wave: lane holds head ln's running max (the same
+// in every k-group), its k-group's share of the running sum, and
+// O^T[16m + 4lq + r][ln] in acc[m][r].
+template <int NB>
+struct SoftmaxState {
+  f32x4 acc[NB];
+  float m_run, l_run;
+  __device__ inline void reset() {
+#pragma unroll
+    for (int m = 0; m < NB; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_run = kNegInf;
+    l_run = 0.f;
+  }
+  // Sum of head ln over the four k-groups.
+  __device__ inline float total() const {
+    float l = l_run + __shfl_xor(l_run, 16);
+    return l + __shfl_xor(l, 32);
+  }
+  // Folds scaled scores sl (masked rows at -inf) and returns the weights p;
+  // the caller then accumulates P . V.
+  __device__ inline void fold(const float sl[4], float p[4]) {
+    float mx = fmaxf(fmaxf(sl[0], sl[1]), fmaxf(sl[2], sl[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == kNegInf ? 0.f : m_new;
+    const float alpha = exp2_fast(m_run - m_use);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[r] = exp2_fast(sl[r] - m_use);
+    l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    m_run = m_new;
+#pragma unroll
+    for (int m = 0; m < NB; ++m) acc[m] *= alpha;
+  }
+};
+
+// Physical page of logical page lp of sequence b, or -1 when the table entry
+// is outside the pool.  The tile of an invalid page is read from page 0 and
+// fully masked.
+__device__ inline int64_t phys_page(const DecodeArgs& a, const int32_t* bt, int b, int lp) {
+  const int64_t p = bt[(int64_t)b * a.max_blocks + lp];
+  return (p < 0 || p >= a.num_pages) ? -1 : p;
+}
+
+// Visibility of rows 4*lq + r of logical page lp for the walk w.
+__device__ inline void rows_visible(const PageWalk& w, int lp, bool live, const DecodeArgs& a,
+                                    int lq, bool vis[4]) {
+  const int pos0 = lp * kBS + 4 * lq;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int pos = pos0 + r;
+    vis[r] = live && pos < w.L && (pos >= w.win_start || pos < a.n_sink);
+  }
+}
+
+// Register-level tile machinery of one wave (lane = 16 * lq + ln) for pools of
+// the query dtype DT.  Interface shared with TileOps8: QReg / TileReg register
+// sets, load_q, load_tile, score.
 template <int DT, int D>
 struct TileOps {
   using Tr = Traits<DT>;
   using E = typename Tr::E;
   using VChunk = typename Tr::VChunk;
+  static constexpr int kD = D;
   static constexpr int X = 16 / (int)sizeof(E);  // elements per 16-byte K chunk
   static constexpr int KLD = D / X / 4;          // K loads per lane per tile
   static constexpr int NB = D / 16;              // 16-dim blocks (PV MFMAs per tile)
   static constexpr int64_t kTile = (int64_t)D * kBS;  // elements of one tile
-
-  // Online-softmax state of the wave: lane holds head ln's running max (the
-  // same in every k-group), its k-group's share of the running sum, and
-  // O^T[16m + 4lq + r][ln] in acc[m][r].
-  struct State {
-    f32x4 acc[NB];
-    float m_run, l_run;
-    __device__ inline void reset() {
-#pragma unroll
-      for (int m = 0; m < NB; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-      m_run = kNegInf;
-      l_run = 0.f;
-    }
-    // Sum of head ln over the four k-groups.
-    __device__ inline float total() const {
-      float l = l_run + __shfl_xor(l_run, 16);
-      return l + __shfl_xor(l, 32);
-    }
+  using State = SoftmaxState<NB>;
+  struct QReg {
+    Chunk16 c[KLD];
+  };
+  struct TileReg {
+    Chunk16 k[KLD];
+    VChunk v[NB];
   };
 
   // Query rows of kv head h's group for sequence b, in K-chunk order (chunk
   // 4*j + lq).  MFMA columns ln >= G repeat head G-1: their scores are never
   // written out, and the loads stay unconditional (no exec-masked branch,
   // whose join would make the compiler wait for every outstanding load).
-  static __device__ inline void load_q(const DecodeArgs& a, int b, int h, int ln, int lq,
-                                       Chunk16 (&qr)[KLD]) {
+  static __device__ inline void load_q(const DecodeArgs& a, int b, int h, int ln, int lq, QReg& qr) {
     const int g = ln < a.G ? ln : a.G - 1;
     const E* qb = static_cast<const E*>(a.q) + ((int64_t)b * a.Hkv * a.G + h * a.G + g) * D;
 #pragma unroll
-    for (int j = 0; j < KLD; ++j) qr[j] = *reinterpret_cast<const Chunk16*>(qb + (4 * j + lq) * X);
-  }
-
-  // Physical page of logical page lp of sequence b, or -1 when the table entry
-  // is outside the pool.  The tile of an invalid page is read from page 0 and
-  // fully masked.
-  static __device__ inline int64_t phys_page(const DecodeArgs& a, const int32_t* bt, int b, int lp) {
-    const int64_t p = bt[(int64_t)b * a.max_blocks + lp];
-    return (p < 0 || p >= a.num_pages) ? -1 : p;
+    for (int j = 0; j < KLD; ++j) qr.c[j] = *reinterpret_cast<const Chunk16*>(qb + (4 * j + lq) * X);
   }
 
   // Issues the loads of one tile.  The empty asm with a memory clobber pins
   // them here: loads of read-only memory may otherwise be sunk down to their
   // first use in the next ring step, which serialises load and compute.
   static __device__ inline void load_tile(const DecodeArgs& a, int64_t phys, int h, int ln, int lq,
-                                          Chunk16 (&kd)[KLD], VChunk (&vd)[NB]) {
+                                          TileReg& t) {
     const int64_t tile = ((phys < 0 ? 0 : phys) * a.Hkv + h) * kTile;
     const E* kp = static_cast<const E*>(a.k_pool) + tile;
     const E* vp = static_cast<const E*>(a.v_pool) + tile;
 #pragma unroll
-    for (int j = 0; j < KLD; ++j) kd[j] = *reinterpret_cast<const Chunk16*>(kp + ((4 * j + lq) * kBS + ln) * X);
+    for (int j = 0; j < KLD; ++j) t.k[j] = *reinterpret_cast<const Chunk16*>(kp + ((4 * j + lq) * kBS + ln) * X);
 #pragma unroll
-    for (int m = 0; m < NB; ++m) vd[m] = *reinterpret_cast<const VChunk*>(vp + (16 * m + ln) * kBS + 4 * lq);
+    for (int m = 0; m < NB; ++m) t.v[m] = *reinterpret_cast<const VChunk*>(vp + (16 * m + ln) * kBS + 4 * lq);
     __asm__ volatile("" ::: "memory");
   }
 
   // Scores one loaded tile of logical page lp and folds it into st.  With
   // live == false (a padding slot of the ring) every row is masked.
-  static __device__ inline void score(State& st, const Chunk16 (&kc)[KLD], VChunk (&vc)[NB],
-                                      const Chunk16 (&qr)[KLD], const PageWalk& w, int lp,
-                                      bool live, const DecodeArgs& a, int lq) {
+  static __device__ inline void score(State& st, TileReg& t, const QReg& qr, const PageWalk& w,
+                                      int lp, bool live, const DecodeArgs& a, int lq) {
     // S^T = K . Q^T : lane holds rows 4*lq + r of head ln.
     f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < KLD; ++j) s = Tr::qk(kc[j], qr[j], s);
-    const int pos0 = lp * kBS + 4 * lq;
-    float sl[4];
+    for (int j = 0; j < KLD; ++j) s = Tr::qk(t.k[j], qr.c[j], s);
     bool vis[4];
+    rows_visible(w, lp, live, a, lq, vis);
+    float sl[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int pos = pos0 + r;
-      vis[r] = live && pos < w.L && (pos >= w.win_start || pos < a.n_sink);
-      sl[r] = vis[r] ? s[r] * a.scale_log2 : kNegInf;
-    }
+    for (int r = 0; r < 4; ++r) sl[r] = vis[r] ? s[r] * a.scale_log2 : kNegInf;
     // Rows that are not attended may hold any bits (0 * NaN would poison acc).
     // Branch-free: no block boundary between the MFMAs and their first use.
 #pragma unroll
-    for (int m = 0; m < NB; ++m) Tr::mask_rows(vc[m], vis);
-    float mx = fmaxf(fmaxf(sl[0], sl[1]), fmaxf(sl[2], sl[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(st.m_run, mx);
-    const float m_use = m_new == kNegInf ? 0.f : m_new;
-    const float alpha = exp2_fast(st.m_run - m_use);
+    for (int m = 0; m < NB; ++m) Tr::mask_rows(t.v[m], vis);
     float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = exp2_fast(sl[r] - m_use);
-    st.l_run = st.l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    st.m_run = m_new;
-#pragma unroll
-    for (int m = 0; m < NB; ++m) st.acc[m] *= alpha;
+    st.fold(sl, p);
     // O^T += V^T . P^T
     const typename Tr::PVec pv = Tr::pack_p(p);
 #pragma unroll
-    for (int m = 0; m < NB; ++m) st.acc[m] = Tr::pv(vc[m], pv, st.acc[m]);
+    for (int m = 0; m < NB; ++m) st.acc[m] = Tr::pv(t.v[m], pv, st.acc[m]);
+  }
+};
+
+// The same for FP8 (OCP e4m3fn) pools with per-(slot, kv head) scaling factors
+// (quantized = x * sf, sf = 448 / amax of the row; k_scale / v_scale [page][Hkv][16]
+// fp32), queries and output of dtype DT (fp16 or bf16).  Layout: k_pool
+// [page][Hkv][D/16][16][16] bytes, v_pool [page][Hkv][D][16] bytes.  A lane's 16-byte K
+// chunk holds dims 16c .. 16c+15 (c = 4i + lq) of row ln; it is converted to two
+// 8-element operands (v_cvt_scalef32_pk_*_fp8, exact) for two 16x16x32 MFMAs, whose
+// query chunks are loaded in the same dim order.  Per key, 1/sf_k joins the score
+// scale and 1/sf_v multiplies p before the PV product.
+template <int DT, int D>
+struct TileOps8 {
+  using Tr = Traits<DT>;
+  using E = typename Tr::E;
+  using VChunk = typename Tr::VChunk;
+  static constexpr int kD = D;
+  static constexpr int KL = D / 64;   // 16-byte K loads (16 dims) per lane per tile
+  static constexpr int NB = D / 16;
+  static constexpr int64_t kTileBytes = (int64_t)D * kBS;
+  using State = SoftmaxState<NB>;
+  struct QReg {
+    Chunk16 c[2 * KL];  // c[2i + half]: dims 16 * (4i + lq) + 8 * half .. + 8
+  };
+  struct TileReg {
+    Chunk16 k[KL];
+    uint32_t v[NB];  // keys 4lq .. 4lq+3 of dim 16m + ln, one byte each
+    f32x4 ks, vs;    // scaling factors of keys 4lq .. 4lq+3
+  };
+
+  static __device__ inline void load_q(const DecodeArgs& a, int b, int h, int ln, int lq, QReg& qr) {
+    const int g = ln < a.G ? ln : a.G - 1;
+    const E* qb = static_cast<const E*>(a.q) + ((int64_t)b * a.Hkv * a.G + h * a.G + g) * D;
+#pragma unroll
+    for (int i = 0; i < KL; ++i)
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+        qr.c[2 * i + half] = *reinterpret_cast<const Chunk16*>(qb + 16 * (4 * i + lq) + 8 * half);
+  }
+
+  static __device__ inline void load_tile(const DecodeArgs& a, int64_t phys, int h, int ln, int lq,
+                                          TileReg& t) {
+    const int64_t tile = (phys < 0 ? 0 : phys) * a.Hkv + h;
+    const uint8_t* kp = static_cast<const uint8_t*>(a.k_pool) + tile * kTileBytes;
+    const uint8_t* vp = static_cast<const uint8_t*>(a.v_pool) + tile * kTileBytes;
+#pragma unroll
+    for (int i = 0; i < KL; ++i) t.k[i] = *reinterpret_cast<const Chunk16*>(kp + ((4 * i + lq) * kBS + ln) * 16);
+#pragma unroll
+    for (int m = 0; m < NB; ++m) t.v[m] = *reinterpret_cast<const uint32_t*>(vp + (16 * m + ln) * kBS + 4 * lq);
+    t.ks = *reinterpret_cast<const f32x4*>(a.k_scale + tile * kBS + 4 * lq);
+    t.vs = *reinterpret_cast<const f32x4*>(a.v_scale + tile * kBS + 4 * lq);
+    __asm__ volatile("" ::: "memory");
+  }
+
+  // Two fp8 values (bytes 2*HI, 2*HI+1 of w) as two DT values, exactly.
+  template <bool HI>
+  static __device__ inline uint32_t cvt2(uint32_t w) {
+    if constexpr (DT == IVAKV_F16)
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
+    else
+      return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+  }
+
+  static __device__ inline void score(State& st, TileReg& t, const QReg& qr, const PageWalk& w,
+                                      int lp, bool live, const DecodeArgs& a, int lq) {
+    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < KL; ++i) {
+      const Chunk16 lo{{cvt2<false>(t.k[i].w[0]), cvt2<true>(t.k[i].w[0]),
+                        cvt2<false>(t.k[i].w[1]), cvt2<true>(t.k[i].w[1])}};
+      const Chunk16 hi{{cvt2<false>(t.k[i].w[2]), cvt2<true>(t.k[i].w[2]),
+                        cvt2<false>(t.k[i].w[3]), cvt2<true>(t.k[i].w[3])}};
+      s = Tr::qk(lo, qr.c[2 * i], s);
+      s = Tr::qk(hi, qr.c[2 * i + 1], s);
+    }
+    bool vis[4];
+    rows_visible(w, lp, live, a, lq, vis);
+    float sl[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      sl[r] = vis[r] ? s[r] * (a.scale_log2 * __builtin_amdgcn_rcpf(t.ks[r])) : kNegInf;
+    // Zero the bytes of rows that are not attended (any bits, NaN codes included).
+    const uint32_t keep = (vis[0] ? 0xFFu : 0u) | (vis[1] ? 0xFF00u : 0u) |
+                          (vis[2] ? 0xFF0000u : 0u) | (vis[3] ? 0xFF000000u : 0u);
+    float p[4];
+    st.fold(sl, p);
+    float pv_in[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pv_in[r] = p[r] * __builtin_amdgcn_rcpf(t.vs[r]);
+    const typename Tr::PVec pv = Tr::pack_p(pv_in);
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+      const uint32_t vb = t.v[m] & keep;
+      const Chunk8 vh{{cvt2<false>(vb), cvt2<true>(vb)}};
+      st.acc[m] = Tr::pv(vh, pv, st.acc[m]);
+    }
   }
 };
 
@@ -231,8 +354,7 @@ __global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_partial_kern
     DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ ctx) {
   using Ops = TileOps<DT, D>;
   using E = typename Ops::E;
-  using VChunk = typename Ops::VChunk;
-  constexpr int KLD = Ops::KLD, NB = Ops::NB;
+  constexpr int NB = Ops::NB;
 
   const int h = blockIdx.x, b = blockIdx.y, part = blockIdx.z;
   const int lane = threadIdx.x & 63;
@@ -247,7 +369,7 @@ __global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_partial_kern
   const int Hq = a.Hkv * G;
   const bool g_ok = ln < G;
 
-  Chunk16 qr[KLD];
+  typename Ops::QReg qr;
   Ops::load_q(a, b, h, ln, lq, qr);
   typename Ops::State st;
   st.reset();
@@ -259,21 +381,20 @@ __global__ __launch_bounds__(kThreads, kStreamWGsPerCU) void decode_partial_kern
   auto eff_page = [&](int i) { return v_begin + kWaves * min(i, n_mine - 1); };
 
   if (n_mine > 0) {
-    Chunk16 kb[kPageBufs][KLD];
-    VChunk vb[kPageBufs][NB];
+    typename Ops::TileReg tb[kPageBufs];
     int64_t pb[kPageBufs];
 #pragma unroll
     for (int s = 0; s < kPageBufs; ++s) {
-      pb[s] = Ops::phys_page(a, bt, b, logical_page(w, eff_page(s)));
-      Ops::load_tile(a, pb[s], h, ln, lq, kb[s], vb[s]);
+      pb[s] = phys_page(a, bt, b, logical_page(w, eff_page(s)));
+      Ops::load_tile(a, pb[s], h, ln, lq, tb[s]);
     }
     for (int i = 0; i < n_mine; i += kPageBufs) {
 #pragma unroll
       for (int s = 0; s < kPageBufs; ++s) {
-        Ops::score(st, kb[s], vb[s], qr, w, logical_page(w, eff_page(i + s)),
+        Ops::score(st, tb[s], qr, w, logical_page(w, eff_page(i + s)),
                    i + s < n_mine && pb[s] >= 0, a, lq);
-        pb[s] = Ops::phys_page(a, bt, b, logical_page(w, eff_page(i + s + kPageBufs)));
-        Ops::load_tile(a, pb[s], h, ln, lq, kb[s], vb[s]);
+        pb[s] = phys_page(a, bt, b, logical_page(w, eff_page(i + s + kPageBufs)));
+        Ops::load_tile(a, pb[s], h, ln, lq, tb[s]);
       }
     }
   }
@@ -427,13 +548,11 @@ struct WaveSplit {
 // with the workspace and output stores in the loop, that is what lets the
 // compiler read them through the scalar cache (s_load, lgkmcnt) instead of
 // vector loads whose vmcnt wait would drain the page ring.
-template <int DT, int D>
+template <class Ops>
 __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kernel(
     DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ ctx) {
-  using Ops = TileOps<DT, D>;
   using E = typename Ops::E;
-  using VChunk = typename Ops::VChunk;
-  constexpr int KLD = Ops::KLD, NB = Ops::NB;
+  constexpr int D = Ops::kD, NB = Ops::NB;
   extern __shared__ int32_t s_pref[];  // [B + 1] page prefix, then [kStreamThreads] scan scratch
   int32_t* s_scan = s_pref + a.batch + 1;
 
@@ -529,14 +648,13 @@ __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kern
   //    drain the ring before every tile.
   Cursor lc = c0r, cc = c0r;
   int issued = 0;
-  Chunk16 qb[kPageBufs][KLD];
-  Chunk16 kb[kPageBufs][KLD];
-  VChunk vb[kPageBufs][NB];
+  typename Ops::QReg qb[kPageBufs];
+  typename Ops::TileReg tb[kPageBufs];
   int64_t pb[kPageBufs];
   auto issue = [&](int s) {
     Ops::load_q(a, lc.b, lc.h, ln, lq, qb[s]);
-    pb[s] = Ops::phys_page(a, bt, lc.b, logical_page(lc.w, lc.v));
-    Ops::load_tile(a, pb[s], lc.h, ln, lq, kb[s], vb[s]);
+    pb[s] = phys_page(a, bt, lc.b, logical_page(lc.w, lc.v));
+    Ops::load_tile(a, pb[s], lc.h, ln, lq, tb[s]);
     if (++issued < count) advance(lc);
   };
 #pragma unroll
@@ -556,7 +674,7 @@ __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kern
         frag_first = cc.v;
         fresh = false;
       }
-      Ops::score(st, kb[s], vb[s], qb[s], cc.w, logical_page(cc.w, cc.v), live && pb[s] >= 0, a, lq);
+      Ops::score(st, tb[s], qb[s], cc.w, logical_page(cc.w, cc.v), live && pb[s] >= 0, a, lq);
       if (live) {
         const bool unit_end = cc.v == cc.n - 1;
         if (unit_end || i + s == count - 1) {
@@ -764,14 +882,18 @@ void launch_partial(int D, dim3 grid, size_t smem, hipStream_t stream, const Dec
   }
 }
 
-template <int DT>
+// The walk for pools of the query dtype, or of FP8 with per-slot scales.
+template <int DT, bool kFp8, int D>
+using WalkOps = typename std::conditional<kFp8, TileOps8<DT, D>, TileOps<DT, D>>::type;
+
+template <int DT, bool kFp8 = false>
 void launch_stream(Stage stage, int D, dim3 grid, size_t smem, hipStream_t stream,
                    const DecodeArgs& a) {
   if (stage != kMerge) {
     switch (D) {
-      case 64: decode_stream_kernel<DT, 64><<<grid, kStreamThreads, smem, stream>>>(a, a.bt, a.ctx); break;
-      case 128: decode_stream_kernel<DT, 128><<<grid, kStreamThreads, smem, stream>>>(a, a.bt, a.ctx); break;
-      default: decode_stream_kernel<DT, 256><<<grid, kStreamThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+      case 64: decode_stream_kernel<WalkOps<DT, kFp8, 64>><<<grid, kStreamThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+      case 128: decode_stream_kernel<WalkOps<DT, kFp8, 128>><<<grid, kStreamThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+      default: decode_stream_kernel<WalkOps<DT, kFp8, 256>><<<grid, kStreamThreads, smem, stream>>>(a, a.bt, a.ctx); break;
     }
   }
   // Merge grid: (kv head, sequence, column split) with one output element per
@@ -805,8 +927,18 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
                  void* out, void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
                  int num_kv_heads, int head_dim, int block_size, int max_blocks, int num_pages,
                  float scale, int window, int n_sink, int partition_pages, int dtype,
-                 hipStream_t stream, const void* k_new = nullptr, const void* v_new = nullptr) {
+                 hipStream_t stream, const void* k_new = nullptr, const void* v_new = nullptr,
+                 const float* k_scale = nullptr, const float* v_scale = nullptr, bool fp8 = false) {
   if (dtype_size(dtype) == 0) return fail(IVAKV_E_DTYPE, "%s: unknown dtype code %d", name, dtype);
+  if (fp8) {
+    if (dtype != IVAKV_F16 && dtype != IVAKV_BF16)
+      return fail(IVAKV_E_DTYPE, "%s: FP8 pools take fp16 or bf16 queries (dtype %d)", name, dtype);
+    if (partition_pages > 0 || batch > kMaxStreamBatch)
+      return fail(IVAKV_E_ARG, "%s: FP8 pools use the stream walk (partition_pages <= 0, "
+                  "batch <= %d)", name, kMaxStreamBatch);
+    if (batch > 0 && (!k_scale || !v_scale || !aligned16(k_scale) || !aligned16(v_scale)))
+      return fail(IVAKV_E_ARG, "%s: k_scale / v_scale must be 16-byte aligned device pointers", name);
+  }
   Plan plan;
   int st = make_plan(name, stage, batch, num_q_heads, num_kv_heads, head_dim, block_size,
                      max_blocks, window, n_sink, partition_pages, &plan);
@@ -853,15 +985,23 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
   a.k_new = k_new;
   a.v_new = v_new;
   a.fused = stage == kFused;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
 
   if (plan.stream) {
     const int wgs = stream_workgroups();
     a.n_waves = wgs * kStreamWaves;
     const size_t smem = sizeof(int32_t) * ((size_t)batch + 1 + kStreamThreads);
+    const dim3 grid((unsigned)wgs);
+    if (fp8) {
+      if (dtype == IVAKV_F16) launch_stream<IVAKV_F16, true>(stage, head_dim, grid, smem, stream, a);
+      else launch_stream<IVAKV_BF16, true>(stage, head_dim, grid, smem, stream, a);
+      return launch_status(name);
+    }
     switch (dtype) {
-      case IVAKV_F16: launch_stream<IVAKV_F16>(stage, head_dim, dim3((unsigned)wgs), smem, stream, a); break;
-      case IVAKV_BF16: launch_stream<IVAKV_BF16>(stage, head_dim, dim3((unsigned)wgs), smem, stream, a); break;
-      default: launch_stream<IVAKV_F32>(stage, head_dim, dim3((unsigned)wgs), smem, stream, a); break;
+      case IVAKV_F16: launch_stream<IVAKV_F16>(stage, head_dim, grid, smem, stream, a); break;
+      case IVAKV_BF16: launch_stream<IVAKV_BF16>(stage, head_dim, grid, smem, stream, a); break;
+      default: launch_stream<IVAKV_F32>(stage, head_dim, grid, smem, stream, a); break;
     }
     return launch_status(name);
   }
@@ -938,4 +1078,17 @@ extern "C" int ivakv_decode_append_attn(const void* q, const void* k_new, const 
                       context_lens, out, workspace, workspace_bytes, batch, num_q_heads,
                       num_kv_heads, head_dim, block_size, max_blocks, num_pages, scale, window,
                       n_sink, 0, dtype, stream, k_new, v_new);
+}
+
+extern "C" int ivakv_decode_attn_fp8(const void* q, const void* k_pool, const void* v_pool,
+                                     const float* k_scale, const float* v_scale,
+                                     const int32_t* block_tables, const int32_t* context_lens,
+                                     void* out, void* workspace, size_t workspace_bytes,
+                                     int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                     int block_size, int max_blocks, int num_pages, float scale,
+                                     int window, int n_sink, int dtype, hipStream_t stream) {
+  return decode_entry(kFull, "ivakv_decode_attn_fp8", q, k_pool, v_pool, block_tables,
+                      context_lens, out, workspace, workspace_bytes, batch, num_q_heads,
+                      num_kv_heads, head_dim, block_size, max_blocks, num_pages, scale, window,
+                      n_sink, 0, dtype, stream, nullptr, nullptr, k_scale, v_scale, true);
 }

@@ -5,9 +5,11 @@ kernels on the current HIP stream of the tensors' device.  Nothing falls back
 to another implementation: a CPU tensor, an unsupported dtype or a missing
 library raises.
 
-Pool layout (X = 16 bytes / element size, e.g. 8 for fp16, 4 for fp32):
+Pool layout (X = 16 bytes / element size, e.g. 8 for fp16, 4 for fp32, 16 for fp8):
     k_pool: [num_pages, Hkv, D // X, block_size, X]
     v_pool: [num_pages, Hkv, D, block_size]
+FP8 pools (torch.float8_e4m3fn) carry one fp32 scaling factor per (slot, kv head):
+    k_scale, v_scale: [num_pages, Hkv, block_size]; a row reads back as code / scale.
 """
 from __future__ import annotations
 
@@ -19,6 +21,31 @@ import torch
 from . import _abi
 
 _DTYPE_CODES = {torch.float32: _abi.F32, torch.float16: _abi.F16, torch.bfloat16: _abi.BF16}
+
+
+FP8 = torch.float8_e4m3fn
+
+
+def is_fp8(t: torch.Tensor) -> bool:
+    return t.dtype == FP8
+
+
+def scale_shape(num_pages: int, num_kv_heads: int, block_size: int = 16) -> Tuple[int, int, int]:
+    """Shape of the per-(slot, kv head) scaling factors of an FP8 pool."""
+    return (num_pages, num_kv_heads, block_size)
+
+
+def _scales(k_pool, k_scale, v_scale):
+    """Checks the scaling-factor tensors of an FP8 pool pair."""
+    if k_scale is None or v_scale is None:
+        raise ValueError("FP8 pools need k_scale and v_scale ([num_pages, Hkv, block_size] fp32)")
+    shape = (k_pool.shape[0], k_pool.shape[1], k_pool.shape[3])
+    for name, t in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if tuple(t.shape) != shape or t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 tensor of shape {shape}")
+        if t.device != k_pool.device:
+            raise RuntimeError(f"{name} on {t.device}, pools on {k_pool.device}")
+    return k_scale, v_scale
 
 
 def dtype_code(dtype: torch.dtype) -> int:
@@ -81,14 +108,18 @@ def _i32(t: torch.Tensor, name: str) -> torch.Tensor:
 
 
 def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
-              slot_mapping: torch.Tensor) -> None:
+              slot_mapping: torch.Tensor, k_scale: Optional[torch.Tensor] = None,
+              v_scale: Optional[torch.Tensor] = None) -> None:
     """Scatters rows ``k_new[t], v_new[t]`` ([n_tok, Hkv, D], last dim contiguous) into
     ``slot_mapping[t]`` of the pools, in place.  A slot of -1 (or any slot outside the
-    pool) leaves the pools untouched for that token.
+    pool) leaves the pools untouched for that token.  FP8 pools quantize each (token,
+    kv head) row with its own scaling factor, written to ``k_scale`` / ``v_scale``.
 
     Paged counterpart of ``KVCache.update`` (src/core/rope_kv.py:98-110) and the
     ``torch.cat`` append of ``AttentionTorch.forward`` (src/core/attention.py:61-63).
     """
+    if is_fp8(k_pool):
+        return _append_fp8(k_new, v_new, k_pool, v_pool, slot_mapping, k_scale, v_scale)
     dev = _require_gpu(k_new, v_new, k_pool, v_pool, slot_mapping)
     num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
     if k_new.dim() != 3 or tuple(k_new.shape) != tuple(v_new.shape):
@@ -115,15 +146,20 @@ def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor, v_
 
 def kv_gather(k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Tensor,
               context_lens: torch.Tensor, out_len: Optional[int] = None,
-              out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
-              ) -> Tuple[torch.Tensor, torch.Tensor]:
+              out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+              k_scale: Optional[torch.Tensor] = None, v_scale: Optional[torch.Tensor] = None,
+              out_dtype: Optional[torch.dtype] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Gathers each sequence's pages back into contiguous ``[B, Hkv, out_len, D]`` K and V
     (pool dtype).  Rows at or beyond ``context_lens[b]`` are zero.  ``out_len`` defaults to
-    ``block_tables.shape[1] * block_size``.
+    ``block_tables.shape[1] * block_size``.  FP8 pools are dequantized (code / scale) into
+    ``out_dtype`` (default float16).
 
     Paged counterpart of ``KVCache.get_slice`` (src/core/rope_kv.py:136-137) and the gather
     branch of ``KVOpsTriton`` (src/kernels_t/kv_ops_triton.py:111-123).
     """
+    if is_fp8(k_pool):
+        return _gather_fp8(k_pool, v_pool, block_tables, context_lens, out_len, out, k_scale,
+                           v_scale, out_dtype or torch.float16)
     dev = _require_gpu(k_pool, v_pool, block_tables, context_lens)
     num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
     block_tables = _i32(block_tables, "block_tables")
@@ -173,13 +209,18 @@ def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
 
 
 def _decode(entry: str, q, k_pool, v_pool, block_tables, context_lens, scale, window, n_sink,
-            partition_pages, out, workspace):
+            partition_pages, out, workspace, scales=None):
     dev = _require_gpu(q, k_pool, v_pool, block_tables, context_lens)
     num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
     if q.dim() != 3 or q.shape[2] != head_dim:
         raise ValueError(f"q must be [B, Hq, {head_dim}]; got {tuple(q.shape)}")
-    if q.dtype != k_pool.dtype:
+    if scales is not None:
+        if q.dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError(f"FP8 pools take float16 or bfloat16 queries, got {q.dtype}")
+    elif q.dtype != k_pool.dtype:
         raise TypeError(f"q dtype {q.dtype} != pool dtype {k_pool.dtype}")
+    elif is_fp8(k_pool):
+        raise ValueError("FP8 pools need k_scale / v_scale")
     batch, hq, _ = q.shape
     block_tables = _i32(block_tables, "block_tables")
     context_lens = _i32(context_lens, "context_lens").reshape(-1)
@@ -203,6 +244,14 @@ def _decode(entry: str, q, k_pool, v_pool, block_tables, context_lens, scale, wi
     elif workspace.numel() * workspace.element_size() < nbytes:
         raise ValueError(f"workspace has {workspace.numel() * workspace.element_size()} bytes, "
                          f"{nbytes} needed")
+    if scales is not None:
+        _abi.call(entry, q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+                  scales[0].data_ptr(), scales[1].data_ptr(), block_tables.data_ptr(),
+                  context_lens.data_ptr(), out.data_ptr(), workspace.data_ptr(),
+                  workspace.numel() * workspace.element_size(), batch, hq, hkv, head_dim, bs,
+                  max_blocks, num_pages, float(scale), window, n_sink, dtype_code(q.dtype),
+                  _stream(dev))
+        return out
     _abi.call(entry, q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), block_tables.data_ptr(),
               context_lens.data_ptr(), out.data_ptr(), workspace.data_ptr(),
               workspace.numel() * workspace.element_size(), batch, hq, hkv, head_dim, bs,
@@ -216,7 +265,9 @@ def paged_decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
                            scale: Optional[float] = None, window: Optional[int] = None,
                            n_sink: int = 0, partition_pages: Optional[int] = None,
                            out: Optional[torch.Tensor] = None,
-                           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                           workspace: Optional[torch.Tensor] = None,
+                           k_scale: Optional[torch.Tensor] = None,
+                           v_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Single-query attention over paged K/V: ``q`` is ``[B, Hq, D]``; returns ``[B, Hq, D]``.
 
     Sequence b attends to positions ``j < context_lens[b]`` that lie in the sliding window
@@ -224,8 +275,17 @@ def paged_decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
     attention-sink positions.  Query head h reads KV head ``h // (Hq // Hkv)``.
     ``scale`` defaults to ``1/sqrt(D)`` as in ``AttentionTorch`` (src/core/attention.py:35).
 
+    FP8 pools (``torch.float8_e4m3fn`` with ``k_scale`` / ``v_scale``) take fp16 or bf16
+    queries and attend over the dequantized keys and values.
+
     Replaces the cache branch of ``AttentionTorch.forward`` (src/core/attention.py:77-102).
     """
+    if is_fp8(k_pool):
+        if partition_pages:
+            raise ValueError("FP8 pools use the stream walk (partition_pages must be 0/None)")
+        return _decode("ivakv_decode_attn_fp8", q, k_pool, v_pool, block_tables, context_lens,
+                       scale, window, n_sink, None, out, workspace,
+                       scales=_scales(k_pool, k_scale, v_scale))
     return _decode("ivakv_decode_attn", q, k_pool, v_pool, block_tables, context_lens, scale,
                    window, n_sink, partition_pages, out, workspace)
 
@@ -299,6 +359,61 @@ def paged_decode_append_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: t
               max_blocks, num_pages, float(scale), window, n_sink, dtype_code(q.dtype),
               _stream(dev))
     return out
+
+
+def _append_fp8(k_new, v_new, k_pool, v_pool, slot_mapping, k_scale, v_scale) -> None:
+    dev = _require_gpu(k_new, v_new, k_pool, v_pool, slot_mapping)
+    num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
+    k_scale, v_scale = _scales(k_pool, k_scale, v_scale)
+    if k_new.dim() != 3 or tuple(k_new.shape) != tuple(v_new.shape):
+        raise ValueError(f"k_new/v_new must be [n_tok, Hkv, D]; got {tuple(k_new.shape)} and {tuple(v_new.shape)}")
+    n_tok = k_new.shape[0]
+    if k_new.shape[1:] != (hkv, head_dim):
+        raise ValueError(f"new rows are {tuple(k_new.shape[1:])}, pool holds ({hkv}, {head_dim})")
+    if k_new.dtype != v_new.dtype:
+        raise TypeError("k_new and v_new dtypes differ")
+    code = dtype_code(k_new.dtype)
+    slot_mapping = _i32(slot_mapping, "slot_mapping").reshape(-1)
+    if slot_mapping.numel() != n_tok:
+        raise ValueError(f"slot_mapping has {slot_mapping.numel()} entries for {n_tok} tokens")
+    if n_tok == 0:
+        return
+    if k_new.stride(2) != 1:
+        k_new = k_new.contiguous()
+    if v_new.stride(2) != 1:
+        v_new = v_new.contiguous()
+    _abi.call("ivakv_append_fp8", k_new.data_ptr(), v_new.data_ptr(),
+              k_new.stride(0), k_new.stride(1), v_new.stride(0), v_new.stride(1),
+              k_pool.data_ptr(), v_pool.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
+              slot_mapping.data_ptr(), n_tok, hkv, head_dim, bs, num_pages, code, _stream(dev))
+
+
+def _gather_fp8(k_pool, v_pool, block_tables, context_lens, out_len, out, k_scale, v_scale,
+                out_dtype):
+    dev = _require_gpu(k_pool, v_pool, block_tables, context_lens)
+    num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
+    k_scale, v_scale = _scales(k_pool, k_scale, v_scale)
+    block_tables = _i32(block_tables, "block_tables")
+    context_lens = _i32(context_lens, "context_lens").reshape(-1)
+    if block_tables.dim() != 2 or block_tables.shape[0] != context_lens.numel():
+        raise ValueError("block_tables must be [B, max_blocks] with B == len(context_lens)")
+    batch, max_blocks = block_tables.shape
+    if out_len is None:
+        out_len = max_blocks * bs
+    shape = (batch, hkv, out_len, head_dim)
+    if out is None:
+        k_out = torch.empty(shape, dtype=out_dtype, device=dev)
+        v_out = torch.empty(shape, dtype=out_dtype, device=dev)
+    else:
+        k_out, v_out = out
+        for t in (k_out, v_out):
+            if tuple(t.shape) != shape or not t.is_contiguous():
+                raise ValueError(f"gather outputs must be contiguous {shape}")
+    _abi.call("ivakv_gather_fp8", k_pool.data_ptr(), v_pool.data_ptr(), k_scale.data_ptr(),
+              v_scale.data_ptr(), block_tables.data_ptr(), context_lens.data_ptr(), batch,
+              max_blocks, hkv, head_dim, bs, num_pages, out_len, k_out.data_ptr(),
+              v_out.data_ptr(), dtype_code(k_out.dtype), _stream(dev))
+    return k_out, v_out
 
 
 def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,

@@ -275,6 +275,102 @@ def prefill_attention(q: np.ndarray, k_pool: np.ndarray, v_pool: np.ndarray,
     return out
 
 
+# ---------------------------------------------------------------------------- FP8 pools
+#
+# kv_cache_dtype "fp8" (configs/quant_infer.yaml:22,52) as OCP e4m3fn codes, the format
+# of torch.float8_e4m3fn that the reference's FP8 runtime uses
+# (src/quant/fp8_runtime.py:34), with the reference's scaling rule sf = 448 / amax,
+# 1 for amax == 0, clamped to [1e-8, 1e8] (fp8_runtime.py:66-76), applied per
+# (token, kv head) row: codes = e4m3(x * sf), read back as code / sf.
+
+FP8_MAX = np.float32(448.0)
+
+
+def e4m3_encode(x) -> np.ndarray:
+    """float32 -> e4m3fn codes: round to nearest even, saturating at +-448; NaN -> 0x7F."""
+    x = np.asarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.int64)
+    sign = (u >> 24) & 0x80
+    au = u & 0x7FFFFFFF
+    a = au.astype(np.uint32).view(np.float32)
+    sub = a < np.float32(2.0 ** -6)
+    code_sub = np.rint(np.where(sub, a, 0) * np.float32(512.0)).astype(np.int64)  # step 2^-9
+    r = (au + 0x7FFFF + ((au >> 20) & 1)) >> 20  # 3 mantissa bits, RNE, exponent carried
+    code_n = np.where(r >= 960 + 0x7F, 0x7E, r - 960)  # rebias 127 -> 7
+    code = np.minimum(np.where(sub, code_sub, code_n), 0x7E)
+    code = np.where(au > 0x7F800000, 0x7F, code)
+    return (code | sign).astype(np.uint8)
+
+
+def e4m3_decode(codes) -> np.ndarray:
+    """e4m3fn codes -> float32, exactly (0x7F / 0xFF are NaN)."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    e, m = (c >> 3) & 0xF, c & 7
+    normal = ((e + 120) << 23) | (m << 20)
+    v = np.where(e == 0, m.astype(np.float32) * np.float32(2.0 ** -9),
+                 normal.astype(np.uint32).view(np.float32))
+    v = np.where((e == 15) & (m == 7), np.float32(np.nan), v).astype(np.float32)
+    return np.where(c & 0x80, -v, v).astype(np.float32)
+
+
+def row_scale(amax) -> np.ndarray:
+    """Scaling factor of rows with max |x| = amax (float32)."""
+    amax = np.asarray(amax, dtype=np.float32)
+    with np.errstate(divide="ignore"):
+        sf = np.where(amax > 0, FP8_MAX / np.where(amax > 0, amax, np.float32(1)), np.float32(1))
+    return np.clip(sf, np.float32(1e-8), np.float32(1e8)).astype(np.float32)
+
+
+def quantize_rows(x: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
+    """Rows over the last axis: (codes, sf) with codes = e4m3(x * sf) in float32."""
+    x = np.asarray(x, dtype=np.float32)
+    sf = row_scale(np.abs(x).max(axis=-1))
+    return e4m3_encode(x * sf[..., None]), sf
+
+
+def empty_scales(num_pages: int, hkv: int, block_size: int) -> np.ndarray:
+    return np.ones((num_pages, hkv, block_size), dtype=np.float32)
+
+
+def append_fp8(k_pool: np.ndarray, v_pool: np.ndarray, k_scale: np.ndarray, v_scale: np.ndarray,
+               k_new: np.ndarray, v_new: np.ndarray, slot_mapping: np.ndarray) -> None:
+    """In place: each (token, kv head) row of ``k_new/v_new`` quantized with its own scaling
+    factor; codes go where :func:`append` puts a row, factors to ``[page, head, row]``."""
+    kc, ksf = quantize_rows(k_new)
+    vc, vsf = quantize_rows(v_new)
+    append(k_pool, v_pool, kc, vc, slot_mapping)
+    num_pages, hkv, _, bs, _ = k_pool.shape
+    slots = np.asarray(slot_mapping, dtype=np.int64).reshape(-1)
+    ok = (slots >= 0) & (slots < num_pages * bs)
+    ts = np.nonzero(ok)[0]
+    page, off = slots[ts] // bs, slots[ts] % bs
+    k_scale[page, :, off] = ksf[ts]
+    v_scale[page, :, off] = vsf[ts]
+
+
+def dequantize_pools(k_pool: np.ndarray, v_pool: np.ndarray, k_scale: np.ndarray,
+                     v_scale: np.ndarray, dtype=np.float32) -> Tuple[np.ndarray, np.ndarray]:
+    """FP8 pools as pools of ``dtype`` with the same layout: code / sf (float32 division)."""
+    k = e4m3_decode(k_pool) / k_scale[:, :, None, :, None]
+    v = e4m3_decode(v_pool) / v_scale[:, :, None, :]
+    return k.astype(dtype), v.astype(dtype)
+
+
+def gather_fp8(k_pool, v_pool, k_scale, v_scale, block_tables, ctx_lens,
+               out_len: Optional[int] = None) -> Tuple[np.ndarray, np.ndarray]:
+    """:func:`gather` of the dequantized FP8 pools (float32)."""
+    kd, vd = dequantize_pools(k_pool, v_pool, k_scale, v_scale)
+    return gather(kd, vd, block_tables, ctx_lens, out_len)
+
+
+def decode_attention_fp8(q, k_pool, v_pool, k_scale, v_scale, block_tables, ctx_lens,
+                         scale: Optional[float] = None, window: int = 0,
+                         n_sink: int = 0) -> np.ndarray:
+    """:func:`decode_attention` over the dequantized FP8 pools."""
+    kd, vd = dequantize_pools(k_pool, v_pool, k_scale, v_scale, np.float64)
+    return decode_attention(q, kd, vd, block_tables, ctx_lens, scale, window, n_sink)
+
+
 def index_gather(kv: np.ndarray, indices: np.ndarray) -> np.ndarray:
     """``out[b, h, j] = kv[b, h, indices[j]]`` (kv_gather_kernel, kv_ops_triton.py:33-40)."""
     return kv[:, :, np.asarray(indices, dtype=np.int64), :].copy()

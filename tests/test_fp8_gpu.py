@@ -1,0 +1,158 @@
+"""FP8 (OCP e4m3fn) KV pages on the GPU vs the CPU oracle.
+
+  * append: codes and per-(slot, kv head) scaling factors bit-exact (untouched bytes
+    and factors unchanged), for fp32 / fp16 / bf16 source rows over six decades of
+    row magnitude, all-zero rows and skipped slots;
+  * gather: dequantized rows exact (float32 division, then the output cast), and all
+    256 codes decode as torch.float8_e4m3fn does;
+  * decode attention over FP8 pages (unit-scale data, as the other attention tests):
+    within 2e-3 (+ one half-ulp of the output dtype times |exact|) of the fp64 oracle on
+    the dequantized pages, fp16 and bf16 queries, windows and sinks, invalid page ids,
+    garbage (NaN included) codes past the context.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_kv as orc
+
+pytestmark = pytest.mark.gpu
+
+FP8 = torch.float8_e4m3fn
+OUT_ULP = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}
+
+
+def u8(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().view(torch.uint8).numpy()
+
+
+def fp8_case(iva, lengths, hkv, d, src_dtype, seed, extra_pages=3, decades=6.0):
+    """Rows of magnitude 10^U(-decades/2, decades/2) (decades=0: N(0, 1/d) rows, the
+    scale of the other attention tests), written over garbage codes and factors."""
+    gen = torch.Generator().manual_seed(seed)
+    need = sum(math.ceil(n / 16) for n in lengths)
+    num_pages = need + extra_pages
+    layout = iva.workloads.permuted_layout(lengths, num_pages, gen)
+    ks, vs = iva.pool_shapes(num_pages, hkv, d, 16, FP8)
+    k_pool = torch.randint(0, 256, ks, dtype=torch.uint8, generator=gen)  # garbage codes
+    v_pool = torch.randint(0, 256, vs, dtype=torch.uint8, generator=gen)
+    k_scale = torch.rand(iva.scale_shape(num_pages, hkv), generator=gen) + 0.5
+    v_scale = torch.rand(iva.scale_shape(num_pages, hkv), generator=gen) + 0.5
+    n_tok = sum(lengths)
+    mag = 10.0 ** ((torch.rand(n_tok, hkv, 1, generator=gen) - 0.5) * decades) if decades \
+        else torch.full((n_tok, hkv, 1), d ** -0.5)
+    k_new = (torch.randn(n_tok, hkv, d, generator=gen) * mag).to(src_dtype)
+    v_new = (torch.randn(n_tok, hkv, d, generator=gen) * mag).to(src_dtype)
+    if n_tok > 5:
+        k_new[5] = 0
+    slots = torch.cat([layout.slots(b, torch.arange(n)) for b, n in enumerate(lengths)])
+    return dict(layout=layout, k_pool=k_pool, v_pool=v_pool, k_scale=k_scale, v_scale=v_scale,
+                k_new=k_new, v_new=v_new, slots=slots, num_pages=num_pages)
+
+
+def append_both(iva, dev, c, slots=None):
+    """The same append on the GPU and in the oracle; returns (gpu tensors, oracle arrays)."""
+    slots = c["slots"] if slots is None else slots
+    g = {k: c[k].clone().to(dev) for k in ("k_pool", "v_pool", "k_scale", "v_scale")}
+    g["k_pool"], g["v_pool"] = g["k_pool"].view(FP8), g["v_pool"].view(FP8)
+    iva.kv_append(c["k_new"].to(dev), c["v_new"].to(dev), g["k_pool"], g["v_pool"],
+                  slots.to(dev), k_scale=g["k_scale"], v_scale=g["v_scale"])
+    o = dict(k_pool=c["k_pool"].numpy().copy(), v_pool=c["v_pool"].numpy().copy(),
+             k_scale=c["k_scale"].numpy().copy(), v_scale=c["v_scale"].numpy().copy())
+    orc.append_fp8(o["k_pool"], o["v_pool"], o["k_scale"], o["v_scale"],
+                   c["k_new"].float().numpy(), c["v_new"].float().numpy(), slots.numpy())
+    return g, o
+
+
+@pytest.mark.parametrize("src", [torch.float32, torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_append_fp8_bit_exact(iva, dev, src, d):
+    c = fp8_case(iva, [17, 40, 3], 4, d, src, seed=d)
+    slots = c["slots"].clone()
+    slots[7] = -1
+    slots[9] = c["num_pages"] * 16 + 3  # outside the pool: skipped
+    g, o = append_both(iva, dev, c, slots)
+    torch.cuda.synchronize()
+    assert np.array_equal(u8(g["k_pool"]), o["k_pool"])
+    assert np.array_equal(u8(g["v_pool"]), o["v_pool"])
+    assert np.array_equal(g["k_scale"].cpu().numpy(), o["k_scale"])
+    assert np.array_equal(g["v_scale"].cpu().numpy(), o["v_scale"])
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16], ids=str)
+def test_gather_fp8_exact(iva, dev, out_dtype):
+    c = fp8_case(iva, [17, 40, 3, 0], 2, 128, torch.float16, seed=3)
+    g, o = append_both(iva, dev, c)
+    lay = c["layout"]
+    bt = lay.block_tables.clone()
+    bt[1, 1] = -1
+    ko, vo = iva.kv_gather(g["k_pool"], g["v_pool"], bt.to(dev), lay.context_lens.to(dev),
+                           out_len=48, k_scale=g["k_scale"], v_scale=g["v_scale"],
+                           out_dtype=out_dtype)
+    rk, rv = orc.gather_fp8(o["k_pool"], o["v_pool"], o["k_scale"], o["v_scale"], bt.numpy(),
+                            lay.context_lens.numpy(), out_len=48)
+    exp_k = torch.from_numpy(rk).to(out_dtype)
+    exp_v = torch.from_numpy(rv).to(out_dtype)
+    assert torch.equal(ko.cpu(), exp_k) and torch.equal(vo.cpu(), exp_v)
+
+
+def test_all_codes_decode_as_torch(iva, dev):
+    """Every code (each appears 16 times in one page, factor 1) gathers as
+    torch.float8_e4m3fn converts it."""
+    ks, vs = iva.pool_shapes(1, 1, 256, 16, FP8)
+    kb = (torch.arange(4096) % 256).to(torch.uint8).reshape(ks)   # [1, 1, 16, 16, 16]
+    vb = (torch.arange(4096) * 7 % 256).to(torch.uint8).reshape(vs)  # [1, 1, 256, 16]
+    scale = torch.ones(1, 1, 16)
+    ko, vo = iva.kv_gather(kb.view(FP8).to(dev), vb.view(FP8).to(dev),
+                           torch.zeros(1, 1, dtype=torch.int32, device=dev),
+                           torch.tensor([16], dtype=torch.int32, device=dev), out_len=16,
+                           k_scale=scale.to(dev), v_scale=scale.to(dev), out_dtype=torch.float32)
+    kref = kb.view(FP8).float()[0, 0].permute(1, 0, 2).reshape(16, 256)  # [row, dim]
+    vref = vb.view(FP8).float()[0, 0].t()
+    for got, exp in ((ko[0, 0].cpu(), kref), (vo[0, 0].cpu(), vref)):
+        assert torch.equal(torch.isnan(got), torch.isnan(exp))
+        assert torch.equal(got[~torch.isnan(got)], exp[~torch.isnan(exp)])
+
+
+@pytest.mark.parametrize("qdt", [torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("window,sink", [(0, 0), (70, 4)])
+def test_decode_fp8_vs_oracle(iva, dev, qdt, d, window, sink):
+    lengths = [1, 16, 17, 100, 257, 513]
+    hq, hkv = 8, 2
+    c = fp8_case(iva, lengths, hkv, d, torch.float32, seed=11 + d, decades=0)
+    g, o = append_both(iva, dev, c)
+    lay = c["layout"]
+    bt = lay.block_tables.clone()
+    bt[4, 3] = -1                     # an invalid page inside a context
+    q = (torch.randn(len(lengths), hq, d, generator=torch.Generator().manual_seed(5)) * d ** -0.5).to(qdt)
+    out = iva.paged_decode_attention(q.to(dev), g["k_pool"], g["v_pool"], bt.to(dev),
+                                     lay.context_lens.to(dev), window=window, n_sink=sink,
+                                     k_scale=g["k_scale"], v_scale=g["v_scale"])
+    ref = orc.decode_attention_fp8(q.float().numpy(), o["k_pool"], o["v_pool"], o["k_scale"],
+                                   o["v_scale"], bt.numpy(), lay.context_lens.numpy(),
+                                   window=window, n_sink=sink)
+    err = np.abs(out.float().cpu().numpy() - ref)
+    bound = 2e-3 + OUT_ULP[qdt] * np.abs(ref)
+    assert (err <= bound).all(), f"max err {err.max():.3e}"
+
+
+def test_fp8_argument_errors(iva, dev):
+    c = fp8_case(iva, [20], 2, 64, torch.float16, seed=1)
+    g, _ = append_both(iva, dev, c)
+    lay = c["layout"]
+    q = torch.randn(1, 4, 64, device=dev).half()
+    args = (q, g["k_pool"], g["v_pool"], lay.block_tables.to(dev), lay.context_lens.to(dev))
+    with pytest.raises(ValueError, match="k_scale"):
+        iva.paged_decode_attention(*args)
+    with pytest.raises(TypeError, match="float16 or bfloat16"):
+        iva.paged_decode_attention(q.float(), *args[1:], k_scale=g["k_scale"], v_scale=g["v_scale"])
+    with pytest.raises(ValueError, match="stream walk"):
+        iva.paged_decode_attention(*args, partition_pages=8, k_scale=g["k_scale"], v_scale=g["v_scale"])
+    with pytest.raises(ValueError, match="k_scale"):
+        iva.kv_append(c["k_new"].to(dev), c["v_new"].to(dev), g["k_pool"], g["v_pool"],
+                      c["slots"].to(dev))

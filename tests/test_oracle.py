@@ -441,3 +441,63 @@ def test_prefill_planted_mistakes_are_caught(monkeypatch, mutant):
         monkeypatch.setattr(orc, "visible_at", lambda p, n, w=0, s=0: real(p - 1, n, w, s))
     results = [check(fn) for check in PF_CHECKS]
     assert not all(results), f"planted mistake {mutant} passed every prefill pin check"
+
+
+# ------------------------------------------------------------------ FP8 pools
+
+def test_e4m3_decode_matches_torch_exhaustively():
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = orc.e4m3_decode(codes)
+    assert np.array_equal(np.isnan(ref), np.isnan(got))
+    assert np.array_equal(ref[~np.isnan(ref)], got[~np.isnan(got)])
+
+
+def test_e4m3_encode_matches_torch_rounding():
+    """Every representable value, every midpoint (ties to even) and its neighbours,
+    subnormals and random values in [-448, 448] round as torch's float8_e4m3fn cast."""
+    vals = np.unique(orc.e4m3_decode(np.arange(256, dtype=np.uint8)))
+    vals = vals[~np.isnan(vals)]
+    mids = ((vals[:-1].astype(np.float64) + vals[1:]) / 2).astype(np.float32)
+    rng = np.random.default_rng(0)
+    xs = np.concatenate([vals, mids, np.nextafter(mids, np.float32(np.inf)),
+                         np.nextafter(mids, np.float32(-np.inf)),
+                         rng.uniform(-448, 448, 50000).astype(np.float32),
+                         (rng.standard_normal(20000) * 0.01).astype(np.float32),
+                         np.array([2.0 ** -10, 2.0 ** -12, 1e-30, 0.0, -0.0], np.float32)])
+    xs = xs[np.abs(xs) <= 448]
+    ref = torch.from_numpy(xs).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(orc.e4m3_encode(xs), ref)
+    # beyond +-448 this build saturates (torch's cast gives NaN from 464 on)
+    assert orc.e4m3_encode(np.array([470.0, -1e9, np.inf], np.float32)).tolist() == [0x7E, 0xFE, 0x7E]
+
+
+def test_row_scale_is_the_reference_rule():
+    """fp8_runtime.py:66-76: sf = 448 / amax, 1 for amax == 0, clamped to [1e-8, 1e8]."""
+    amax = np.array([0.0, 1.0, 448.0, 3.5, 1e-12, 1e12], np.float32)
+    exp = [1.0, 448.0, 1.0, np.float32(448.0) / np.float32(3.5), 1e8, np.float32(1e-8)]
+    assert np.array_equal(orc.row_scale(amax), np.array(exp, np.float32))
+
+
+def test_fp8_rows_round_trip_and_layout():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((40, 2, 32)) * np.array([1e-3, 50.0])[None, :, None]).astype(np.float32)
+    x[3] = 0.0
+    codes, sf = orc.quantize_rows(x)
+    back = orc.e4m3_decode(codes) / sf[..., None]
+    amax = np.abs(x).max(axis=-1, keepdims=True)
+    assert np.all(np.abs(back - x) <= 2.0 ** -4 * np.abs(x) + 2.0 ** -9 / 448 * amax + 1e-30)
+    assert np.all(codes[3] == 0) and np.all(sf[3] == 1)
+    # append_fp8 = quantize + the (pinned) append address formula + factors at [page, head, row]
+    c = rand_case(4, [7, 20], 2, 32, 16)
+    kp, vp = orc.empty_pools(c["num_pages"], 2, 32, 16, np.uint8)
+    ks, vs = orc.empty_scales(c["num_pages"], 2, 16), orc.empty_scales(c["num_pages"], 2, 16)
+    orc.append_fp8(kp, vp, ks, vs, c["k_new"], c["v_new"], c["slots"])
+    kc, ksf = orc.quantize_rows(c["k_new"])
+    kf, vf = orc.empty_pools(c["num_pages"], 2, 32, 16, np.uint8)
+    kf, vf = kf.reshape(-1), vf.reshape(-1)
+    vc, vsf = orc.quantize_rows(c["v_new"])
+    orc.append_loops(kf, vf, kc, vc, c["slots"], c["num_pages"], 2, 32, 16)
+    assert np.array_equal(kp.reshape(-1), kf) and np.array_equal(vp.reshape(-1), vf)
+    for t, s in enumerate(c["slots"]):
+        assert np.array_equal(ks[s // 16, :, s % 16], ksf[t]) and np.array_equal(vs[s // 16, :, s % 16], vsf[t])
