@@ -72,10 +72,10 @@ def parse_args():
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="write the HBM traffic summary from two rocprofv3 --pmc runs")
     p.add_argument("--c5-steps", type=int, default=40, help="timed churn steps of --workload c5")
-    p.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "prefill"), default="c2",
+    p.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "prefill", "c2fp8"), default="c2",
                    help="c2 (default): the contract line; c3 dense-decoder tokens/s, c4 "
                         "long-context window+sinks decode, c5 ragged churn, prefill: 512-token "
-                        "chunks over paged context (informational lines)")
+                        "chunks over paged context, c2fp8: C2 over FP8 pages (informational lines)")
     return p.parse_args()
 
 
@@ -256,6 +256,83 @@ def bench_c3(args, iva, torch, dev):
     }
 
 
+def bench_c2fp8(args, iva, torch, dev):
+    """C2's batch (B 32, GQA 32/8, D 128, context U[512, 4096] seed 0) over FP8 (e4m3fn)
+    pages with per-(slot, kv head) scaling factors; fp16 queries.  GB/s on the bytes the
+    FP8 walk must move (codes, factors, q, out, tables) and decode tokens/s, beside the
+    fp16-page attention of the same batch."""
+    wl = iva.workloads
+    measure = _timer(torch, dev)
+    hq, hkv, d = 32, 8, 128
+    lengths = wl.c2_lengths(seed=0)
+    batch = len(lengths)
+    sc = 1 / math.sqrt(d)
+    sets8, sets16 = [], []
+    for i in range(args.pools):
+        dd = wl.decode_batch(lengths, hq, hkv, d, torch.float16, seed=100 + i, device=dev, scale=sc)
+        lay = dd["layout"]
+        bt, ctx = lay.block_tables.to(dev), lay.context_lens.to(dev)
+        ks, vs = iva.pool_shapes(lay.num_pages, hkv, d, 16, torch.float8_e4m3fn)
+        k8 = torch.zeros(ks, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+        v8 = torch.zeros(vs, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+        kss = torch.ones(iva.scale_shape(lay.num_pages, hkv), device=dev)
+        vss = torch.ones_like(kss)
+        kc, vc = iva.kv_gather(dd["k_pool"], dd["v_pool"], bt, ctx)  # the fp16 rows, re-paged
+        slots = torch.cat([lay.slots(b, torch.arange(n)) for b, n in enumerate(lengths)]).to(dev)
+        rows_k = torch.cat([kc[b, :, :n].transpose(0, 1) for b, n in enumerate(lengths)])
+        rows_v = torch.cat([vc[b, :, :n].transpose(0, 1) for b, n in enumerate(lengths)])
+        iva.kv_append(rows_k, rows_v, k8, v8, slots, k_scale=kss, v_scale=vss)
+        del kc, vc, rows_k, rows_v
+        q, out = dd["q"], torch.empty_like(dd["q"])
+        sets8.append((q, k8, v8, bt, ctx, out, kss, vss))
+        sets16.append((q, dd["k_pool"], dd["v_pool"], bt, ctx, out))
+    ws = torch.empty(iva.decode_workspace_bytes(batch, hq, hkv, d, 16, sets8[0][3].shape[1]),
+                     dtype=torch.uint8, device=dev)
+    run8 = lambda s: iva.paged_decode_attention(s[0], s[1], s[2], s[3], s[4], out=s[5],
+                                                workspace=ws, k_scale=s[6], v_scale=s[7])
+    run16 = lambda s: iva.paged_decode_attention(s[0], s[1], s[2], s[3], s[4], out=s[5],
+                                                 workspace=ws)
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    reps = 20
+    with torch.cuda.stream(stream):
+        for s in sets8:
+            run8(s)
+        for s in sets16:
+            run16(s)
+        torch.cuda.synchronize(dev)
+        graphs = []
+        for fn, sets in ((run8, sets8), (run16, sets16)):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for r in range(reps):
+                    fn(sets[r % len(sets)])
+            graphs.append(g)
+        times = []
+        for g in graphs:
+            g.replay()
+            torch.cuda.synchronize(dev)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(10):
+                g.replay()
+            e1.record(stream)
+            torch.cuda.synchronize(dev)
+            times.append(e0.elapsed_time(e1) * 1e-3 / (10 * reps))
+    t8, t16 = times
+    tokens = sum(lengths)
+    byts = 2 * tokens * hkv * d + 2 * tokens * hkv * 4 + 2 * batch * hq * d * 2 + \
+        sum(-(-n // 16) for n in lengths) * 4 + 4 * batch
+    return {"metric": "C2 decode attention over FP8 pages GB/s (codes + factors) and tokens/s",
+            "workload": "c2fp8", "value": round(byts / t8 / 1e9, 1), "unit": "GB/s",
+            "dtype": "fp8 e4m3fn pages, f16 q/out",
+            "config": {"batch": batch, "heads": "32/8", "head_dim": d, "context": "U[512,4096] seed 0",
+                       "launch": "hip graph", "walk": "stream"},
+            "attention_us": round(t8 * 1e6, 2), "fp16_pages_attention_us": round(t16 * 1e6, 2),
+            "speedup_vs_fp16_pages": round(t16 / t8, 3), "bytes": byts,
+            "tokens_per_s": round(batch / t8, 1)}
+
+
 def bench_c4(args, iva, torch, dev):
     """C4: long-context decode, bf16, B 4 at 32k/64k/96k/128k, GQA 32/8, D 128, window
     4096 + 4 sinks (union); GB/s on attended bytes."""
@@ -376,8 +453,8 @@ def main():
     torch.cuda.set_device(dev)
     wl = iva.workloads
     if args.workload != "c2":
-        fn = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5,
-              "prefill": bench_prefill}[args.workload]
+        fn = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "prefill": bench_prefill,
+              "c2fp8": bench_c2fp8}[args.workload]
         print(json.dumps(fn(args, iva, torch, dev)), flush=True)
         return
 

@@ -176,6 +176,7 @@ struct TileOps {
   static constexpr int KLD = D / X / 4;          // K loads per lane per tile
   static constexpr int NB = D / 16;              // 16-dim blocks (PV MFMAs per tile)
   static constexpr int64_t kTile = (int64_t)D * kBS;  // elements of one tile
+  static constexpr int kRing = kPageBufs;             // stream walk: tiles in flight
   using State = SoftmaxState<NB>;
   struct QReg {
     Chunk16 c[KLD];
@@ -254,6 +255,9 @@ struct TileOps8 {
   static constexpr int KL = D / 64;   // 16-byte K loads (16 dims) per lane per tile
   static constexpr int NB = D / 16;
   static constexpr int64_t kTileBytes = (int64_t)D * kBS;
+  // The plain ring: a deeper one (as many bytes in flight as for 16-bit pages)
+  // measured slower, the FP8 walk being issue-bound rather than latency-bound.
+  static constexpr int kRing = kPageBufs;
   using State = SoftmaxState<NB>;
   struct QReg {
     Chunk16 c[2 * KL];  // c[2i + half]: dims 16 * (4i + lq) + 8 * half .. + 8
@@ -553,6 +557,7 @@ __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kern
     DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ ctx) {
   using E = typename Ops::E;
   constexpr int D = Ops::kD, NB = Ops::NB;
+  constexpr int kRing = Ops::kRing;  // tiles in flight per wave
   extern __shared__ int32_t s_pref[];  // [B + 1] page prefix, then [kStreamThreads] scan scratch
   int32_t* s_scan = s_pref + a.batch + 1;
 
@@ -640,7 +645,7 @@ __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kern
     }
   };
 
-  // 3. The ring: the load cursor runs kPageBufs tiles ahead of the compute
+  // 3. The ring: the load cursor runs kRing tiles ahead of the compute
   //    cursor.  Past the wave's last tile it stays there and re-loads it (an L2
   //    hit) into padding slots that score() masks.  Every slot also loads the
   //    query rows of its tile's unit (an L2 hit after the first): a q load only
@@ -648,9 +653,9 @@ __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kern
   //    drain the ring before every tile.
   Cursor lc = c0r, cc = c0r;
   int issued = 0;
-  typename Ops::QReg qb[kPageBufs];
-  typename Ops::TileReg tb[kPageBufs];
-  int64_t pb[kPageBufs];
+  typename Ops::QReg qb[kRing];
+  typename Ops::TileReg tb[kRing];
+  int64_t pb[kRing];
   auto issue = [&](int s) {
     Ops::load_q(a, lc.b, lc.h, ln, lq, qb[s]);
     pb[s] = phys_page(a, bt, lc.b, logical_page(lc.w, lc.v));
@@ -658,16 +663,16 @@ __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kern
     if (++issued < count) advance(lc);
   };
 #pragma unroll
-  for (int s = 0; s < kPageBufs; ++s) issue(s);
+  for (int s = 0; s < kRing; ++s) issue(s);
 
   typename Ops::State st;
   st.reset();
   bool fresh = true;   // next live tile starts a fragment
   int frag_first = 0;  // first page of the current fragment
   const int Hq = Hkv * G;
-  for (int i = 0; i < count; i += kPageBufs) {
+  for (int i = 0; i < count; i += kRing) {
 #pragma unroll
-    for (int s = 0; s < kPageBufs; ++s) {
+    for (int s = 0; s < kRing; ++s) {
       const bool live = i + s < count;
       if (live && fresh) {
         st.reset();

@@ -49,7 +49,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .ops import kv_gather, paged_decode_append_attention, paged_prefill_attention
+from .ops import (kv_gather, paged_decode_append_attention, paged_decode_attention,
+                  paged_prefill_attention)
 from .paged_cache import PagedKVCache
 
 
@@ -89,6 +90,8 @@ class TransformerConfig:
     kv_block_size: int = 16
     kv_num_pages: Optional[int] = None   # None = enough for every sequence at seq_len
     sink_tokens: int = 0                 # attention-sink tokens kept visible with the window
+    kv_cache_dtype: Optional[str] = None  # None = model dtype; "fp8" = e4m3fn pages
+                                          # (configs/quant_infer.yaml:52 memory.kv_cache_dtype)
 
     def __post_init__(self):
         if self.d_model % self.n_heads != 0:
@@ -103,6 +106,8 @@ class TransformerConfig:
             self.n_kv_heads = self.n_heads
         if self.n_heads % self.n_kv_heads != 0:
             raise ValueError(f"n_heads ({self.n_heads}) must be a multiple of n_kv_heads ({self.n_kv_heads})")
+        if self.kv_cache_dtype not in (None, "fp8"):
+            raise ValueError(f"kv_cache_dtype must be None or 'fp8', got {self.kv_cache_dtype!r}")
 
     @property
     def head_dim(self) -> int:
@@ -314,8 +319,16 @@ class PagedAttention(_AttentionBase):
             out = out.transpose(1, 2)
         else:
             decode = s == 1 and self.causal
-            view = kv_cache.layer_step(k.contiguous(), v.contiguous(), append=not decode)
-            if decode:
+            fp8 = kv_cache.pool.fp8
+            view = kv_cache.layer_step(k.contiguous(), v.contiguous(), append=fp8 or not decode)
+            if decode and fp8:
+                # FP8 pages: the append above quantized the row; attend over the pages
+                o = paged_decode_attention(
+                    q.view(b, self.n_heads, self.head_dim), view.k_pool, view.v_pool,
+                    view.block_tables, view.context_lens, scale=self.scale, window=window or 0,
+                    n_sink=n_sink if window else 0, **view.scales)
+                out = o.view(b, 1, self.n_heads, self.head_dim)
+            elif decode:
                 # append + attend in one op: the new row lands at position L-1 of each page
                 # table and is scored straight from k / v (ivakv_decode_append_attn)
                 o = paged_decode_append_attention(
@@ -324,7 +337,7 @@ class PagedAttention(_AttentionBase):
                     view.block_tables, view.context_lens, scale=self.scale, window=window or 0,
                     n_sink=n_sink if window else 0)
                 out = o.view(b, 1, self.n_heads, self.head_dim)
-            elif self.causal:
+            elif self.causal and not fp8:
                 # the chunk's rows sit at positions start .. start+s-1 of every sequence
                 qs = torch.arange(0, (b + 1) * s, s, dtype=torch.int32, device=x.device)
                 o = paged_prefill_attention(
@@ -333,10 +346,16 @@ class PagedAttention(_AttentionBase):
                     window=window or 0, n_sink=n_sink if window else 0, max_query_len=s)
                 out = o.view(b, s, self.n_heads, self.head_dim)
             else:
+                # non-causal, or a multi-token step over FP8 pages: gather (dequantized)
+                # and evaluate the masked attention of the new tokens in torch
                 total = view.start + s
+                kw = dict(view.scales, out_dtype=q.dtype) if fp8 else {}
                 kc, vc = kv_gather(view.k_pool, view.v_pool, view.block_tables,
-                                   view.context_lens, out_len=total)
-                allowed = torch.ones(s, total, dtype=torch.bool, device=x.device)
+                                   view.context_lens, out_len=total, **kw)
+                q_pos = torch.arange(view.start, total, device=x.device)
+                k_pos = torch.arange(total, device=x.device)
+                allowed = _visible(q_pos, k_pos, window, n_sink) if self.causal else \
+                    torch.ones(s, total, dtype=torch.bool, device=x.device)
                 out = _attend(q.transpose(1, 2), kc, vc, self.scale, allowed[None, None])
                 out = out.transpose(1, 2)
         out = out.reshape(b, s, self.d_model)
@@ -446,9 +465,11 @@ class Transformer(nn.Module):
         device = device or self.token_embedding.weight.device
         dtype = dtype or self.token_embedding.weight.dtype
         if cfg.attn_impl == "hip_paged":
-            cache = PagedKVCache(batch_size, cfg.n_kv_heads, cfg.head_dim, 0, device, dtype,
+            page_dtype = torch.float8_e4m3fn if cfg.kv_cache_dtype == "fp8" else dtype
+            cache = PagedKVCache(batch_size, cfg.n_kv_heads, cfg.head_dim, 0, device, page_dtype,
                                  num_layers=cfg.n_layers, block_size=cfg.kv_block_size,
-                                 max_seq_len=max_seq_len, num_pages=cfg.kv_num_pages)
+                                 max_seq_len=max_seq_len, num_pages=cfg.kv_num_pages,
+                                 compute_dtype=dtype)
             cache.resize(max_seq_len)
             return cache
         return LayeredKVCache(batch_size, cfg.n_kv_heads, cfg.head_dim, cfg.n_layers, device, dtype)

@@ -25,13 +25,13 @@ Layout of one layer's pools (X = 16 bytes / element size), see include/ivakv.h:
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
 
-from .ops import kv_append, kv_gather, pool_shapes
+from .ops import FP8, kv_append, kv_gather, pool_shapes, scale_shape
 
 
 class OutOfPagesError(RuntimeError):
@@ -77,6 +77,9 @@ class PagedKVPool:
         self.context_lens = np.zeros(self.max_seqs, dtype=np.int32)
         self.k_pools: List[torch.Tensor] = []
         self.v_pools: List[torch.Tensor] = []
+        # FP8 pools: one fp32 scaling factor per (slot, kv head) and layer
+        self.k_scales: List[torch.Tensor] = []
+        self.v_scales: List[torch.Tensor] = []
         if allocate_storage:
             ks, vs = pool_shapes(self.num_pages, self.num_kv_heads, self.head_dim,
                                  self.block_size, dtype)
@@ -84,6 +87,21 @@ class PagedKVPool:
             for _ in range(self.num_layers):
                 self.k_pools.append(torch.zeros(ks, dtype=dtype, device=self.device))
                 self.v_pools.append(torch.zeros(vs, dtype=dtype, device=self.device))
+                if self.fp8:
+                    shape = scale_shape(self.num_pages, self.num_kv_heads, self.block_size)
+                    self.k_scales.append(torch.ones(shape, dtype=torch.float32, device=self.device))
+                    self.v_scales.append(torch.ones(shape, dtype=torch.float32, device=self.device))
+
+    @property
+    def fp8(self) -> bool:
+        """Pages hold e4m3fn codes with per-(slot, kv head) scaling factors."""
+        return self.dtype == FP8
+
+    def scales(self, layer: int) -> Dict[str, Optional[torch.Tensor]]:
+        """``k_scale`` / ``v_scale`` keyword arguments of the ops for one layer."""
+        if not self.fp8:
+            return {}
+        return {"k_scale": self.k_scales[layer], "v_scale": self.v_scales[layer]}
 
     # ------------------------------------------------------------------ config
     @classmethod
@@ -92,16 +110,18 @@ class PagedKVPool:
                     max_seqs: int = 256) -> "PagedKVPool":
         """Pool sized by the ``memory`` block of configs/quant_infer.yaml:50-60:
         ``kv_cache_blocks`` pages, ``kv_cache_size`` tokens per sequence at most,
-        ``kv_cache_dtype`` the element type (fp16 / bf16 / fp32; fp8 is not built)."""
+        ``kv_cache_dtype`` the element type (fp16 / bf16 / fp32, or fp8: e4m3fn codes with
+        per-(slot, kv head) scaling factors)."""
         if not memory_cfg.get("paged_kv_cache", True):
             raise ValueError("memory.paged_kv_cache is false: use the contiguous KVCache")
         names = {"fp16": torch.float16, "float16": torch.float16, "bf16": torch.bfloat16,
-                 "bfloat16": torch.bfloat16, "fp32": torch.float32, "float32": torch.float32}
+                 "bfloat16": torch.bfloat16, "fp32": torch.float32, "float32": torch.float32,
+                 "fp8": FP8, "fp8_e4m3": FP8, "float8_e4m3fn": FP8}
         kv_dtype = memory_cfg.get("kv_cache_dtype")
         if kv_dtype is not None:
             if str(kv_dtype) not in names:
                 raise NotImplementedError(f"kv_cache_dtype {kv_dtype!r} is not supported by the "
-                                          "paged KV kernels (fp16, bf16, fp32)")
+                                          "paged KV kernels (fp16, bf16, fp32, fp8)")
             dtype = names[str(kv_dtype)]
         num_pages = int(memory_cfg.get("kv_cache_blocks", 256))
         max_tokens = int(memory_cfg.get("kv_cache_size", num_pages * block_size))
@@ -230,9 +250,8 @@ class PagedKVPool:
                 src_page = s.pages[full]
                 new_page = self._take_page()
                 d.pages.append(new_page)
-                for k, v in zip(self.k_pools, self.v_pools):
-                    k[new_page].copy_(k[src_page])
-                    v[new_page].copy_(v[src_page])
+                for t in self.k_pools + self.v_pools + self.k_scales + self.v_scales:
+                    t[new_page].copy_(t[src_page])
         except OutOfPagesError:
             self.free(dst_id)
             raise
@@ -312,6 +331,7 @@ class LayerView:
     context_lens: torch.Tensor   # int32 [B], lengths after this forward's append
     start: int                   # position of the first new token
     new_tokens: int              # T
+    scales: Dict[str, torch.Tensor] = field(default_factory=dict)  # FP8: k_scale / v_scale
 
 
 class PagedKVCache:
@@ -326,12 +346,14 @@ class PagedKVCache:
     def __init__(self, batch_size: int, n_heads: int, head_dim: int, seq_len: int = 0,
                  device=None, dtype: torch.dtype = torch.float16, *, num_layers: int = 1,
                  block_size: int = 16, max_seq_len: int = 4096, num_pages: Optional[int] = None,
-                 pool: Optional[PagedKVPool] = None):
+                 pool: Optional[PagedKVPool] = None, compute_dtype: Optional[torch.dtype] = None):
         self.batch_size = int(batch_size)
         self.n_heads = int(n_heads)
         self.head_dim = int(head_dim)
         self.device = torch.device(device) if device is not None else torch.device("cuda")
         self.dtype = dtype
+        # FP8 pages: rows written from and read back as float16 unless told otherwise
+        self.compute_dtype = compute_dtype or (torch.float16 if dtype == FP8 else dtype)
         self.num_layers = int(num_layers)
         self.block_size = int(block_size)
         if pool is None:
@@ -355,7 +377,7 @@ class PagedKVCache:
         self._static: Optional[dict] = None
         if seq_len > 0:
             z = torch.zeros(self.batch_size, self.n_heads, int(seq_len), self.head_dim,
-                            dtype=dtype, device=self.device)
+                            dtype=self.compute_dtype, device=self.device)
             for layer in range(self.num_layers):
                 self._cursor = layer
                 self._append_all(z, z, layer_only=layer, commit=layer == self.num_layers - 1)
@@ -386,7 +408,13 @@ class PagedKVCache:
         """Contiguous [B, Hkv, seq_len, D] K and V of one layer (gathered, a copy)."""
         bt, ctx = self._tables()
         return kv_gather(self.pool.k_pools[layer], self.pool.v_pools[layer], bt, ctx,
-                         out_len=self.seq_len)
+                         out_len=self.seq_len, **self._gather_kw(layer))
+
+    def _gather_kw(self, layer: int) -> dict:
+        kw = dict(self.pool.scales(layer))
+        if kw:  # FP8 pages read back in the cache's compute dtype
+            kw["out_dtype"] = self.compute_dtype
+        return kw
 
     @property
     def k(self) -> torch.Tensor:
@@ -412,6 +440,8 @@ class PagedKVCache:
             pages = [p for s in self.seq_ids for p in self.pool.pages(s) if p >= 0]
             if pages:
                 idx = torch.tensor(pages, device=k.device)
+                if self.pool.fp8:  # code 0 is +0.0 whatever the scaling factor
+                    k, v = k.view(torch.uint8), v.view(torch.uint8)
                 k.index_fill_(0, idx, 0)
                 v.index_fill_(0, idx, 0)
 
@@ -430,7 +460,7 @@ class PagedKVCache:
         rows_k = new_k.permute(0, 2, 1, 3).reshape(-1, self.n_heads, self.head_dim)
         rows_v = new_v.permute(0, 2, 1, 3).reshape(-1, self.n_heads, self.head_dim)
         kv_append(rows_k, rows_v, self.pool.k_pools[layer], self.pool.v_pools[layer],
-                  torch.from_numpy(slots).to(self.device))
+                  torch.from_numpy(slots).to(self.device), **self.pool.scales(layer))
         self.seq_len = max(self.seq_len, end)
         self._bt_pages = -1
 
@@ -536,9 +566,10 @@ class PagedKVCache:
         if append:
             kv_append(k_rows.reshape(b * t, self.n_heads, self.head_dim),
                       v_rows.reshape(b * t, self.n_heads, self.head_dim),
-                      self.pool.k_pools[layer], self.pool.v_pools[layer], slot_dev)
+                      self.pool.k_pools[layer], self.pool.v_pools[layer], slot_dev,
+                      **self.pool.scales(layer))
         view = LayerView(layer, self.pool.k_pools[layer], self.pool.v_pools[layer], slot_dev, bt,
-                         ctx, start, t)
+                         ctx, start, t, self.pool.scales(layer))
         self._cursor += 1
         if self._cursor == self.num_layers:
             self._cursor = 0
@@ -565,6 +596,6 @@ class PagedKVCache:
         kv_append(k.permute(0, 2, 1, 3).reshape(-1, self.n_heads, self.head_dim),
                   v.permute(0, 2, 1, 3).reshape(-1, self.n_heads, self.head_dim),
                   self.pool.k_pools[layer_only], self.pool.v_pools[layer_only],
-                  torch.from_numpy(slots).to(self.device))
+                  torch.from_numpy(slots).to(self.device), **self.pool.scales(layer_only))
         if commit:
             self.seq_len = t

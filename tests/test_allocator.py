@@ -117,8 +117,13 @@ def test_from_config_honours_quant_infer_memory_block(iva):
     p = pc.PagedKVPool.from_config(cfg, num_layers=2, num_kv_heads=8, head_dim=128, device="cpu")
     assert p.num_pages == 256 and p.max_blocks == 64 and p.dtype == torch.bfloat16
     assert len(p.k_pools) == 2 and p.k_pools[0].shape == (256, 8, 16, 16, 8)
-    with pytest.raises(NotImplementedError, match="fp8"):
-        pc.PagedKVPool.from_config(dict(cfg, kv_cache_dtype="fp8"), 1, 8, 128, device="cpu")
+    # kv_cache_dtype "fp8" (the file's own value): e4m3fn pages + per-(slot, head) factors
+    p8 = pc.PagedKVPool.from_config(dict(cfg, kv_cache_dtype="fp8"), 1, 8, 128, device="cpu")
+    assert p8.fp8 and p8.k_pools[0].dtype == torch.float8_e4m3fn
+    assert p8.k_pools[0].shape == (256, 8, 8, 16, 16) and p8.v_pools[0].shape == (256, 8, 128, 16)
+    assert p8.k_scales[0].shape == (256, 8, 16) and p8.k_scales[0].dtype == torch.float32
+    with pytest.raises(NotImplementedError, match="fp4"):
+        pc.PagedKVPool.from_config(dict(cfg, kv_cache_dtype="fp4"), 1, 8, 128, device="cpu")
     with pytest.raises(ValueError):
         pc.PagedKVPool.from_config(dict(cfg, paged_kv_cache=False), 1, 8, 128, device="cpu")
 

@@ -140,3 +140,21 @@ def test_graph_decode_matches_eager(M, dev):
     assert cache.seq_len == 40 + 9   # the last sampled token is not fed back
     assert all(cache.pool.length(s) == 49 for s in cache.seq_ids)
     cache.free()
+
+
+def test_fp8_kv_cache_through_the_model(M, dev):
+    """kv_cache_dtype="fp8": prefill over e4m3fn pages (gathered, dequantized) and FP8
+    decode steps.  Logits stay close to the same model with a bf16 cache (the pages are
+    quantized, so this is a closeness check, not parity); graph decode == eager."""
+    _, paged = twin_models(M, torch.bfloat16, dev)
+    _, paged8 = twin_models(M, torch.bfloat16, dev, kv_cache_dtype="fp8")
+    paged8.load_state_dict(paged.state_dict())
+    ids = torch.randint(0, 512, (4, 48 + 12), device=dev)
+    with torch.no_grad():
+        l16, _ = run_steps(paged, ids, 48, dev)
+        l8, cache = run_steps(paged8, ids, 48, dev)
+        assert cache.pool.fp8
+        assert (l16 - l8).abs().max().item() <= 0.25
+        a = paged8.generate(ids[:, :40], max_length=8, do_sample=False, eos_token_id=None, use_graph=True)
+        b = paged8.generate(ids[:, :40], max_length=8, do_sample=False, eos_token_id=None, use_graph=False)
+    assert torch.equal(a, b)
