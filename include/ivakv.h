@@ -228,6 +228,43 @@ int ivakv_decode_attn_fp8(const void* q, const void* k_pool, const void* v_pool,
                           hipStream_t stream);
 
 /*
+ * Rotary position embedding as the reference's RoPE module defines it
+ * (src/core/rope_kv.py:22-50): dims (2i, 2i+1) of a head rotate by a = p * f_i at absolute
+ * position p, f_i = 1 / theta^(2i/D) (double, stored as float), a = float(p) * f_i:
+ *   y[2i] = x[2i] cos a - x[2i+1] sin a,  y[2i+1] = x[2i] sin a + x[2i+1] cos a
+ * in fp32, rounded once to the element type.  The reference computes this state but its
+ * attention leaves q and k unrotated (attention.py:57-59,112-113); these entry points are
+ * the rotation it describes.
+ *
+ * ivakv_rope: x [n_tok][num_heads][D] (element strides per token and head), rotated in
+ * place at positions[t] (int32).  D even.
+ */
+int ivakv_rope(void* x, int64_t tok_stride, int64_t head_stride, const int32_t* positions,
+               int n_tok, int num_heads, int head_dim, float theta, int dtype,
+               hipStream_t stream);
+/*
+ * ivakv_append_rope: ivakv_append with every K row rotated at positions[t] on its way into
+ * the page (V rows unchanged).  Replaces: the k rotation of AttentionTorch.forward
+ * (attention.py:57-59) followed by the cache append (attention.py:61-63).
+ */
+int ivakv_append_rope(const void* k_new, const void* v_new, int64_t k_tok_stride,
+                      int64_t k_head_stride, int64_t v_tok_stride, int64_t v_head_stride,
+                      void* k_pool, void* v_pool, const int32_t* slot_mapping,
+                      const int32_t* positions, int n_tok, int num_kv_heads, int head_dim,
+                      int block_size, int num_pages, float theta, int dtype, hipStream_t stream);
+/*
+ * ivakv_copy_pages: page moves src_pages[i] -> dst_pages[i] (int32, n_moves <= 65535) of a
+ * pool pair, K and V tiles of every kv head (elem_bytes 1, 2 or 4), plus the FP8 scaling
+ * factors when k_scale / v_scale are given (both or neither).  The source and destination
+ * sets must be disjoint.  Used by pool compaction (PagedKVPool.compact), the paged
+ * counterpart of kv_compact_triton (src/kernels_t/kv_ops_triton.py:68-92,159-181).
+ */
+int ivakv_copy_pages(void* k_pool, void* v_pool, float* k_scale, float* v_scale,
+                     const int32_t* src_pages, const int32_t* dst_pages, int n_moves,
+                     int num_kv_heads, int head_dim, int block_size, int elem_bytes,
+                     hipStream_t stream);
+
+/*
  * Paged multi-query causal attention (prefill / chunked prefill).  Sequence b owns
  * query rows query_start[b] .. query_start[b+1]-1 of q ([n_tok][Hq][D] dense, pool
  * dtype); with n_b rows and context length L = context_lens[b], row i sits at

@@ -10,10 +10,12 @@ The directory name is not a Python identifier; load it with
 from . import _abi, model, paged_cache, workloads
 from .ops import (
     chunk_elems,
+    copy_pages,
     decode_workspace_bytes,
     dtype_code,
     is_fp8,
     kv_append,
+    kv_compact,
     kv_gather,
     kv_ops,
     paged_decode_append_attention,
@@ -23,6 +25,7 @@ from .ops import (
     paged_prefill_attention,
     pool_geometry,
     pool_shapes,
+    rope_,
     scale_shape,
 )
 from .model import PagedAttention, Transformer, TransformerConfig, get_attention
@@ -37,10 +40,12 @@ __all__ = [
     "TransformerConfig",
     "get_attention",
     "chunk_elems",
+    "copy_pages",
     "decode_workspace_bytes",
     "dtype_code",
     "is_fp8",
     "kv_append",
+    "kv_compact",
     "kv_gather",
     "kv_ops",
     "paged_decode_append_attention",
@@ -50,5 +55,6 @@ __all__ = [
     "paged_prefill_attention",
     "pool_geometry",
     "pool_shapes",
+    "rope_",
     "scale_shape",
 ]

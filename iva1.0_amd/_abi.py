@@ -95,6 +95,21 @@ SIGNATURES = {
         c_int, c_int, c_int,                   # window, n_sink, dtype
         c_void_p,                              # stream
     ]),
+    "ivakv_rope": (c_int, [
+        c_void_p, c_int64, c_int64, c_void_p,  # x, token / head strides, positions
+        c_int, c_int, c_int, c_float, c_int, c_void_p,  # n_tok, H, D, theta, dtype, stream
+    ]),
+    "ivakv_append_rope": (c_int, [
+        c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,  # k_new, v_new, strides
+        c_void_p, c_void_p, c_void_p, c_void_p,  # k_pool, v_pool, slot_mapping, positions
+        c_int, c_int, c_int, c_int, c_int,     # n_tok, Hkv, D, block_size, num_pages
+        c_float, c_int, c_void_p,              # theta, dtype, stream
+    ]),
+    "ivakv_copy_pages": (c_int, [
+        c_void_p, c_void_p, c_void_p, c_void_p,  # k_pool, v_pool, k_scale, v_scale
+        c_void_p, c_void_p, c_int,             # src_pages, dst_pages, n_moves
+        c_int, c_int, c_int, c_int, c_void_p,  # Hkv, D, block_size, elem_bytes, stream
+    ]),
     "ivakv_prefill_attn": (c_int, [
         c_void_p, c_void_p, c_void_p,          # q, k_pool, v_pool
         c_void_p, c_void_p, c_void_p,          # block_tables, context_lens, query_start

@@ -1,0 +1,227 @@
+// Rotary position embedding fused into the paged append, rotation of query rows in
+// place, and page moves for pool compaction, on gfx950.
+//
+// RoPE as the reference's RoPE module defines it (src/core/rope_kv.py:22-50): dims
+// (2i, 2i+1) of a head form a pair rotated by angle a = p * f_i at absolute position
+// p, with f_i = 1 / theta^(2i / D) (computed in double, stored as float, as the
+// reference's float32 buffer holds it) and a = float(p) * f_i in float:
+//   y[2i]   = x[2i] cos a - x[2i+1] sin a
+//   y[2i+1] = x[2i] sin a + x[2i+1] cos a
+// evaluated in fp32 and rounded once to the element type.
+#include "ivakv_internal.h"
+
+namespace ivakv {
+namespace {
+
+constexpr int64_t kMaxGridR = 0x7fffffff;
+
+struct alignas(16) Chunk16 {
+  uint32_t w[4];
+};
+
+template <typename E>
+__device__ inline float ld(E x) { return (float)x; }
+
+template <typename E>
+__device__ inline void rotate_pair(E& x0, E& x1, float c, float s) {
+  const float a = ld(x0), b = ld(x1);
+  x0 = (E)(a * c - b * s);
+  x1 = (E)(a * s + b * c);
+}
+
+// cos / sin of pair i at position p (accurate library sin / cos of the float angle).
+__device__ inline void pair_angle(int p, int i, int D, float theta, float& c, float& s) {
+  const float f = (float)(1.0 / pow((double)theta, (double)(2 * i) / (double)D));
+  const float ang = (float)p * f;
+  sincosf(ang, &s, &c);
+}
+
+// x [n_tok][H][D] with element strides (token, head), rotated in place at positions[t].
+// One thread per (token, head, pair).
+template <typename E>
+__global__ __launch_bounds__(256) void rope_kernel(E* x, int64_t ts, int64_t hs,
+                                                   const int32_t* pos, int n_tok, int H, int D,
+                                                   float theta) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int half = D / 2;
+  if (gid >= (int64_t)n_tok * H * half) return;
+  const int i = (int)(gid % half);
+  const int64_t th = gid / half;
+  const int h = (int)(th % H);
+  const int64_t t = th / H;
+  float c, s;
+  pair_angle(pos[t], i, D, theta, c, s);
+  E* row = x + t * ts + h * hs;
+  rotate_pair(row[2 * i], row[2 * i + 1], c, s);
+}
+
+// Paged append with K rotated: one thread per (token, kv head, 16-byte chunk) as
+// ivakv_append, the chunk's pairs rotated before the store.
+struct AppendRopeArgs {
+  const void* k_new;
+  const void* v_new;
+  int64_t kts, khs, vts, vhs;
+  void* k_pool;
+  void* v_pool;
+  const int32_t* slots;
+  const int32_t* pos;
+  int n_tok, Hkv, D, bs;
+  int64_t n_slots;
+  float theta;
+};
+
+template <typename E>
+__global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
+  constexpr int X = 16 / sizeof(E);
+  const int nch = a.D / X;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)a.n_tok * a.Hkv * nch) return;
+  const int c = (int)(gid % nch);
+  const int64_t th = gid / nch;
+  const int h = (int)(th % a.Hkv);
+  const int64_t t = th / a.Hkv;
+  const int64_t slot = a.slots[t];
+  if (slot < 0 || slot >= a.n_slots) return;
+  const int64_t page = slot / a.bs;
+  const int off = (int)(slot - page * a.bs);
+  const int64_t head_base = page * a.Hkv + h;
+  const E* ks = static_cast<const E*>(a.k_new) + t * a.kts + h * a.khs + (int64_t)c * X;
+  const E* vs = static_cast<const E*>(a.v_new) + t * a.vts + h * a.vhs + (int64_t)c * X;
+  E k[X];
+#pragma unroll
+  for (int j = 0; j < X; ++j) k[j] = ks[j];
+  const int p = a.pos[t];
+#pragma unroll
+  for (int j = 0; j < X; j += 2) {
+    float cs, sn;
+    pair_angle(p, (c * X + j) / 2, a.D, a.theta, cs, sn);
+    rotate_pair(k[j], k[j + 1], cs, sn);
+  }
+  E* kd = static_cast<E*>(a.k_pool) + ((head_base * nch + c) * a.bs + off) * X;
+  E* vd = static_cast<E*>(a.v_pool) + head_base * a.D * a.bs + (int64_t)c * X * a.bs + off;
+#pragma unroll
+  for (int j = 0; j < X; ++j) {
+    kd[j] = k[j];
+    vd[(int64_t)j * a.bs] = vs[j];
+  }
+}
+
+// Page moves: page src[i] -> dst[i] of every pool tensor (K and V tiles of all kv
+// heads, and the FP8 scaling factors when given).  Grid (chunk block, move), 16
+// bytes per thread.
+__global__ __launch_bounds__(256) void copy_pages_kernel(Chunk16* k, Chunk16* v, Chunk16* ks,
+                                                         Chunk16* vs, const int32_t* src,
+                                                         const int32_t* dst, int64_t page_chunks,
+                                                         int64_t scale_chunks) {
+  const int64_t s = src[blockIdx.y], d = dst[blockIdx.y];
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < page_chunks;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    k[d * page_chunks + i] = k[s * page_chunks + i];
+    v[d * page_chunks + i] = v[s * page_chunks + i];
+    if (ks && i < scale_chunks) {
+      ks[d * scale_chunks + i] = ks[s * scale_chunks + i];
+      vs[d * scale_chunks + i] = vs[s * scale_chunks + i];
+    }
+  }
+}
+
+}  // namespace
+}  // namespace ivakv
+
+using namespace ivakv;
+
+extern "C" int ivakv_rope(void* x, int64_t tok_stride, int64_t head_stride,
+                          const int32_t* positions, int n_tok, int num_heads, int head_dim,
+                          float theta, int dtype, hipStream_t stream) {
+  static const char* name = "ivakv_rope";
+  if (dtype_size(dtype) == 0) return fail(IVAKV_E_DTYPE, "%s: unknown dtype code %d", name, dtype);
+  if (n_tok < 0 || num_heads <= 0 || head_dim <= 0 || head_dim % 2)
+    return fail(IVAKV_E_ARG, "%s: bad sizes n_tok=%d H=%d D=%d (D must be even)", name, n_tok,
+                num_heads, head_dim);
+  if (!(theta > 0.f)) return fail(IVAKV_E_ARG, "%s: theta must be positive", name);
+  if (n_tok == 0) return IVAKV_OK;
+  if (!x || !positions) return fail(IVAKV_E_ARG, "%s: null pointer argument", name);
+  if (tok_stride < 0 || head_stride < 0) return fail(IVAKV_E_ARG, "%s: negative stride", name);
+  const int64_t total = (int64_t)n_tok * num_heads * (head_dim / 2);
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > kMaxGridR) return fail(IVAKV_E_SHAPE, "%s: too many rows", name);
+  switch (dtype) {
+    case IVAKV_F16:
+      rope_kernel<_Float16><<<(unsigned)blocks, 256, 0, stream>>>(
+          static_cast<_Float16*>(x), tok_stride, head_stride, positions, n_tok, num_heads, head_dim, theta);
+      break;
+    case IVAKV_BF16:
+      rope_kernel<__bf16><<<(unsigned)blocks, 256, 0, stream>>>(
+          static_cast<__bf16*>(x), tok_stride, head_stride, positions, n_tok, num_heads, head_dim, theta);
+      break;
+    default:
+      rope_kernel<float><<<(unsigned)blocks, 256, 0, stream>>>(
+          static_cast<float*>(x), tok_stride, head_stride, positions, n_tok, num_heads, head_dim, theta);
+      break;
+  }
+  return launch_status(name);
+}
+
+extern "C" int ivakv_append_rope(const void* k_new, const void* v_new, int64_t k_tok_stride,
+                                 int64_t k_head_stride, int64_t v_tok_stride,
+                                 int64_t v_head_stride, void* k_pool, void* v_pool,
+                                 const int32_t* slot_mapping, const int32_t* positions, int n_tok,
+                                 int num_kv_heads, int head_dim, int block_size, int num_pages,
+                                 float theta, int dtype, hipStream_t stream) {
+  static const char* name = "ivakv_append_rope";
+  const int es = dtype_size(dtype);
+  if (es == 0) return fail(IVAKV_E_DTYPE, "%s: unknown dtype code %d", name, dtype);
+  if (n_tok < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_pages < 0)
+    return fail(IVAKV_E_ARG, "%s: bad sizes n_tok=%d Hkv=%d D=%d block_size=%d num_pages=%d",
+                name, n_tok, num_kv_heads, head_dim, block_size, num_pages);
+  const int X = 16 / es;
+  if (head_dim % X != 0)
+    return fail(IVAKV_E_SHAPE, "%s: head_dim %d must be a multiple of %d", name, head_dim, X);
+  if (!(theta > 0.f)) return fail(IVAKV_E_ARG, "%s: theta must be positive", name);
+  if (n_tok == 0) return IVAKV_OK;
+  if (!k_new || !v_new || !k_pool || !v_pool || !slot_mapping || !positions)
+    return fail(IVAKV_E_ARG, "%s: null pointer argument", name);
+  if (k_tok_stride < 0 || k_head_stride < 0 || v_tok_stride < 0 || v_head_stride < 0)
+    return fail(IVAKV_E_ARG, "%s: negative stride", name);
+  AppendRopeArgs a{k_new, v_new, k_tok_stride, k_head_stride, v_tok_stride, v_head_stride,
+                   k_pool, v_pool, slot_mapping, positions, n_tok, num_kv_heads, head_dim,
+                   block_size, (int64_t)num_pages * block_size, theta};
+  const int64_t total = (int64_t)n_tok * num_kv_heads * (head_dim / X);
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > kMaxGridR) return fail(IVAKV_E_SHAPE, "%s: too many rows", name);
+  switch (dtype) {
+    case IVAKV_F16: append_rope_kernel<_Float16><<<(unsigned)blocks, 256, 0, stream>>>(a); break;
+    case IVAKV_BF16: append_rope_kernel<__bf16><<<(unsigned)blocks, 256, 0, stream>>>(a); break;
+    default: append_rope_kernel<float><<<(unsigned)blocks, 256, 0, stream>>>(a); break;
+  }
+  return launch_status(name);
+}
+
+extern "C" int ivakv_copy_pages(void* k_pool, void* v_pool, float* k_scale, float* v_scale,
+                                const int32_t* src_pages, const int32_t* dst_pages, int n_moves,
+                                int num_kv_heads, int head_dim, int block_size, int elem_bytes,
+                                hipStream_t stream) {
+  static const char* name = "ivakv_copy_pages";
+  if (n_moves < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
+      (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4))
+    return fail(IVAKV_E_ARG, "%s: bad sizes moves=%d Hkv=%d D=%d block_size=%d elem_bytes=%d",
+                name, n_moves, num_kv_heads, head_dim, block_size, elem_bytes);
+  const int64_t page_bytes = (int64_t)num_kv_heads * head_dim * block_size * elem_bytes;
+  const int64_t scale_bytes = (int64_t)num_kv_heads * block_size * 4;
+  if (page_bytes % 16 || (k_scale && scale_bytes % 16))
+    return fail(IVAKV_E_SHAPE, "%s: page of %lld bytes is not a multiple of 16", name,
+                (long long)page_bytes);
+  if (n_moves == 0) return IVAKV_OK;
+  if (!k_pool || !v_pool || !src_pages || !dst_pages || (!k_scale != !v_scale))
+    return fail(IVAKV_E_ARG, "%s: null pointer argument", name);
+  if (!aligned16(k_pool) || !aligned16(v_pool) || (k_scale && (!aligned16(k_scale) || !aligned16(v_scale))))
+    return fail(IVAKV_E_ARG, "%s: pools must be 16-byte aligned", name);
+  if (n_moves > 65535) return fail(IVAKV_E_SHAPE, "%s: at most 65535 moves per call", name);
+  const int64_t chunks = page_bytes / 16;
+  const unsigned bx = (unsigned)((chunks + 255) / 256 < 64 ? (chunks + 255) / 256 : 64);
+  copy_pages_kernel<<<dim3(bx, (unsigned)n_moves), 256, 0, stream>>>(
+      static_cast<Chunk16*>(k_pool), static_cast<Chunk16*>(v_pool),
+      reinterpret_cast<Chunk16*>(k_scale), reinterpret_cast<Chunk16*>(v_scale), src_pages,
+      dst_pages, chunks, k_scale ? scale_bytes / 16 : 0);
+  return launch_status(name);
+}

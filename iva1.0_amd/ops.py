@@ -109,16 +109,21 @@ def _i32(t: torch.Tensor, name: str) -> torch.Tensor:
 
 def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
               slot_mapping: torch.Tensor, k_scale: Optional[torch.Tensor] = None,
-              v_scale: Optional[torch.Tensor] = None) -> None:
+              v_scale: Optional[torch.Tensor] = None,
+              rope_positions: Optional[torch.Tensor] = None, rope_theta: float = 10000.0) -> None:
     """Scatters rows ``k_new[t], v_new[t]`` ([n_tok, Hkv, D], last dim contiguous) into
     ``slot_mapping[t]`` of the pools, in place.  A slot of -1 (or any slot outside the
     pool) leaves the pools untouched for that token.  FP8 pools quantize each (token,
     kv head) row with its own scaling factor, written to ``k_scale`` / ``v_scale``.
+    With ``rope_positions`` (int32 ``[n_tok]``) every K row is rotated at its position on
+    the way in (:func:`rope_`), fused into the append kernel.
 
     Paged counterpart of ``KVCache.update`` (src/core/rope_kv.py:98-110) and the
     ``torch.cat`` append of ``AttentionTorch.forward`` (src/core/attention.py:61-63).
     """
     if is_fp8(k_pool):
+        if rope_positions is not None:
+            raise NotImplementedError("RoPE fused into the append is built for 16/32-bit pools")
         return _append_fp8(k_new, v_new, k_pool, v_pool, slot_mapping, k_scale, v_scale)
     dev = _require_gpu(k_new, v_new, k_pool, v_pool, slot_mapping)
     num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
@@ -138,6 +143,16 @@ def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor, v_
         k_new = k_new.contiguous()
     if v_new.stride(2) != 1:
         v_new = v_new.contiguous()
+    if rope_positions is not None:
+        pos = _i32(rope_positions, "rope_positions").reshape(-1)
+        if pos.numel() != n_tok or pos.device != dev:
+            raise ValueError(f"rope_positions must be {n_tok} int32 values on {dev}")
+        _abi.call("ivakv_append_rope", k_new.data_ptr(), v_new.data_ptr(),
+                  k_new.stride(0), k_new.stride(1), v_new.stride(0), v_new.stride(1),
+                  k_pool.data_ptr(), v_pool.data_ptr(), slot_mapping.data_ptr(), pos.data_ptr(),
+                  n_tok, hkv, head_dim, bs, num_pages, float(rope_theta),
+                  dtype_code(k_pool.dtype), _stream(dev))
+        return
     _abi.call("ivakv_append", k_new.data_ptr(), v_new.data_ptr(),
               k_new.stride(0), k_new.stride(1), v_new.stride(0), v_new.stride(1),
               k_pool.data_ptr(), v_pool.data_ptr(), slot_mapping.data_ptr(),
@@ -468,6 +483,61 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
               int(max_query_len), float(scale), window, n_sink, dtype_code(q.dtype),
               _stream(dev))
     return out
+
+
+def rope_(x: torch.Tensor, positions: torch.Tensor, theta: float = 10000.0) -> torch.Tensor:
+    """Rotates ``x`` ([n_tok, H, D], last dim contiguous) in place at ``positions`` (int32
+    ``[n_tok]``) and returns it: dims (2i, 2i+1) by the angle position * theta^(-2i/D), as
+    the reference's ``RoPE.forward`` (src/core/rope_kv.py:22-50)."""
+    dev = _require_gpu(x, positions)
+    if x.dim() != 3 or x.shape[2] % 2 or x.stride(2) != 1:
+        raise ValueError(f"x must be [n_tok, H, D] with D even and the last dim contiguous; "
+                         f"got {tuple(x.shape)}")
+    pos = _i32(positions, "positions").reshape(-1)
+    if pos.numel() != x.shape[0]:
+        raise ValueError(f"{pos.numel()} positions for {x.shape[0]} rows")
+    _abi.call("ivakv_rope", x.data_ptr(), x.stride(0), x.stride(1), pos.data_ptr(), x.shape[0],
+              x.shape[1], x.shape[2], float(theta), dtype_code(x.dtype), _stream(dev))
+    return x
+
+
+def copy_pages(k_pool: torch.Tensor, v_pool: torch.Tensor, src_pages: torch.Tensor,
+               dst_pages: torch.Tensor, k_scale: Optional[torch.Tensor] = None,
+               v_scale: Optional[torch.Tensor] = None) -> None:
+    """Moves pages ``src_pages[i] -> dst_pages[i]`` (int32, disjoint sets) of a pool pair,
+    with the FP8 scaling factors when the pools are FP8."""
+    dev = _require_gpu(k_pool, v_pool, src_pages, dst_pages)
+    num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
+    src = _i32(src_pages, "src_pages").reshape(-1)
+    dst = _i32(dst_pages, "dst_pages").reshape(-1)
+    if src.numel() != dst.numel():
+        raise ValueError("src_pages and dst_pages differ in length")
+    ks = vs = None
+    if is_fp8(k_pool):
+        ks, vs = _scales(k_pool, k_scale, v_scale)
+    for start in range(0, src.numel(), 65535):
+        n = min(65535, src.numel() - start)
+        _abi.call("ivakv_copy_pages", k_pool.data_ptr(), v_pool.data_ptr(),
+                  ks.data_ptr() if ks is not None else None,
+                  vs.data_ptr() if vs is not None else None,
+                  src[start:].data_ptr(), dst[start:].data_ptr(), n, hkv, head_dim, bs,
+                  k_pool.element_size(), _stream(dev))
+
+
+def kv_compact(kv_cache: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+    """The positions of a contiguous ``[B, H, S, D]`` cache where ``mask`` is true, packed
+    into ``[B, H, n_valid, D]`` (cache dtype) in position order: the compaction
+    ``kv_compact_triton`` performs (src/kernels_t/kv_ops_triton.py:68-92,159-181).  The mask
+    is ``[S]`` or ``[B, S]`` with identical rows (the reference sizes the output by one count
+    for the whole batch, kv_ops_triton.py:165-167)."""
+    if mask.dim() == 2:
+        if bool((mask != mask[:1]).any()):
+            raise ValueError("kv_compact needs the same mask for every sequence of the batch")
+        mask = mask[0]
+    if mask.dim() != 1 or mask.numel() != kv_cache.shape[2]:
+        raise ValueError(f"mask must be [S] or [B, S] with S = {kv_cache.shape[2]}")
+    idx = torch.nonzero(mask.to(torch.bool)).reshape(-1)
+    return kv_ops(kv_cache, idx, operation="gather")
 
 
 def kv_ops(kv_cache: torch.Tensor, indices: torch.Tensor, values: Optional[torch.Tensor] = None,

@@ -31,7 +31,7 @@ from typing import Dict, List, Optional, Sequence, Tuple
 import numpy as np
 import torch
 
-from .ops import FP8, kv_append, kv_gather, pool_shapes, scale_shape
+from .ops import FP8, copy_pages, kv_append, kv_gather, pool_shapes, scale_shape
 
 
 class OutOfPagesError(RuntimeError):
@@ -279,6 +279,43 @@ class PagedKVPool:
         if released:
             self._sync_row(seq_id)
         return released
+
+    # ------------------------------------------------------------ compaction
+    def compaction_moves(self) -> Tuple[List[int], List[int]]:
+        """(src, dst) page moves that pack the referenced pages into ids [0, n_used):
+        every referenced page at or above n_used goes to a free id below it, in
+        ascending order of both.  The two sets are disjoint."""
+        n_used = int((self._ref > 0).sum())
+        src = [int(p) for p in np.nonzero(self._ref > 0)[0] if p >= n_used]
+        dst = [int(p) for p in range(n_used) if self._ref[p] == 0]
+        return src, dst
+
+    def compact(self) -> int:
+        """Packs the live pages into the lowest page ids, moving their contents (every
+        layer, and the FP8 scaling factors) with ivakv_copy_pages and renumbering the
+        block tables; the free list becomes the contiguous tail [n_used, num_pages).
+        The paged counterpart of kv_compact_triton (src/kernels_t/kv_ops_triton.py:
+        68-92,159-181): after it, the pool holds no gaps below its last live page.
+        Device copies of block tables taken earlier are stale.  Returns the pages moved."""
+        src, dst = self.compaction_moves()
+        if not src:
+            return 0
+        if self.k_pools:
+            s_t = torch.tensor(src, dtype=torch.int32).to(self.device)
+            d_t = torch.tensor(dst, dtype=torch.int32).to(self.device)
+            for layer in range(self.num_layers):
+                copy_pages(self.k_pools[layer], self.v_pools[layer], s_t, d_t,
+                           **self.scales(layer))
+        remap = np.arange(self.num_pages)
+        remap[src] = dst
+        for seq_id, seq in self._seqs.items():
+            seq.pages = [int(remap[p]) if p >= 0 else p for p in seq.pages]
+            self._sync_row(seq_id)
+        self._ref[dst] = self._ref[src]
+        self._ref[src] = 0
+        n_used = int((self._ref > 0).sum())
+        self._free = list(range(self.num_pages - 1, n_used - 1, -1))  # pop() -> n_used first
+        return len(src)
 
     # --------------------------------------------------------------- batches
     def tables(self, seq_ids: Sequence) -> Tuple[np.ndarray, np.ndarray]:

@@ -7,6 +7,8 @@ Restates, on the paged layout, the semantics of the reference's
   - AttentionTorch math                    src/core/attention.py:77-102
   - masks (causal / window / sink)         src/core/attention.py:79-93,115-148
   - kv_gather / kv_scatter kernels         src/kernels_t/kv_ops_triton.py:18-65,129
+  - FP8 pages (e4m3fn, per-row scaling)   configs/quant_infer.yaml:22,52, src/quant/fp8_runtime.py:34,66-76
+  - RoPE                                  src/core/rope_kv.py:22-50
 
 Layout (X = 16 // itemsize, BS = block size):
   k_pool [P, Hkv, D/X, BS, X]: K(page, h, t, d) at ((d // X) * BS + t) * X + d % X
@@ -369,6 +371,32 @@ def decode_attention_fp8(q, k_pool, v_pool, k_scale, v_scale, block_tables, ctx_
     """:func:`decode_attention` over the dequantized FP8 pools."""
     kd, vd = dequantize_pools(k_pool, v_pool, k_scale, v_scale, np.float64)
     return decode_attention(q, kd, vd, block_tables, ctx_lens, scale, window, n_sink)
+
+
+# ---------------------------------------------------------------------------- RoPE
+
+def rope_freqs(head_dim: int, theta: float = 10000.0) -> np.ndarray:
+    """f_i = 1 / theta^(2i / D) per dim pair, computed in double and stored as float32 as
+    RoPE._compute_freqs fills its float32 buffer (src/core/rope_kv.py:22-30)."""
+    return np.array([1.0 / (theta ** (i / head_dim)) for i in range(0, head_dim, 2)],
+                    dtype=np.float32)
+
+
+def rope(x: np.ndarray, positions: np.ndarray, theta: float = 10000.0) -> np.ndarray:
+    """Rows ``x[t, ..., D]`` rotated at ``positions[t]`` (rope_kv.py:32-50): pair (2i, 2i+1)
+    by a = float32(p) * f_i (a float32 product, as the reference's float32 tensors
+    compute it), y0 = x0 cos a - x1 sin a, y1 = x0 sin a + x1 cos a, in fp64."""
+    x = np.asarray(x, dtype=np.float64)
+    pos = np.asarray(positions, dtype=np.int64).reshape(-1)
+    f = rope_freqs(x.shape[-1], theta)
+    ang = (pos.astype(np.float32)[:, None] * f[None, :]).astype(np.float64)  # [n, D/2]
+    shape = (len(pos),) + (1,) * (x.ndim - 2) + (f.size,)
+    c, s = np.cos(ang).reshape(shape), np.sin(ang).reshape(shape)
+    x0, x1 = x[..., 0::2], x[..., 1::2]
+    y = np.empty_like(x)
+    y[..., 0::2] = x0 * c - x1 * s
+    y[..., 1::2] = x0 * s + x1 * c
+    return y
 
 
 def index_gather(kv: np.ndarray, indices: np.ndarray) -> np.ndarray:

@@ -138,3 +138,33 @@ def reference_decode_step(cache_k: torch.Tensor, cache_v: torch.Tensor, valid: t
     query_pos = (lengths.to(torch.long) - 1).unsqueeze(1)
     return attention_math(q, k, v, scale, key_valid=key_valid, key_pos=key_pos,
                           query_pos=query_pos, window=window, n_sink=n_sink)
+
+
+class ReferenceRoPE:
+    """The reference's RoPE module (src/core/rope_kv.py:9-50) restated in torch: a float32
+    frequency buffer filled pair by pair, cos / sin of position * frequency, and the
+    pairwise rotation loop writing into a zeros_like(x) result."""
+
+    def __init__(self, head_dim: int, theta: float = 10000.0):
+        self.head_dim = head_dim
+        freqs = torch.zeros(head_dim, dtype=torch.float32)
+        for i in range(0, head_dim, 2):
+            freqs[i] = 1.0 / (theta ** (i / head_dim))
+            if i + 1 < head_dim:
+                freqs[i + 1] = freqs[i]
+        self.freqs = freqs
+
+    def forward(self, x: torch.Tensor, position_ids: torch.Tensor) -> torch.Tensor:
+        """x [B, H, S, D], position_ids [B, S]."""
+        pos_freqs = position_ids.unsqueeze(-1) * self.freqs.unsqueeze(0).unsqueeze(0)
+        cos = torch.cos(pos_freqs).unsqueeze(1).expand(-1, x.shape[1], -1, -1)
+        sin = torch.sin(pos_freqs).unsqueeze(1).expand(-1, x.shape[1], -1, -1)
+        out = torch.zeros_like(x)
+        for i in range(0, self.head_dim, 2):
+            if i + 1 < self.head_dim:
+                out[..., i] = x[..., i] * cos[..., i] - x[..., i + 1] * sin[..., i]
+                out[..., i + 1] = x[..., i] * sin[..., i] + x[..., i + 1] * cos[..., i]
+            else:
+                out[..., i] = x[..., i]
+        return out
+

@@ -159,3 +159,41 @@ def test_churn_keeps_tables_consistent(iva):
             assert p.length(s) == n
             bt, ctx = p.tables([s])
             assert list(bt[0, :len(p.pages(s))]) == p.pages(s) and ctx[0] == n
+
+
+def test_compaction_moves_pack_live_pages(iva):
+    """After churn, compaction moves every live page above n_used to a free id below it
+    (disjoint sets); the renumbered tables keep each sequence's page order, and the
+    free list becomes the tail [n_used, P)."""
+    rng = np.random.default_rng(7)
+    p, pc = pool(iva, pages=64, max_seqs=64)
+    live = []
+    for step in range(60):
+        if p.num_free_pages < 8:
+            break
+        sid = ("s", step)
+        p.add_sequence(sid)
+        p.allocate(sid, int(rng.integers(1, 60)))
+        live.append(sid)
+        if len(live) > 3:
+            p.free(live.pop(int(rng.integers(len(live)))))
+    p.fork(live[0], "fork")                      # shared pages (refcount 2) move once
+    before = {s: p.pages(s) for s in live + ["fork"]}
+    src, dst = p.compaction_moves()
+    n_used = int((p._ref > 0).sum())
+    assert set(src).isdisjoint(dst) and len(src) == len(dst)
+    assert all(s >= n_used for s in src) and all(d < n_used for d in dst)
+    moved = p.compact()
+    assert moved == len(src)
+    remap = dict(zip(src, dst))
+    for s, pages in before.items():
+        assert p.pages(s) == [remap.get(x, x) for x in pages]
+        bt, _ = p.tables([s])
+        assert list(bt[0, :len(pages)]) == p.pages(s)
+    owned = {x for s in before for x in p.pages(s)}
+    assert owned == set(range(n_used))
+    assert sorted(p._free) == list(range(n_used, 64))
+    p.add_sequence("new")
+    p.allocate("new", 1)
+    assert p.pages("new") == [n_used]             # allocation continues from the tail
+    assert p.compact() == 0

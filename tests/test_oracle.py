@@ -501,3 +501,33 @@ def test_fp8_rows_round_trip_and_layout():
     assert np.array_equal(kp.reshape(-1), kf) and np.array_equal(vp.reshape(-1), vf)
     for t, s in enumerate(c["slots"]):
         assert np.array_equal(ks[s // 16, :, s % 16], ksf[t]) and np.array_equal(vs[s // 16, :, s % 16], vsf[t])
+
+
+# ------------------------------------------------------------------ RoPE
+
+def test_rope_matches_the_reference_module():
+    """oracle.rope vs the reference's RoPE module restated in torch float32
+    (reference_path.ReferenceRoPE = rope_kv.py:9-50), at positions up to 70k."""
+    rng = np.random.default_rng(21)
+    for d, theta in ((64, 10000.0), (128, 500000.0), (16, 10.0)):
+        x = rng.standard_normal((2, 3, 40, d)).astype(np.float32)
+        pos = np.stack([np.arange(40), rng.integers(0, 70000, 40)]).astype(np.int64)
+        ref = rp.ReferenceRoPE(d, theta).forward(torch.from_numpy(x), torch.from_numpy(pos)).numpy()
+        for b in range(2):
+            got = orc.rope(x[b].transpose(1, 0, 2), pos[b], theta).transpose(1, 0, 2)
+            assert np.allclose(got, ref[b], rtol=0, atol=2e-6 * max(1.0, np.abs(x).max()))
+
+
+def test_rope_invariants():
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal((10, 4, 32))
+    assert np.allclose(orc.rope(x, np.zeros(10, np.int64)), x, atol=0)     # position 0
+    y = orc.rope(x, rng.integers(0, 5000, 10))
+    assert np.allclose(np.hypot(y[..., 0::2], y[..., 1::2]), np.hypot(x[..., 0::2], x[..., 1::2]))
+    # relative position: <R(p) q, R(p') k> depends only on p - p' (up to the float32
+    # rounding of the angles, ~1e-5 rad at these positions)
+    q, k = rng.standard_normal(32), rng.standard_normal(32)
+    a = (orc.rope(q[None, None], [100])[0, 0] * orc.rope(k[None, None], [37])[0, 0]).sum()
+    b = (orc.rope(q[None, None], [163])[0, 0] * orc.rope(k[None, None], [100])[0, 0]).sum()
+    c = (orc.rope(q[None, None], [163])[0, 0] * orc.rope(k[None, None], [37])[0, 0]).sum()
+    assert abs(a - b) < 1e-4 and abs(a - c) > 1e-2

@@ -1,0 +1,134 @@
+"""RoPE fused into the append, query rotation, page moves, pool compaction and the
+contiguous-cache compaction op on the GPU.
+
+  * ivakv_rope / ivakv_append_rope vs the fp64 oracle (rope_kv.py:22-50): fp16 / bf16
+    elements within one unit in the last place of the exactly rounded result; fp32
+    within 4 ulp of the pair's magnitude (a rotated element can cancel to near zero,
+    so its own ulp is no yardstick); positions up to 100k; V rows of the append and
+    every untouched slot bit-exact;
+  * ivakv_copy_pages and PagedKVPool.compact: bit-exact page contents (fp16 and FP8
+    with scaling factors); gathered sequences identical before and after;
+  * kv_compact vs torch indexing, bit-exact.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_kv as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def ulp_diff(got: torch.Tensor, exact: np.ndarray, dtype) -> float:
+    """Max |got - exact| in units of the last place of the element type at |exact|."""
+    ref = torch.from_numpy(exact).to(dtype).float()                 # exactly rounded
+    g = got.float().cpu()
+    e = torch.from_numpy(exact).float()
+    mant = {torch.float16: 10, torch.bfloat16: 7, torch.float32: 23}[dtype]
+    expo = torch.floor(torch.log2(torch.clamp(e.abs(), min=2.0 ** -14)))
+    ulp = torch.pow(2.0, expo - mant)
+    return float(((g - ref).abs() / ulp).max())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("d", [64, 128])
+def test_rope_in_place_vs_oracle(iva, dev, dtype, d):
+    g = torch.Generator().manual_seed(d)
+    x = torch.randn(50, 6, d, generator=g).to(dtype)
+    pos = torch.randint(0, 100000, (50,), generator=g, dtype=torch.int32)
+    pos[:3] = torch.tensor([0, 1, 65535], dtype=torch.int32)
+    y = iva.rope_(x.clone().to(dev), pos.to(dev), theta=10000.0)
+    exact = orc.rope(x.float().numpy(), pos.numpy(), 10000.0)
+    if dtype == torch.float32:
+        xn = x.numpy()
+        mag = np.repeat(np.hypot(xn[..., 0::2], xn[..., 1::2]), 2, axis=-1)
+        assert (np.abs(y.cpu().numpy() - exact) <= 4 * 2.0 ** -23 * mag + 1e-30).all()
+    else:
+        assert ulp_diff(y, exact, dtype) <= 1
+    assert torch.equal(y[0].cpu(), x[0])                           # position 0: identity
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
+def test_append_rope_vs_oracle(iva, dev, dtype):
+    lengths = [7, 33, 20]
+    c = iva.workloads.c1_append_gather(seed=2, dtype=dtype)
+    lay = iva.workloads.permuted_layout(lengths, 12, torch.Generator().manual_seed(3))
+    n = sum(lengths)
+    k_new, v_new = c["k_new"][:n], c["v_new"][:n]
+    slots = torch.cat([lay.slots(b, torch.arange(m)) for b, m in enumerate(lengths)])
+    positions = torch.cat([torch.arange(m) + 1000 * b for b, m in enumerate(lengths)]).to(torch.int32)
+    ks, vs = iva.pool_shapes(12, 8, 64, 16, dtype)
+    kp = torch.full(ks, 3.0, dtype=dtype, device=dev)
+    vp = torch.full(vs, 3.0, dtype=dtype, device=dev)
+    iva.kv_append(k_new.to(dev), v_new.to(dev), kp, vp, slots.to(dev),
+                  rope_positions=positions.to(dev), rope_theta=10000.0)
+    # expected pools: the oracle append of the rotated K rows (rounded once), V as is
+    k_rot = orc.rope(k_new.float().numpy(), positions.numpy(), 10000.0)
+    ek = np.full(ks, 3.0)  # fp64 values in the pools' fp16 / bf16 layout
+    ev = np.full(vs, 3.0)
+    orc.append(ek, ev, k_rot, v_new.float().numpy(), slots.numpy())
+    assert ulp_diff(kp, ek, dtype) <= 1
+    assert torch.equal(vp.cpu(), torch.from_numpy(ev).to(dtype))
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_copy_pages_and_pool_compaction(iva, dev, fp8):
+    from importlib import import_module
+    pc = import_module("iva_amd.paged_cache")
+    dtype = torch.float8_e4m3fn if fp8 else torch.float16
+    pool = pc.PagedKVPool(48, 2, 64, 16, num_layers=2, dtype=dtype, device=dev, max_seqs=16)
+    rng = np.random.default_rng(5)
+    live = []
+    for step in range(30):
+        sid = ("s", step)
+        pool.add_sequence(sid)
+        n = int(rng.integers(1, 70))
+        slots = torch.from_numpy(pool.allocate(sid, n)).to(dev)
+        for layer in range(2):
+            rows = torch.randn(n, 2, 64, device=dev).to(torch.float16)
+            iva.kv_append(rows, rows * 2, pool.k_pools[layer], pool.v_pools[layer], slots,
+                          **pool.scales(layer))
+        live.append(sid)
+        if len(live) > 4:
+            pool.free(live.pop(int(rng.integers(len(live)))))
+        if pool.num_free_pages < 10:
+            break
+
+    def gathered():
+        bt, ctx = pool.device_tables(live)
+        kw = {"out_dtype": torch.float16} if fp8 else {}
+        return [iva.kv_gather(pool.k_pools[l], pool.v_pools[l], bt, ctx, **pool.scales(l), **kw)
+                for l in range(2)]
+
+    before = gathered()
+    raw = [t.clone().view(torch.uint8).cpu() for t in pool.k_pools + pool.v_pools + pool.k_scales + pool.v_scales]
+    src, dst = pool.compaction_moves()
+    assert src, "the churn above must leave gaps"
+    assert pool.compact() == len(src)
+    after = gathered()
+    for (k0, v0), (k1, v1) in zip(before, after):
+        assert torch.equal(k0.view(torch.int16), k1.view(torch.int16))
+        assert torch.equal(v0.view(torch.int16), v1.view(torch.int16))
+    # the moved pages are byte copies; pages that did not move are untouched
+    now = [t.view(torch.uint8).cpu() for t in pool.k_pools + pool.v_pools + pool.k_scales + pool.v_scales]
+    for r, w in zip(raw, now):
+        for s_, d_ in zip(src, dst):
+            assert torch.equal(w[d_], r[s_])
+        keep = [p for p in range(48) if p not in dst]
+        assert torch.equal(w[keep], r[keep])
+
+
+def test_kv_compact_vs_torch(iva, dev):
+    kv = torch.randn(3, 4, 40, 64, device=dev).half()
+    mask = torch.zeros(40, dtype=torch.bool)
+    mask[[0, 3, 4, 17, 39]] = True
+    got = iva.kv_compact(kv, mask.to(dev))
+    assert torch.equal(got, kv[:, :, mask.to(dev)])
+    got2 = iva.kv_compact(kv, mask.expand(3, 40).to(dev))
+    assert torch.equal(got2, got)
+    bad = mask.expand(3, 40).clone()
+    bad[1, 5] = True
+    with pytest.raises(ValueError, match="same mask"):
+        iva.kv_compact(kv, bad.to(dev))
