@@ -50,7 +50,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .ops import (kv_gather, paged_decode_append_attention, paged_decode_attention,
-                  paged_prefill_attention)
+                  paged_prefill_attention, rope_)
 from .paged_cache import PagedKVCache
 
 
@@ -90,6 +90,10 @@ class TransformerConfig:
     kv_block_size: int = 16
     kv_num_pages: Optional[int] = None   # None = enough for every sequence at seq_len
     sink_tokens: int = 0                 # attention-sink tokens kept visible with the window
+    # The reference computes RoPE state but its attention never applies it
+    # (attention.py:57-59,112-113); True rotates q and k as its RoPE module describes
+    # (rope_kv.py:22-50), fused into the paged append on the hip_paged backend.
+    rope_in_attention: bool = False
     kv_cache_dtype: Optional[str] = None  # None = model dtype; "fp8" = e4m3fn pages
                                           # (configs/quant_infer.yaml:52 memory.kv_cache_dtype)
 
@@ -208,6 +212,22 @@ def _sink_count(sink_cfg: Optional[Dict[str, Any]], default: int) -> int:
     return int(sink_cfg.get("sink_tokens", 4))  # attention.py:138 default
 
 
+def _rope_torch(x: torch.Tensor, positions: torch.Tensor, theta: float) -> torch.Tensor:
+    """The reference's RoPE.forward (src/core/rope_kv.py:22-50), vectorized: x [B, H, S, D]
+    rotated pairwise at positions [S], in float32, returned in x's dtype."""
+    d = x.shape[-1]
+    f = torch.tensor([1.0 / (theta ** (i / d)) for i in range(0, d, 2)], dtype=torch.float32,
+                     device=x.device)
+    ang = positions.to(torch.float32)[:, None] * f[None, :]
+    c, s = torch.cos(ang), torch.sin(ang)
+    xf = x.float()
+    x0, x1 = xf[..., 0::2], xf[..., 1::2]
+    y = torch.empty_like(xf)
+    y[..., 0::2] = x0 * c - x1 * s
+    y[..., 1::2] = x0 * s + x1 * c
+    return y.to(x.dtype)
+
+
 class _AttentionBase(nn.Module):
     def __init__(self, config: TransformerConfig):
         super().__init__()
@@ -225,6 +245,8 @@ class _AttentionBase(nn.Module):
         self.o_proj = nn.Linear(self.d_model, self.d_model, bias=False)
         self.dropout_layer = nn.Dropout(self.dropout)
         self.scale = 1.0 / math.sqrt(self.head_dim)
+        self.rope = bool(config.rope_in_attention)
+        self.rope_theta = float(config.rope_theta)
 
     def _project(self, x):
         b, s, _ = x.shape
@@ -255,16 +277,18 @@ class AttentionTorch(_AttentionBase):
         q = self._apply_rope(q.transpose(1, 2), rope_state)
         k = self._apply_rope(k.transpose(1, 2), rope_state)
         v = v.transpose(1, 2)
-        start = 0
+        start = kv_cache.seq_len if kv_cache is not None else 0
+        if self.rope:
+            pos = torch.arange(start, start + s, device=x.device)
+            q = _rope_torch(q, pos, self.rope_theta)
+            k = _rope_torch(k, pos, self.rope_theta)
         if isinstance(kv_cache, LayeredKVCache):
             layer = kv_cache.next_layer()
-            start = kv_cache.seq_len
             k = torch.cat([layer.k, k], dim=2)  # attention.py:62-63
             v = torch.cat([layer.v, v], dim=2)
             layer.k, layer.v, layer.seq_len = k, v, start + s
             kv_cache.commit(s)
         elif kv_cache is not None:
-            start = kv_cache.seq_len
             k = torch.cat([kv_cache.k, k], dim=2)
             v = torch.cat([kv_cache.v, v], dim=2)
             new = type(kv_cache)(batch_size=kv_cache.batch_size, n_heads=kv_cache.n_heads,
@@ -310,6 +334,16 @@ class PagedAttention(_AttentionBase):
         q, k, v = self._project(x)
         n_sink = _sink_count(sink_cfg, self.config.sink_tokens)
         window = sliding_window if sliding_window and sliding_window > 0 else None
+        rope_pos = None  # K rows rotated inside the append instead of separately
+        if self.rope:
+            # absolute positions of the new tokens, token-major [B * s] int32 on the device
+            pos = kv_cache.token_positions(s) if kv_cache is not None else \
+                torch.arange(s, dtype=torch.int32, device=x.device).repeat(b)
+            rope_(q.reshape(b * s, self.n_heads, self.head_dim), pos, self.rope_theta)
+            if kv_cache is None or s == 1 or kv_cache.pool.fp8:
+                rope_(k.reshape(b * s, self.n_kv_heads, self.head_dim), pos, self.rope_theta)
+            else:
+                rope_pos = pos
         if kv_cache is None:
             qp = torch.arange(s, device=x.device)
             allowed = _visible(qp, qp, window, n_sink) if self.causal else \
@@ -320,7 +354,8 @@ class PagedAttention(_AttentionBase):
         else:
             decode = s == 1 and self.causal
             fp8 = kv_cache.pool.fp8
-            view = kv_cache.layer_step(k.contiguous(), v.contiguous(), append=fp8 or not decode)
+            view = kv_cache.layer_step(k.contiguous(), v.contiguous(), append=fp8 or not decode,
+                                       rope_positions=rope_pos, rope_theta=self.rope_theta)
             if decode and fp8:
                 # FP8 pages: the append above quantized the row; attend over the pages
                 o = paged_decode_attention(

@@ -412,6 +412,7 @@ class PagedKVCache:
         self._bt_dev: Optional[torch.Tensor] = None
         self._bt_pages = -1
         self._static: Optional[dict] = None
+        self._positions: Optional[torch.Tensor] = None
         if seq_len > 0:
             z = torch.zeros(self.batch_size, self.n_heads, int(seq_len), self.head_dim,
                             dtype=self.compute_dtype, device=self.device)
@@ -538,6 +539,7 @@ class PagedKVCache:
             "ctx": torch.from_numpy(ctx).to(self.device),
             "slot": torch.empty(self.batch_size, dtype=torch.int32, device=self.device),
             "pos": torch.empty(self.batch_size, 1, dtype=torch.int64, device=self.device),
+            "rope_pos": torch.empty(self.batch_size, dtype=torch.int32, device=self.device),
             "limit": self.seq_len + int(steps),
         }
         self._static["pos"].copy_(self._static["ctx"].view(-1, 1))
@@ -574,8 +576,23 @@ class PagedKVCache:
         ctx.add_(1)
         return st["slot"], st["bt"], ctx, self.seq_len, 1
 
+    def token_positions(self, t: int) -> torch.Tensor:
+        """Absolute positions of this forward's ``t`` new tokens per sequence, int32
+        ``[B * t]`` token-major on the device.  Computed at the first layer and reused by
+        the others; in static decode read from the device-side lengths (graph-safe)."""
+        if self._cursor == 0 or self._positions is None:
+            if self._static is not None:
+                buf = self._static["rope_pos"]
+                buf.copy_(self._static["ctx"])
+                self._positions = buf
+            else:
+                self._positions = torch.arange(self.seq_len, self.seq_len + int(t), dtype=torch.int32,
+                                               device=self.device).repeat(self.batch_size)
+        return self._positions
+
     def layer_step(self, k_rows: torch.Tensor, v_rows: torch.Tensor,
-                   append: bool = True) -> LayerView:
+                   append: bool = True, rope_positions: Optional[torch.Tensor] = None,
+                   rope_theta: float = 10000.0) -> LayerView:
         """Appends the new tokens' K/V rows ([B, T, Hkv, D]) of the layer at the cursor and
         returns that layer's view.  The first call of a forward allocates the pages of
         the T new tokens of every sequence; the call of the last layer advances
@@ -601,10 +618,12 @@ class PagedKVCache:
         slot_dev, bt, ctx, start, t = self._view
         layer = self._cursor
         if append:
+            rope = {} if rope_positions is None else {"rope_positions": rope_positions,
+                                                      "rope_theta": rope_theta}
             kv_append(k_rows.reshape(b * t, self.n_heads, self.head_dim),
                       v_rows.reshape(b * t, self.n_heads, self.head_dim),
                       self.pool.k_pools[layer], self.pool.v_pools[layer], slot_dev,
-                      **self.pool.scales(layer))
+                      **self.pool.scales(layer), **rope)
         view = LayerView(layer, self.pool.k_pools[layer], self.pool.v_pools[layer], slot_dev, bt,
                          ctx, start, t, self.pool.scales(layer))
         self._cursor += 1

@@ -113,3 +113,31 @@ def test_paged_backend_needs_the_gpu_library(M):
     cache = pc.PagedKVCache(1, 2, 16, 0, "cpu", torch.float32, num_layers=1, max_seq_len=32)
     with pytest.raises(RuntimeError, match="GPU"):
         att(torch.randn(1, 3, 64), kv_cache=cache)  # the HIP kernels run on the GPU only
+
+
+def test_rope_torch_is_the_reference_module(M):
+    """_rope_torch == the reference's RoPE.forward restated (rope_kv.py:22-50), bit for bit
+    in float32, at the reference's default theta 100000."""
+    from oracle import reference_path as rp
+    torch.manual_seed(4)
+    x = torch.randn(2, 3, 30, 16)
+    pos = torch.arange(500, 530)
+    ref = rp.ReferenceRoPE(16, 100000.0).forward(x, pos.unsqueeze(0).expand(2, -1))
+    assert torch.equal(M._rope_torch(x, pos, 100000.0), ref)
+
+
+def test_rope_in_attention_incremental_equals_full(M):
+    torch.manual_seed(5)
+    model = M.Transformer(small_cfg(M, rope_in_attention=True, sliding_window=6, sink_tokens=2)).eval()
+    ids = torch.randint(0, 97, (2, 18))
+    with torch.no_grad():
+        full = model(ids)["logits"]
+        cache = model.new_kv_cache(2, 18, device="cpu", dtype=torch.float32)
+        parts = [model(ids[:, :7], kv_cache=cache)["logits"]]
+        for t in range(7, 18):
+            parts.append(model(ids[:, t:t + 1], kv_cache=cache)["logits"])
+    assert torch.allclose(torch.cat(parts, dim=1), full, atol=1e-5)
+    plain = M.Transformer(small_cfg(M, sliding_window=6, sink_tokens=2)).eval()
+    plain.load_state_dict(model.state_dict())
+    with torch.no_grad():
+        assert not torch.allclose(plain(ids)["logits"], full, atol=1e-3)  # RoPE does act

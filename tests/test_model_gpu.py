@@ -158,3 +158,20 @@ def test_fp8_kv_cache_through_the_model(M, dev):
         a = paged8.generate(ids[:, :40], max_length=8, do_sample=False, eos_token_id=None, use_graph=True)
         b = paged8.generate(ids[:, :40], max_length=8, do_sample=False, eos_token_id=None, use_graph=False)
     assert torch.equal(a, b)
+
+
+def test_rope_in_attention_paged_vs_torch(M, dev):
+    """rope_in_attention=True: the paged backend rotates q in place and K inside the
+    append (fused) or before the fused decode op; logits match the torch backend's
+    vectorized reference RoPE; graph decode (device-side positions) == eager."""
+    ref, paged = twin_models(M, torch.float32, dev, rope_in_attention=True)
+    ids = torch.randint(0, 512, (3, 40 + 10), device=dev)
+    with torch.no_grad():
+        lr, _ = run_steps(ref, ids, 40, dev)
+        lp, _ = run_steps(paged, ids, 40, dev)
+    assert (lr - lp).abs().max().item() <= 1e-4
+    _, p16 = twin_models(M, torch.bfloat16, dev, rope_in_attention=True)
+    with torch.no_grad():
+        a = p16.generate(ids[:, :24], max_length=8, do_sample=False, eos_token_id=None, use_graph=True)
+        b = p16.generate(ids[:, :24], max_length=8, do_sample=False, eos_token_id=None, use_graph=False)
+    assert torch.equal(a, b)
