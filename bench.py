@@ -147,7 +147,7 @@ def _mean_kib(directory: str, counter: str, match) -> float:
 def summarize_pmc(fetch_dir: str, write_dir: str) -> None:
     """Scales the walk's FETCH_SIZE / WRITE_SIZE (KiB per dispatch) by what the same
     counters read for the plain copy of COPY_BYTES, and writes the traffic summary."""
-    is_walk = lambda k: WALK_KERNEL in k and "<1, 128>" in k
+    is_walk = lambda k: WALK_KERNEL in k and "TileOps<1, 128>" in k
     is_copy = lambda k: "copy" in k.lower() and "ivakv" not in k
 
     def copy_kib(directory, counter):
