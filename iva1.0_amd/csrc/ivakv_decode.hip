@@ -526,6 +526,14 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a, int D) 
 // stream walk
 // ---------------------------------------------------------------------------
 
+// n / d for n >= 0, d > 0: one 32-bit division when both fit in 32 bits (the
+// usual case; a uniform branch), else the 64-bit routine, a loop of ~100
+// instructions per bit pair that sits on the walk's and the merges' start-up path.
+__device__ inline int64_t div_nn(int64_t n, int64_t d) {
+  if (((uint64_t)n | (uint64_t)d) >> 32 == 0) return (int64_t)((uint32_t)n / (uint32_t)d);
+  return n / d;
+}
+
 // Waves that share T tiles: every wave gets at least kMinTilesPerWave.
 __device__ inline int64_t stream_waves(int64_t T, int n_waves) {
   const int64_t want = (T + kMinTilesPerWave - 1) / kMinTilesPerWave;
@@ -538,8 +546,8 @@ __device__ inline int64_t stream_waves(int64_t T, int n_waves) {
 struct WaveSplit {
   int64_t T, W;
   __device__ WaveSplit(int64_t T_, const DecodeArgs& a) : T(T_), W(stream_waves(T_, a.n_waves)) {}
-  __device__ int64_t start(int64_t k) const { return k * T / W; }
-  __device__ int64_t owner(int64_t t) const { return ((t + 1) * W - 1) / T; }
+  __device__ int64_t start(int64_t k) const { return div_nn(k * T, W); }
+  __device__ int64_t owner(int64_t t) const { return div_nn((t + 1) * W - 1, T); }
 };
 
 // Flat tile order: sequence-major, then kv head, then effective page.  Unit
@@ -610,7 +618,7 @@ __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kern
   //    pref[b] <= t_begin / Hkv (it is non-empty), then kv head and page.
   int lo = 0, hi = B;
   {
-    const int key = (int)(t_begin / Hkv);
+    const int key = (int)div_nn(t_begin, Hkv);
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
       if (uni(s_pref[mid]) <= key) lo = mid;
@@ -627,7 +635,7 @@ __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kern
   c0r.n = uni(s_pref[lo + 1]) - uni(s_pref[lo]);
   {
     const int64_t r = t_begin - (int64_t)Hkv * uni(s_pref[lo]);
-    c0r.h = (int)(r / c0r.n);
+    c0r.h = (int)div_nn(r, c0r.n);
     c0r.v = (int)(r - (int64_t)c0r.h * c0r.n);
   }
   c0r.w = seq_walk(a, ctx[c0r.b]);
@@ -722,15 +730,17 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, 
   using E = typename Traits<DT>::E;
   const int h = blockIdx.x, b = blockIdx.y;
   const int Hkv = a.Hkv, G = a.G;
-  const int64_t pb = a.ws_pref[b];
-  const int n = a.ws_pref[b + 1] - (int)pb;
+  const int p0 = a.ws_pref[b], p1 = a.ws_pref[b + 1], ptot = a.ws_pref[a.batch];
+  asm volatile("" ::"s"(p0), "s"(p1), "s"(ptot));  // all three loads before the branch
+  const int64_t pb = p0;
+  const int n = p1 - p0;
+  const int64_t T = (int64_t)Hkv * ptot;
   if (n == 0) {
     E* o = static_cast<E*>(a.out) + ((int64_t)b * Hkv * G + h * G) * D;
     for (int idx = threadIdx.x + blockIdx.z * blockDim.x; idx < G * D; idx += blockDim.x * gridDim.z)
       o[idx] = Traits<DT>::from_float(0.f);
     return;
   }
-  const int64_t T = (int64_t)Hkv * a.ws_pref[a.batch];
   const WaveSplit split(T, a);
   const int64_t first_tile = (int64_t)Hkv * pb + (int64_t)h * n;
   const int64_t k0 = split.owner(first_tile), k1 = split.owner(first_tile + n - 1);
@@ -752,7 +762,15 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a, i
   const int h = blockIdx.x, b = blockIdx.y;
   const int Hkv = a.Hkv, G = a.G, Hq = Hkv * G;
   const int lane = threadIdx.x & 63;
+  // Every index the merge needs is loaded up front, in one round trip (the
+  // empty asm keeps the compiler from sinking the prefix loads below the first
+  // branch).
   const int L = a.ctx[b];
+  const int p0 = a.ws_pref[b], p1 = a.ws_pref[b + 1], ptot = a.ws_pref[a.batch];
+  asm volatile("" ::"s"(L), "s"(p0), "s"(p1), "s"(ptot));
+  const int64_t pb = p0;
+  const int n = p1 - p0;
+  const int64_t T = (int64_t)Hkv * ptot;
   E* out = static_cast<E*>(a.out) + ((int64_t)b * Hq + h * G) * D;
   const int idx0 = threadIdx.x + blockIdx.z * blockDim.x, stride = blockDim.x * gridDim.z;
   if (L <= 0) {
@@ -761,19 +779,24 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a, i
   }
   // The new token's slot; an invalid page id there means it is neither stored nor
   // attended (as ivakv_append skips the slot and the walk masks the row).
-  const int pos = L - 1, lp = pos / kBS, row = pos % kBS;
-  int64_t page = lp < a.max_blocks ? (int64_t)a.bt[(int64_t)b * a.max_blocks + lp] : -1;
+  // The entry is loaded unconditionally (from context_lens when it lies outside
+  // the table), through an offset that an empty asm turns into a vector
+  // register: a conditional load, or one whose value is moved to a scalar
+  // register, would be waited for at once instead of alongside the partials.
+  const int pos = L - 1, row = pos % kBS, lp = pos / kBS;
+  const bool in_table = lp < a.max_blocks;
+  int64_t off = in_table ? (int64_t)b * a.max_blocks + lp : b;
+  asm volatile("" : "+v"(off));
+  const int32_t entry = (in_table ? a.bt : a.ctx)[off];
+  const int64_t page = in_table ? (int64_t)entry : -1;
   const bool new_ok = page >= 0 && page < a.num_pages;
   const E* kn = static_cast<const E*>(a.k_new) + ((int64_t)b * Hkv + h) * D;
   const E* vn = static_cast<const E*>(a.v_new) + ((int64_t)b * Hkv + h) * D;
   const E* qb = static_cast<const E*>(a.q) + ((int64_t)b * Hq + h * G) * D;
 
   // Partials of the pool walk (positions < L-1): fragments k0..k1 of the unit.
-  const int64_t pb = a.ws_pref[b];
-  const int n = a.ws_pref[b + 1] - (int)pb;
   int64_t k0 = 0, nf = 0;
   if (n > 0) {
-    const int64_t T = (int64_t)Hkv * a.ws_pref[a.batch];
     const WaveSplit split(T, a);
     const int64_t first_tile = (int64_t)Hkv * pb + (int64_t)h * n;
     k0 = split.owner(first_tile);
@@ -792,13 +815,13 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a, i
     for (int d = lane; d < D; d += 64) dot += (float)qb[g * D + d] * (float)kn[d];
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o);
-    if (new_ok) {
-      const float sc = dot * a.scale_log2;
-      const float mn = fmaxf(M, sc);
-      const float f = exp2_fast(M - mn), w = exp2_fast(sc - mn);
-      L_sum = L_sum * f + w;
-      O = O * f + (float)vn[idx - g * D] * w;
-    }
+    // Selects, not a branch: the page id's load is then waited for only here,
+    // after the partials' loads were issued.
+    const float sc = dot * a.scale_log2;
+    const float mn = fmaxf(M, sc);
+    const float f = new_ok ? exp2_fast(M - mn) : 1.f, w = new_ok ? exp2_fast(sc - mn) : 0.f;
+    L_sum = L_sum * f + w;
+    O = O * f + (float)vn[idx - g * D] * w;
     out[idx] = Tr::from_float(L_sum > 0.f ? O / L_sum : 0.f);
   }
 
