@@ -72,6 +72,10 @@ def parse_args():
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="write the HBM traffic summary from two rocprofv3 --pmc runs")
     p.add_argument("--c5-steps", type=int, default=40, help="timed churn steps of --workload c5")
+    p.add_argument("--context", default="c2",
+                   help="c2 (default): context lengths U[512, 4096] seed 0 (the contract line); "
+                        "an integer N: every sequence of the batch at context N (e.g. 4096, "
+                        "the north-star target's 4k context)")
     p.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "prefill", "c2fp8"), default="c2",
                    help="c2 (default): the contract line; c3 dense-decoder tokens/s, c4 "
                         "long-context window+sinks decode, c5 ragged churn, prefill: 512-token "
@@ -460,6 +464,10 @@ def main():
 
     hq, hkv, d, dtype, esize = 32, 8, 128, torch.float16, 2
     lengths = wl.c2_lengths(seed=0)
+    context_desc = "U[512,4096] seed 0"
+    if args.context != "c2":
+        lengths = [int(args.context)] * len(lengths)
+        context_desc = f"{int(args.context)} (every sequence)"
     batch = len(lengths)
     sc = 1 / math.sqrt(d)
     sets = []
@@ -610,7 +618,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": "C2 paged decode attention + 1-row KV append per sequence",
                    "batch": batch, "num_q_heads": hq, "num_kv_heads": hkv, "head_dim": d,
-                   "block_size": 16, "context": "U[512,4096] seed 0",
+                   "block_size": 16, "context": context_desc,
                    "mean_context": round(sum(lengths) / batch, 1), "pools_rotated": args.pools,
                    "pool_bytes_total": pool_bytes, "launch": "eager" if args.eager else "hip graph",
                    "walk": "partitioned, %d pages" % args.partition_pages

@@ -566,7 +566,7 @@ __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kern
   using E = typename Ops::E;
   constexpr int D = Ops::kD, NB = Ops::NB;
   constexpr int kRing = Ops::kRing;  // tiles in flight per wave
-  extern __shared__ int32_t s_pref[];  // [B + 1] page prefix, then [kStreamThreads] scan scratch
+  extern __shared__ int32_t s_pref[];  // [B + 1] page prefix, then per-wave scan totals
   int32_t* s_scan = s_pref + a.batch + 1;
 
   const int B = a.batch, Hkv = a.Hkv, G = a.G;
@@ -575,8 +575,10 @@ __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kern
   const int ln = lane & 15;
   const int lq = lane >> 4;
 
-  // 1. Page prefix of the batch: thread t sums a contiguous chunk of sequences,
-  //    a Hillis-Steele scan over the 256 chunk sums, then the chunk prefixes.
+  // 1. Page prefix of the batch: thread t sums a contiguous chunk of sequences;
+  //    an inclusive scan of the chunk sums within each wave (lane shuffles) plus
+  //    the totals of the waves before it (two barriers in all), then the chunk
+  //    prefixes.
   const int chunk = cdiv(B, kStreamThreads);
   const int c0 = min(tid * chunk, B), c1 = min(c0 + chunk, B);
   int local = 0;
@@ -585,16 +587,17 @@ __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kern
     s_pref[bb + 1] = n;
     local += n;
   }
-  s_scan[tid] = local;
-  __syncthreads();
-  for (int off = 1; off < kStreamThreads; off <<= 1) {
-    const int add = tid >= off ? s_scan[tid - off] : 0;
-    __syncthreads();
-    s_scan[tid] += add;
-    __syncthreads();
+  int incl = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int v = __shfl_up(incl, off);
+    if (lane >= off) incl += v;
   }
+  if (lane == 63) s_scan[tid >> 6] = incl;
+  __syncthreads();
   {
-    int run = s_scan[tid] - local;  // exclusive prefix of this chunk
+    int run = incl - local;  // exclusive prefix of this chunk
+    for (int w = 0; w < (tid >> 6); ++w) run += s_scan[w];
     if (tid == 0) s_pref[0] = 0;
     for (int bb = c0; bb < c1; ++bb) {
       run += s_pref[bb + 1];
@@ -616,13 +619,20 @@ __global__ __launch_bounds__(kStreamThreads, kStreamWGs) void decode_stream_kern
 
   // 2. Unit and page of the first tile: the last sequence b with
   //    pref[b] <= t_begin / Hkv (it is non-empty), then kv head and page.
+  //    pref is non-decreasing, so b is the count of entries <= key, less one:
+  //    one ballot when the batch fits a wave, else a binary search.
   int lo = 0, hi = B;
   {
     const int key = (int)div_nn(t_begin, Hkv);
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (uni(s_pref[mid]) <= key) lo = mid;
-      else hi = mid;
+    if (B <= 64) {
+      const bool le = lane < B && s_pref[lane < B ? lane : 0] <= key;
+      lo = __popcll(__ballot(le)) - 1;
+    } else {
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (uni(s_pref[mid]) <= key) lo = mid;
+        else hi = mid;
+      }
     }
   }
   // A cursor walks (sequence, kv head, effective page) in flat order.
