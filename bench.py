@@ -29,7 +29,8 @@ Profiling helpers (no timing line):
                        rocprofv3 FETCH_SIZE / WRITE_SIZE counters.
   --summarize-pmc F W  reads the counter CSVs of a FETCH_SIZE run (directory F)
                        and a WRITE_SIZE run (directory W) and writes
-                       profiles/decode_attn_c2_traffic.{json,md}.
+                       profiles/decode_attn_c2_traffic.json (with --context N:
+                       profiles/decode_attn_ctxN_traffic.json).
 """
 from __future__ import annotations
 
@@ -48,7 +49,10 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "paged decode-attn + KV append GB/s and % HBM peak; decode tokens/s at 1 GPU"
-PROFILE_TRAFFIC = ROOT / "profiles" / "decode_attn_c2_traffic.json"
+def traffic_path(context: str):
+    """Committed HBM-traffic summary of the walk for a --context choice."""
+    name = "c2" if context == "c2" else f"ctx{int(context)}"
+    return ROOT / "profiles" / f"decode_attn_{name}_traffic.json"
 WALK_KERNEL = "decode_stream_kernel"
 COPY_BYTES = 256 << 20
 
@@ -148,7 +152,7 @@ def _mean_kib(directory: str, counter: str, match) -> float:
     return sum(vals) / len(vals)
 
 
-def summarize_pmc(fetch_dir: str, write_dir: str) -> None:
+def summarize_pmc(fetch_dir: str, write_dir: str, context: str = "c2") -> None:
     """Scales the walk's FETCH_SIZE / WRITE_SIZE (KiB per dispatch) by what the same
     counters read for the plain copy of COPY_BYTES, and writes the traffic summary."""
     is_walk = lambda k: WALK_KERNEL in k and "TileOps<1, 128>" in k
@@ -176,7 +180,8 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> None:
     read_b = fetch_walk * 1024 * f_scale
     write_b = write_walk * 1024 * w_scale
     summary = {
-        "kernel": "decode_stream_kernel<f16,128> (C2)",
+        "kernel": "decode_stream_kernel<f16,128> (%s)" % (
+            "C2" if context == "c2" else f"B 32 at context {int(context)}"),
         "fetch_kib_per_dispatch": round(fetch_walk, 1),
         "write_kib_per_dispatch": round(write_walk, 1),
         "copy_calibration_bytes": COPY_BYTES,
@@ -188,8 +193,9 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> None:
         "hbm_write_bytes_per_launch": int(write_b),
         "hbm_bytes_per_launch": int(read_b + write_b),
     }
-    PROFILE_TRAFFIC.parent.mkdir(exist_ok=True)
-    PROFILE_TRAFFIC.write_text(json.dumps(summary, indent=1) + "\n")
+    out = traffic_path(context)
+    out.parent.mkdir(exist_ok=True)
+    out.write_text(json.dumps(summary, indent=1) + "\n")
     print(json.dumps(summary))
 
 
@@ -441,7 +447,7 @@ def bench_prefill(args, iva, torch, dev):
 def main():
     args = parse_args()
     if args.summarize_pmc:
-        summarize_pmc(*args.summarize_pmc)
+        summarize_pmc(*args.summarize_pmc, context=args.context)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -584,9 +590,9 @@ def main():
     achieved = attn_b / (walk_us * 1e-6) / 1e9
 
     traffic = None
-    if PROFILE_TRAFFIC.exists():
+    if traffic_path(args.context).exists():
         try:
-            traffic = json.loads(PROFILE_TRAFFIC.read_text()).get("hbm_bytes_per_launch")
+            traffic = json.loads(traffic_path(args.context).read_text()).get("hbm_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
 
