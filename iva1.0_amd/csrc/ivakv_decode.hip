@@ -765,10 +765,11 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, 
 // partials of positions < L-1, writes `out`, and stores the new K/V rows into the
 // token's slot for later steps.  Every unit is merged here (the fused walk never
 // writes `out` directly).
-template <int DT>
-__global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a, int D) {
+template <int DT, int D>
+__global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
   using Tr = Traits<DT>;
   using E = typename Tr::E;
+  constexpr int DL = D / 64;  // dims of the new token's dot product per lane
   const int h = blockIdx.x, b = blockIdx.y;
   const int Hkv = a.Hkv, G = a.G, Hq = Hkv * G;
   const int lane = threadIdx.x & 63;
@@ -813,16 +814,25 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a, i
     nf = split.owner(first_tile + n - 1) - k0 + 1;
   }
   const int64_t base = k0 + (int64_t)b * Hkv + h;
-  // The partials are folded first (their loads wait only on the prefix), then
-  // the new token.  D is a multiple of 64, so the 64 outputs of a wave share one
-  // query head g, and the wave scores the new token for g with a lane-strided
-  // dot product.
+  // D is a multiple of 64, so the 64 outputs of a wave share one query head g,
+  // and the wave scores the new token for g with a lane-strided dot product.
+  // Its operands (and the value element) are loaded before the partials, so
+  // every load of the element is in flight at once; then the partials are
+  // folded, then the new token.
   for (int idx = idx0; idx < G * D; idx += stride) {
     const int g = idx / D;
+    float qv[DL], kv[DL];
+#pragma unroll
+    for (int j = 0; j < DL; ++j) {
+      qv[j] = (float)qb[g * D + lane + 64 * j];
+      kv[j] = (float)kn[lane + 64 * j];
+    }
+    const float vv = (float)vn[idx - g * D];
     float M = kNegInf, L_sum = 0.f, O = 0.f;
     fold_slots(a, g, idx, D, (int)nf, [&](int i) { return base + i; }, M, L_sum, O);
     float dot = 0.f;
-    for (int d = lane; d < D; d += 64) dot += (float)qb[g * D + d] * (float)kn[d];
+#pragma unroll
+    for (int j = 0; j < DL; ++j) dot += qv[j] * kv[j];
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o);
     // Selects, not a branch: the page id's load is then waited for only here,
@@ -831,21 +841,19 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a, i
     const float mn = fmaxf(M, sc);
     const float f = new_ok ? exp2_fast(M - mn) : 1.f, w = new_ok ? exp2_fast(sc - mn) : 0.f;
     L_sum = L_sum * f + w;
-    O = O * f + (float)vn[idx - g * D] * w;
+    O = O * f + vv * w;
     out[idx] = Tr::from_float(L_sum > 0.f ? O / L_sum : 0.f);
   }
 
   // Append: the new rows go to the slot of position L-1.
-  {
-    if (new_ok && blockIdx.z == 0) {
-      constexpr int X = 16 / (int)sizeof(E);
-      const int64_t tile = (page * Hkv + h) * (int64_t)D * kBS;
-      E* kp = static_cast<E*>(const_cast<void*>(a.k_pool)) + tile;
-      E* vp = static_cast<E*>(const_cast<void*>(a.v_pool)) + tile;
-      for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        kp[((d / X) * kBS + row) * X + d % X] = kn[d];
-        vp[d * kBS + row] = vn[d];
-      }
+  if (new_ok && blockIdx.z == 0) {
+    constexpr int X = 16 / (int)sizeof(E);
+    const int64_t tile = (page * Hkv + h) * (int64_t)D * kBS;
+    E* kp = static_cast<E*>(const_cast<void*>(a.k_pool)) + tile;
+    E* vp = static_cast<E*>(const_cast<void*>(a.v_pool)) + tile;
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+      kp[((d / X) * kBS + row) * X + d % X] = kn[d];
+      vp[d * kBS + row] = vn[d];
     }
   }
 }
@@ -942,8 +950,13 @@ void launch_stream(Stage stage, int D, dim3 grid, size_t smem, hipStream_t strea
   const int threads = units >= 256 ? 256 : 64;
   const int zsplit = cdiv(a.G * D, threads);
   const dim3 mgrid((unsigned)a.Hkv, (unsigned)a.batch, (unsigned)zsplit);
-  if (stage == kFused)
-    decode_fused_merge_kernel<DT><<<mgrid, threads, 0, stream>>>(a, D);
+  if (stage == kFused) {
+    switch (D) {
+      case 64: decode_fused_merge_kernel<DT, 64><<<mgrid, threads, 0, stream>>>(a); break;
+      case 128: decode_fused_merge_kernel<DT, 128><<<mgrid, threads, 0, stream>>>(a); break;
+      default: decode_fused_merge_kernel<DT, 256><<<mgrid, threads, 0, stream>>>(a); break;
+    }
+  }
   else if (stage != kPartial)
     decode_stream_merge_kernel<DT><<<mgrid, threads, 0, stream>>>(a, D);
 }
