@@ -187,7 +187,9 @@ int ivakv_decode_append_attn(const void* q, const void* k_new, const void* v_new
  * FP8 KV pages (OCP e4m3fn codes, one byte per element) with one fp32 scaling factor
  * per (slot, kv head):
  *   k_pool  [num_pages][Hkv][D/16][BS][16] bytes (16-byte chunks of 16 dims)
- *   v_pool  [num_pages][Hkv][D][BS] bytes
+ *   v_pool  [num_pages][Hkv][D * BS] bytes; within a tile the code of (dim d,
+ *           key t) is at ((d%16 * 4 + t/4) * D/16 + d/16) * 4 + t%4, so each lane of
+ *           the decode walk reads its V bytes as whole 16-byte loads
  *   k_scale, v_scale [num_pages][Hkv][BS] fp32
  * A row x of one (token, kv head) is stored as e4m3(x * sf), sf = 448 / max|x|
  * (1 for an all-zero row), clamped to [1e-8, 1e8], rounded to nearest even and

@@ -241,7 +241,8 @@ struct TileOps {
 // The same for FP8 (OCP e4m3fn) pools with per-(slot, kv head) scaling factors
 // (quantized = x * sf, sf = 448 / amax of the row; k_scale / v_scale [page][Hkv][16]
 // fp32), queries and output of dtype DT (fp16 or bf16).  Layout: k_pool
-// [page][Hkv][D/16][16][16] bytes, v_pool [page][Hkv][D][16] bytes.  A lane's 16-byte K
+// [page][Hkv][D/16][16][16] bytes, v_pool [page][Hkv][16 * D] bytes in the order of
+// fp8_v_offset ([d%16][r/4][d/16][r%4]: a lane's V words are consecutive).  A lane's 16-byte K
 // chunk holds dims 16c .. 16c+15 (c = 4i + lq) of row ln; it is converted to two
 // 8-element operands (v_cvt_scalef32_pk_*_fp8, exact) for two 16x16x32 MFMAs, whose
 // query chunks are loaded in the same dim order.  Per key, 1/sf_k joins the score
@@ -285,8 +286,15 @@ struct TileOps8 {
     const uint8_t* vp = static_cast<const uint8_t*>(a.v_pool) + tile * kTileBytes;
 #pragma unroll
     for (int i = 0; i < KL; ++i) t.k[i] = *reinterpret_cast<const Chunk16*>(kp + ((4 * i + lq) * kBS + ln) * 16);
+    // Words m = 0 .. NB-1 (dims 16m + ln, keys 4lq .. 4lq+3) are consecutive in the
+    // FP8 V tile order (fp8_v_offset): NB / 4 16-byte loads.
+    const uint8_t* vl = vp + fp8_v_offset(ln, 4 * lq, D);
 #pragma unroll
-    for (int m = 0; m < NB; ++m) t.v[m] = *reinterpret_cast<const uint32_t*>(vp + (16 * m + ln) * kBS + 4 * lq);
+    for (int m = 0; m < NB; m += 4) {
+      const Chunk16 c = *reinterpret_cast<const Chunk16*>(vl + 4 * m);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) t.v[m + j] = c.w[j];
+    }
     t.ks = *reinterpret_cast<const f32x4*>(a.k_scale + tile * kBS + 4 * lq);
     t.vs = *reinterpret_cast<const f32x4*>(a.v_scale + tile * kBS + 4 * lq);
     __asm__ volatile("" ::: "memory");

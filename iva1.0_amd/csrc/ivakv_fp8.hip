@@ -3,8 +3,10 @@
 // (ivakv_decode.hip).
 //
 // Pool layout (bytes): k_pool [page][Hkv][D/16][16][16] (16-byte chunks of 16 dims,
-// rows of a chunk column contiguous), v_pool [page][Hkv][D][16] (V transposed per
-// page), k_scale / v_scale [page][Hkv][16] fp32.  A row x of one (token, kv head) is
+// rows of a chunk column contiguous), v_pool [page][Hkv][16 * D] with the byte of
+// (dim d, key r) at fp8_v_offset(d, r, D) = order [d%16][r/4][d/16][r%4] (each lane of
+// the decode walk reads its V bytes as whole 16-byte loads), k_scale / v_scale
+// [page][Hkv][16] fp32.  A row x of one (token, kv head) is
 // stored as codes e4m3(x * sf) with sf = 448 / max|x| (1 for an all-zero row),
 // clamped to [1e-8, 1e8] -- the reference's scaling rule
 // (src/quant/fp8_runtime.py:66-76) applied per row -- and read back as code / sf.
@@ -110,7 +112,7 @@ __global__ __launch_bounds__(256) void append8_kernel(Append8Args a) {
   for (int i = 0; i < PER; ++i) {
     const int d = lane * PER + i;
     kp[((d >> 4) * 16 + off) * 16 + (d & 15)] = (uint8_t)e4m3_encode(kx[i] * ksf);
-    vp[d * 16 + off] = (uint8_t)e4m3_encode(vx[i] * vsf);
+    vp[fp8_v_offset(d, off, a.D)] = (uint8_t)e4m3_encode(vx[i] * vsf);
   }
   if (lane == 0) {
     a.k_scale[tile * 16 + off] = ksf;
@@ -149,7 +151,7 @@ __global__ __launch_bounds__(256) void gather8_kernel(Gather8Args a) {
     float kv = 0.f, vv = 0.f;
     if (page_ok && pos < L) {
       const uint32_t kc = a.k_pool[tile * (int64_t)a.D * 16 + ((d >> 4) * 16 + r) * 16 + (d & 15)];
-      const uint32_t vc = a.v_pool[tile * (int64_t)a.D * 16 + d * 16 + r];
+      const uint32_t vc = a.v_pool[tile * (int64_t)a.D * 16 + fp8_v_offset(d, r, a.D)];
       kv = e4m3_decode(kc) / a.k_scale[tile * 16 + r];
       vv = e4m3_decode(vc) / a.v_scale[tile * 16 + r];
     }

@@ -63,6 +63,14 @@ __host__ __device__ inline int logical_page(const PageWalk& w, int v) {
   return v < w.sink_pages ? v : w.win_first + (v - w.sink_pages);
 }
 
+// Byte of (dim d, key r) in an FP8 V tile (head_dim D, 16 keys): order
+// [d % 16][r / 4][d / 16][r % 4].  Lane (ln, lq) of the decode walk needs keys
+// 4lq .. 4lq+3 of dims ln, 16 + ln, ..., one 4-byte word per 16 dims: in this
+// order its D/16 words are consecutive, D/64 16-byte loads.
+__host__ __device__ inline int fp8_v_offset(int d, int r, int D) {
+  return (((d & 15) * 4 + (r >> 2)) * (D >> 4) + (d >> 4)) * 4 + (r & 3);
+}
+
 // Effective pages of a walk whose logical page lies inside the block table
 // (logical_page is increasing, so these are the first ones).  Positions on the
 // pages past the table are never attended, so the walks stop there.

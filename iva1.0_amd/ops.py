@@ -62,7 +62,9 @@ def chunk_elems(dtype: torch.dtype) -> int:
 
 def pool_shapes(num_pages: int, num_kv_heads: int, head_dim: int, block_size: int,
                 dtype: torch.dtype) -> Tuple[Tuple[int, ...], Tuple[int, ...]]:
-    """Shapes of (k_pool, v_pool) for one layer."""
+    """Shapes of (k_pool, v_pool) for one layer.  For FP8 pools the V tile's 16 * D
+    bytes are not in (dim, key) order but in the walk's order [d%16][key/4][d/16][key%4]
+    (ivakv_internal.h fp8_v_offset); only the kernels read or write them."""
     x = chunk_elems(dtype)
     if head_dim % x:
         raise ValueError(f"head_dim {head_dim} must be a multiple of {x} for {dtype}")

@@ -330,6 +330,27 @@ def quantize_rows(x: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
     return e4m3_encode(x * sf[..., None]), sf
 
 
+def fp8_v_to_tiles(v_nat: np.ndarray) -> np.ndarray:
+    """FP8 V tiles from natural [..., D, 16] (dim, key) order to the pool's byte order
+    [d % 16][key / 4][d / 16][key % 4] (same shape): ivakv_internal.h fp8_v_offset, chosen
+    so each lane of the decode walk reads whole 16-byte words.  An order of this build,
+    not of the reference (whose KV cache is contiguous)."""
+    *lead, d, bs = v_nat.shape
+    n = len(lead)
+    t = v_nat.reshape(*lead, d // 16, 16, bs // 4, 4)          # (d/16, d%16, key/4, key%4)
+    t = t.transpose(*range(n), n + 1, n + 2, n, n + 3)        # (d%16, key/4, d/16, key%4)
+    return np.ascontiguousarray(t).reshape(*lead, d, bs)
+
+
+def fp8_v_from_tiles(v_dev: np.ndarray) -> np.ndarray:
+    """Inverse of :func:`fp8_v_to_tiles`."""
+    *lead, d, bs = v_dev.shape
+    n = len(lead)
+    t = v_dev.reshape(*lead, 16, bs // 4, d // 16, 4)          # (d%16, key/4, d/16, key%4)
+    t = t.transpose(*range(n), n + 2, n, n + 1, n + 3)        # (d/16, d%16, key/4, key%4)
+    return np.ascontiguousarray(t).reshape(*lead, d, bs)
+
+
 def empty_scales(num_pages: int, hkv: int, block_size: int) -> np.ndarray:
     return np.ones((num_pages, hkv, block_size), dtype=np.float32)
 
@@ -337,10 +358,13 @@ def empty_scales(num_pages: int, hkv: int, block_size: int) -> np.ndarray:
 def append_fp8(k_pool: np.ndarray, v_pool: np.ndarray, k_scale: np.ndarray, v_scale: np.ndarray,
                k_new: np.ndarray, v_new: np.ndarray, slot_mapping: np.ndarray) -> None:
     """In place: each (token, kv head) row of ``k_new/v_new`` quantized with its own scaling
-    factor; codes go where :func:`append` puts a row, factors to ``[page, head, row]``."""
+    factor; K codes go where :func:`append` puts a row, V codes there in the FP8 tile order
+    (:func:`fp8_v_to_tiles`), factors to ``[page, head, row]``."""
     kc, ksf = quantize_rows(k_new)
     vc, vsf = quantize_rows(v_new)
-    append(k_pool, v_pool, kc, vc, slot_mapping)
+    v_nat = fp8_v_from_tiles(v_pool)
+    append(k_pool, v_nat, kc, vc, slot_mapping)
+    v_pool[...] = fp8_v_to_tiles(v_nat)
     num_pages, hkv, _, bs, _ = k_pool.shape
     slots = np.asarray(slot_mapping, dtype=np.int64).reshape(-1)
     ok = (slots >= 0) & (slots < num_pages * bs)
@@ -352,9 +376,10 @@ def append_fp8(k_pool: np.ndarray, v_pool: np.ndarray, k_scale: np.ndarray, v_sc
 
 def dequantize_pools(k_pool: np.ndarray, v_pool: np.ndarray, k_scale: np.ndarray,
                      v_scale: np.ndarray, dtype=np.float32) -> Tuple[np.ndarray, np.ndarray]:
-    """FP8 pools as pools of ``dtype`` with the same layout: code / sf (float32 division)."""
+    """FP8 pools as pools of ``dtype`` in the 16-bit layout (V back in natural order):
+    code / sf (float32 division)."""
     k = e4m3_decode(k_pool) / k_scale[:, :, None, :, None]
-    v = e4m3_decode(v_pool) / v_scale[:, :, None, :]
+    v = e4m3_decode(fp8_v_from_tiles(v_pool)) / v_scale[:, :, None, :]
     return k.astype(dtype), v.astype(dtype)
 
 

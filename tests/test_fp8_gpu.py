@@ -112,7 +112,9 @@ def test_all_codes_decode_as_torch(iva, dev):
                            torch.tensor([16], dtype=torch.int32, device=dev), out_len=16,
                            k_scale=scale.to(dev), v_scale=scale.to(dev), out_dtype=torch.float32)
     kref = kb.view(FP8).float()[0, 0].permute(1, 0, 2).reshape(16, 256)  # [row, dim]
-    vref = vb.view(FP8).float()[0, 0].t()
+    # V bytes are in the FP8 tile order; the oracle's inverse gives (dim, key)
+    vnat = torch.from_numpy(orc.fp8_v_from_tiles(vb.numpy()))
+    vref = vnat.view(FP8).float()[0, 0].t()
     for got, exp in ((ko[0, 0].cpu(), kref), (vo[0, 0].cpu(), vref)):
         assert torch.equal(torch.isnan(got), torch.isnan(exp))
         assert torch.equal(got[~torch.isnan(got)], exp[~torch.isnan(exp)])

@@ -498,9 +498,28 @@ def test_fp8_rows_round_trip_and_layout():
     kf, vf = kf.reshape(-1), vf.reshape(-1)
     vc, vsf = orc.quantize_rows(c["v_new"])
     orc.append_loops(kf, vf, kc, vc, c["slots"], c["num_pages"], 2, 32, 16)
-    assert np.array_equal(kp.reshape(-1), kf) and np.array_equal(vp.reshape(-1), vf)
+    assert np.array_equal(kp.reshape(-1), kf)
+    assert np.array_equal(orc.fp8_v_from_tiles(vp).reshape(-1), vf)   # V in the FP8 tile order
     for t, s in enumerate(c["slots"]):
         assert np.array_equal(ks[s // 16, :, s % 16], ksf[t]) and np.array_equal(vs[s // 16, :, s % 16], vsf[t])
+
+
+def test_fp8_v_tile_order_gives_each_lane_consecutive_words():
+    """The FP8 V tile order is a permutation of the tile's bytes (round trip exact) in
+    which lane (ln, lq) of the decode walk finds its operand words -- keys 4lq..4lq+3 of
+    dims ln, 16 + ln, ..., one word per 16 dims -- as consecutive bytes, lanes in order."""
+    for d in (64, 128, 256):
+        nat = np.arange(d * 16, dtype=np.int32).reshape(1, 1, d, 16)
+        dev = orc.fp8_v_to_tiles(nat)
+        assert np.array_equal(orc.fp8_v_from_tiles(dev), nat)
+        flat = dev.reshape(-1)
+        assert np.array_equal(np.sort(flat), np.arange(d * 16))
+        nb = d // 16
+        for ln in range(16):
+            for lq in range(4):
+                words = flat[(ln * 4 + lq) * nb * 4:(ln * 4 + lq + 1) * nb * 4].reshape(nb, 4)
+                want = nat[0, 0, 16 * np.arange(nb)[:, None] + ln, 4 * lq + np.arange(4)[None, :]]
+                assert np.array_equal(words, want)
 
 
 # ------------------------------------------------------------------ RoPE
