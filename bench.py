@@ -294,7 +294,11 @@ def bench_c2fp8(args, iva, torch, dev):
         iva.kv_append(rows_k, rows_v, k8, v8, slots, k_scale=kss, v_scale=vss)
         del kc, vc, rows_k, rows_v
         q, out = dd["q"], torch.empty_like(dd["q"])
-        sets8.append((q, k8, v8, bt, ctx, out, kss, vss))
+        gen = torch.Generator(device=dev).manual_seed(500 + i)
+        kn = (torch.randn(batch, hkv, d, generator=gen, device=dev) * sc).half()
+        vn = (torch.randn(batch, hkv, d, generator=gen, device=dev) * sc).half()
+        last = torch.stack([lay.slots(b, torch.tensor([n - 1])) for b, n in enumerate(lengths)])
+        sets8.append((q, k8, v8, bt, ctx, out, kss, vss, kn, vn, last.reshape(-1).to(dev)))
         sets16.append((q, dd["k_pool"], dd["v_pool"], bt, ctx, out))
     ws = torch.empty(iva.decode_workspace_bytes(batch, hq, hkv, d, 16, sets8[0][3].shape[1]),
                      dtype=torch.uint8, device=dev)
@@ -302,17 +306,28 @@ def bench_c2fp8(args, iva, torch, dev):
                                                 workspace=ws, k_scale=s[6], v_scale=s[7])
     run16 = lambda s: iva.paged_decode_attention(s[0], s[1], s[2], s[3], s[4], out=s[5],
                                                  workspace=ws)
+    # decode steps on FP8 pages: the new row of every sequence (position L-1) appended
+    # and attended, in one op (ivakv_decode_append_attn_fp8) or as append + attention
+    step8 = lambda s: iva.paged_decode_append_attention(
+        s[0], s[8], s[9], s[1], s[2], s[3], s[4], out=s[5], workspace=ws, k_scale=s[6],
+        v_scale=s[7])
+
+    def step8_unfused(s):
+        iva.kv_append(s[8], s[9], s[1], s[2], s[10], k_scale=s[6], v_scale=s[7])
+        run8(s)
     stream = torch.cuda.Stream(device=dev)
     stream.wait_stream(torch.cuda.current_stream(dev))
     reps = 20
     with torch.cuda.stream(stream):
         for s in sets8:
             run8(s)
+            step8(s)
+            step8_unfused(s)
         for s in sets16:
             run16(s)
         torch.cuda.synchronize(dev)
         graphs = []
-        for fn, sets in ((run8, sets8), (run16, sets16)):
+        for fn, sets in ((run8, sets8), (run16, sets16), (step8, sets8), (step8_unfused, sets8)):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
                 for r in range(reps):
@@ -329,7 +344,7 @@ def bench_c2fp8(args, iva, torch, dev):
             e1.record(stream)
             torch.cuda.synchronize(dev)
             times.append(e0.elapsed_time(e1) * 1e-3 / (10 * reps))
-    t8, t16 = times
+    t8, t16, ts8, ts8u = times
     tokens = sum(lengths)
     byts = 2 * tokens * hkv * d + 2 * tokens * hkv * 4 + 2 * batch * hq * d * 2 + \
         sum(-(-n // 16) for n in lengths) * 4 + 4 * batch
@@ -340,7 +355,10 @@ def bench_c2fp8(args, iva, torch, dev):
                        "launch": "hip graph", "walk": "stream"},
             "attention_us": round(t8 * 1e6, 2), "fp16_pages_attention_us": round(t16 * 1e6, 2),
             "speedup_vs_fp16_pages": round(t16 / t8, 3), "bytes": byts,
-            "tokens_per_s": round(batch / t8, 1)}
+            "tokens_per_s": round(batch / t8, 1),
+            "step_us": round(ts8 * 1e6, 2), "step_unfused_us": round(ts8u * 1e6, 2),
+            "step_ops": "ivakv_decode_append_attn_fp8 (fused); unfused: ivakv_append_fp8 + "
+                        "ivakv_decode_attn_fp8"}
 
 
 def bench_c4(args, iva, torch, dev):

@@ -230,6 +230,26 @@ int ivakv_decode_attn_fp8(const void* q, const void* k_pool, const void* v_pool,
                           hipStream_t stream);
 
 /*
+ * ivakv_decode_append_attn_fp8: ivakv_decode_append_attn over FP8 pools.  The new rows
+ * k_new / v_new ([batch][Hkv][D], dtype `dtype` like q) are quantized exactly as
+ * ivakv_append_fp8 quantizes them (the pools and factors afterwards are byte-identical
+ * to that append's), attended as their dequantized values, and stored into the slot of
+ * position L-1; positions < L-1 come from the pools as in ivakv_decode_attn_fp8.  Same
+ * result as ivakv_append_fp8 followed by ivakv_decode_attn_fp8, in two launches
+ * instead of three.  Workspace, geometry and alignment as ivakv_decode_attn_fp8.
+ * Replaces: the append + score sequence of AttentionTorch.forward with a cache
+ * (src/core/attention.py:61-102) on a kv_cache_dtype "fp8" cache
+ * (configs/quant_infer.yaml:22,52; scaling rule src/quant/fp8_runtime.py:66-76).
+ */
+int ivakv_decode_append_attn_fp8(const void* q, const void* k_new, const void* v_new,
+                                 void* k_pool, void* v_pool, float* k_scale, float* v_scale,
+                                 const int32_t* block_tables, const int32_t* context_lens,
+                                 void* out, void* workspace, size_t workspace_bytes, int batch,
+                                 int num_q_heads, int num_kv_heads, int head_dim,
+                                 int block_size, int max_blocks, int num_pages, float scale,
+                                 int window, int n_sink, int dtype, hipStream_t stream);
+
+/*
  * Rotary position embedding as the reference's RoPE module defines it
  * (src/core/rope_kv.py:22-50): dims (2i, 2i+1) of a head rotate by a = p * f_i at absolute
  * position p, f_i = 1 / theta^(2i/D) (double, stored as float), a = float(p) * f_i:

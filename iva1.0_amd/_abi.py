@@ -95,6 +95,16 @@ SIGNATURES = {
         c_int, c_int, c_int,                   # window, n_sink, dtype
         c_void_p,                              # stream
     ]),
+    "ivakv_decode_append_attn_fp8": (c_int, [
+        c_void_p, c_void_p, c_void_p,          # q, k_new, v_new
+        c_void_p, c_void_p, c_void_p, c_void_p,  # k_pool, v_pool, k_scale, v_scale
+        c_void_p, c_void_p,                    # block_tables, context_lens
+        c_void_p, c_void_p, c_size_t,          # out, workspace, workspace_bytes
+        c_int, c_int, c_int, c_int,            # batch, num_q_heads, num_kv_heads, head_dim
+        c_int, c_int, c_int, c_float,          # block_size, max_blocks, num_pages, scale
+        c_int, c_int, c_int,                   # window, n_sink, dtype
+        c_void_p,                              # stream
+    ]),
     "ivakv_rope": (c_int, [
         c_void_p, c_int64, c_int64, c_void_p,  # x, token / head strides, positions
         c_int, c_int, c_int, c_float, c_int, c_void_p,  # n_tok, H, D, theta, dtype, stream

@@ -28,6 +28,7 @@
 //     and merged through LDS, then across partitions by decode_merge_kernel.
 #include <type_traits>
 
+#include "ivakv_e4m3.h"
 #include "ivakv_tile.h"
 
 namespace ivakv {
@@ -773,7 +774,12 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, 
 // partials of positions < L-1, writes `out`, and stores the new K/V rows into the
 // token's slot for later steps.  Every unit is merged here (the fused walk never
 // writes `out` directly).
-template <int DT, int D>
+//
+// FP8 pools (kFp8): the new rows are quantized as ivakv_append_fp8 does (per-row
+// factor sf = row_sf(max |x|) from a wave reduction over the row, codes e4m3(x * sf)),
+// attended as their dequantized values code / sf -- what an append followed by the
+// walk would read -- and their codes and factors are stored into the slot.
+template <int DT, int D, bool kFp8>
 __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
   using Tr = Traits<DT>;
   using E = typename Tr::E;
@@ -822,6 +828,29 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
     nf = split.owner(first_tile + n - 1) - k0 + 1;
   }
   const int64_t base = k0 + (int64_t)b * Hkv + h;
+  // The new K row, lane-strided (dims lane + 64j); FP8: its and the V row's factors
+  // (every lane ends with the row's max) and the dequantized K values.
+  float kv[DL];
+#pragma unroll
+  for (int j = 0; j < DL; ++j) kv[j] = (float)kn[lane + 64 * j];
+  float sfk = 1.f, sfv = 1.f;
+  if constexpr (kFp8) {
+    float ka = 0.f, va = 0.f;
+#pragma unroll
+    for (int j = 0; j < DL; ++j) {
+      ka = fmaxf(ka, fabsf(kv[j]));
+      va = fmaxf(va, fabsf((float)vn[lane + 64 * j]));
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      ka = fmaxf(ka, __shfl_xor(ka, o));
+      va = fmaxf(va, __shfl_xor(va, o));
+    }
+    sfk = row_sf(ka);
+    sfv = row_sf(va);
+#pragma unroll
+    for (int j = 0; j < DL; ++j) kv[j] = e4m3_decode(e4m3_encode(kv[j] * sfk)) / sfk;
+  }
   // D is a multiple of 64, so the 64 outputs of a wave share one query head g,
   // and the wave scores the new token for g with a lane-strided dot product.
   // Its operands (and the value element) are loaded before the partials, so
@@ -829,13 +858,11 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
   // folded, then the new token.
   for (int idx = idx0; idx < G * D; idx += stride) {
     const int g = idx / D;
-    float qv[DL], kv[DL];
+    float qv[DL];
 #pragma unroll
-    for (int j = 0; j < DL; ++j) {
-      qv[j] = (float)qb[g * D + lane + 64 * j];
-      kv[j] = (float)kn[lane + 64 * j];
-    }
-    const float vv = (float)vn[idx - g * D];
+    for (int j = 0; j < DL; ++j) qv[j] = (float)qb[g * D + lane + 64 * j];
+    float vv = (float)vn[idx - g * D];
+    if constexpr (kFp8) vv = e4m3_decode(e4m3_encode(vv * sfv)) / sfv;
     float M = kNegInf, L_sum = 0.f, O = 0.f;
     fold_slots(a, g, idx, D, (int)nf, [&](int i) { return base + i; }, M, L_sum, O);
     float dot = 0.f;
@@ -853,15 +880,30 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
     out[idx] = Tr::from_float(L_sum > 0.f ? O / L_sum : 0.f);
   }
 
-  // Append: the new rows go to the slot of position L-1.
+  // Append: the new rows go to the slot of position L-1.  (Threads d < D ran the
+  // element loop's wave, so their sfk / sfv are the row's.)
   if (new_ok && blockIdx.z == 0) {
-    constexpr int X = 16 / (int)sizeof(E);
-    const int64_t tile = (page * Hkv + h) * (int64_t)D * kBS;
-    E* kp = static_cast<E*>(const_cast<void*>(a.k_pool)) + tile;
-    E* vp = static_cast<E*>(const_cast<void*>(a.v_pool)) + tile;
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-      kp[((d / X) * kBS + row) * X + d % X] = kn[d];
-      vp[d * kBS + row] = vn[d];
+    if constexpr (kFp8) {
+      const int64_t tile = page * Hkv + h;
+      uint8_t* kp = static_cast<uint8_t*>(const_cast<void*>(a.k_pool)) + tile * D * kBS;
+      uint8_t* vp = static_cast<uint8_t*>(const_cast<void*>(a.v_pool)) + tile * D * kBS;
+      for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        kp[((d >> 4) * kBS + row) * 16 + (d & 15)] = (uint8_t)e4m3_encode((float)kn[d] * sfk);
+        vp[fp8_v_offset(d, row, D)] = (uint8_t)e4m3_encode((float)vn[d] * sfv);
+      }
+      if (threadIdx.x == 0) {
+        const_cast<float*>(a.k_scale)[tile * kBS + row] = sfk;
+        const_cast<float*>(a.v_scale)[tile * kBS + row] = sfv;
+      }
+    } else {
+      constexpr int X = 16 / (int)sizeof(E);
+      const int64_t tile = (page * Hkv + h) * (int64_t)D * kBS;
+      E* kp = static_cast<E*>(const_cast<void*>(a.k_pool)) + tile;
+      E* vp = static_cast<E*>(const_cast<void*>(a.v_pool)) + tile;
+      for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        kp[((d / X) * kBS + row) * X + d % X] = kn[d];
+        vp[d * kBS + row] = vn[d];
+      }
     }
   }
 }
@@ -960,9 +1002,9 @@ void launch_stream(Stage stage, int D, dim3 grid, size_t smem, hipStream_t strea
   const dim3 mgrid((unsigned)a.Hkv, (unsigned)a.batch, (unsigned)zsplit);
   if (stage == kFused) {
     switch (D) {
-      case 64: decode_fused_merge_kernel<DT, 64><<<mgrid, threads, 0, stream>>>(a); break;
-      case 128: decode_fused_merge_kernel<DT, 128><<<mgrid, threads, 0, stream>>>(a); break;
-      default: decode_fused_merge_kernel<DT, 256><<<mgrid, threads, 0, stream>>>(a); break;
+      case 64: decode_fused_merge_kernel<DT, 64, kFp8><<<mgrid, threads, 0, stream>>>(a); break;
+      case 128: decode_fused_merge_kernel<DT, 128, kFp8><<<mgrid, threads, 0, stream>>>(a); break;
+      default: decode_fused_merge_kernel<DT, 256, kFp8><<<mgrid, threads, 0, stream>>>(a); break;
     }
   }
   else if (stage != kPartial)
@@ -1137,6 +1179,21 @@ extern "C" int ivakv_decode_append_attn(const void* q, const void* k_new, const 
                       context_lens, out, workspace, workspace_bytes, batch, num_q_heads,
                       num_kv_heads, head_dim, block_size, max_blocks, num_pages, scale, window,
                       n_sink, 0, dtype, stream, k_new, v_new);
+}
+
+extern "C" int ivakv_decode_append_attn_fp8(const void* q, const void* k_new, const void* v_new,
+                                            void* k_pool, void* v_pool, float* k_scale,
+                                            float* v_scale, const int32_t* block_tables,
+                                            const int32_t* context_lens, void* out,
+                                            void* workspace, size_t workspace_bytes, int batch,
+                                            int num_q_heads, int num_kv_heads, int head_dim,
+                                            int block_size, int max_blocks, int num_pages,
+                                            float scale, int window, int n_sink, int dtype,
+                                            hipStream_t stream) {
+  return decode_entry(kFused, "ivakv_decode_append_attn_fp8", q, k_pool, v_pool, block_tables,
+                      context_lens, out, workspace, workspace_bytes, batch, num_q_heads,
+                      num_kv_heads, head_dim, block_size, max_blocks, num_pages, scale, window,
+                      n_sink, 0, dtype, stream, k_new, v_new, k_scale, v_scale, true);
 }
 
 extern "C" int ivakv_decode_attn_fp8(const void* q, const void* k_pool, const void* v_pool,

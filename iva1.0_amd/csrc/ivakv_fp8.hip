@@ -13,54 +13,17 @@
 //
 // Conversions are written out in integer arithmetic (round to nearest even,
 // saturating at +-448), so the codes do not depend on a hardware rounding mode.
-#include "ivakv_internal.h"
+#include "ivakv_e4m3.h"
 
 namespace ivakv {
 namespace {
 
-constexpr float kFp8Max = 448.f;
 constexpr int64_t kMaxGrid8 = 0x7fffffff;
-
-// float -> e4m3fn code, round to nearest even, saturating at +-448 (NaN -> 0x7F).
-__device__ inline uint32_t e4m3_encode(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  const uint32_t au = u & 0x7fffffffu;
-  if (au > 0x7f800000u) return sign | 0x7Fu;  // NaN
-  const float a = __uint_as_float(au);
-  uint32_t code;
-  if (a < 0.015625f) {  // below 2^-6: subnormal grid step 2^-9
-    code = (uint32_t)__builtin_rintf(a * 512.f);  // 0..8 (8 = smallest normal)
-  } else {
-    // keep 3 mantissa bits with round-to-nearest-even on the float's own bits,
-    // then rebias the exponent from 127 to 7
-    const uint32_t r = (au + 0x7FFFFu + ((au >> 20) & 1u)) >> 20;
-    code = r >= (127u - 7u) * 8u + 0x7Fu ? 0x7Eu : r - (127u - 7u) * 8u;
-  }
-  return sign | (code > 0x7Eu ? 0x7Eu : code);
-}
-
-// e4m3fn code -> float, exactly.
-__device__ inline float e4m3_decode(uint32_t b) {
-  const uint32_t e = (b >> 3) & 0xFu, m = b & 7u;
-  float v;
-  if (e == 0) v = (float)m * 0.001953125f;                       // m * 2^-9
-  else if (e == 15 && m == 7) v = __uint_as_float(0x7fc00000u);  // NaN
-  else v = __uint_as_float(((e + 120u) << 23) | (m << 20));
-  return (b & 0x80u) ? -v : v;
-}
 
 template <typename E>
 __device__ inline float to_f(E x) { return (float)x; }
 template <>
 __device__ inline float to_f<float>(float x) { return x; }
-
-// Scaling factor of a row with max |x| = amax.
-__device__ inline float row_sf(float amax) {
-  if (!(amax > 0.f)) return 1.f;
-  const float sf = kFp8Max / amax;
-  return fminf(fmaxf(sf, 1e-8f), 1e8f);
-}
 
 struct Append8Args {
   const void* k_new;

@@ -49,7 +49,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .ops import (kv_gather, paged_decode_append_attention, paged_decode_attention,
+from .ops import (kv_gather, paged_decode_append_attention,
                   paged_prefill_attention, rope_)
 from .paged_cache import PagedKVCache
 
@@ -354,23 +354,17 @@ class PagedAttention(_AttentionBase):
         else:
             decode = s == 1 and self.causal
             fp8 = kv_cache.pool.fp8
-            view = kv_cache.layer_step(k.contiguous(), v.contiguous(), append=fp8 or not decode,
+            view = kv_cache.layer_step(k.contiguous(), v.contiguous(), append=not decode,
                                        rope_positions=rope_pos, rope_theta=self.rope_theta)
-            if decode and fp8:
-                # FP8 pages: the append above quantized the row; attend over the pages
-                o = paged_decode_attention(
-                    q.view(b, self.n_heads, self.head_dim), view.k_pool, view.v_pool,
-                    view.block_tables, view.context_lens, scale=self.scale, window=window or 0,
-                    n_sink=n_sink if window else 0, **view.scales)
-                out = o.view(b, 1, self.n_heads, self.head_dim)
-            elif decode:
+            if decode:
                 # append + attend in one op: the new row lands at position L-1 of each page
-                # table and is scored straight from k / v (ivakv_decode_append_attn)
+                # table and is scored straight from k / v (ivakv_decode_append_attn; on
+                # FP8 pages quantized as the append would, ivakv_decode_append_attn_fp8)
                 o = paged_decode_append_attention(
                     q.view(b, self.n_heads, self.head_dim), k.view(b, self.n_kv_heads, self.head_dim),
                     v.view(b, self.n_kv_heads, self.head_dim), view.k_pool, view.v_pool,
                     view.block_tables, view.context_lens, scale=self.scale, window=window or 0,
-                    n_sink=n_sink if window else 0)
+                    n_sink=n_sink if window else 0, **view.scales)
                 out = o.view(b, 1, self.n_heads, self.head_dim)
             elif self.causal and not fp8:
                 # the chunk's rows sit at positions start .. start+s-1 of every sequence

@@ -328,12 +328,18 @@ def paged_decode_append_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: t
                                   block_tables: torch.Tensor, context_lens: torch.Tensor,
                                   scale: Optional[float] = None, window: Optional[int] = None,
                                   n_sink: int = 0, out: Optional[torch.Tensor] = None,
-                                  workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                                  workspace: Optional[torch.Tensor] = None,
+                                  k_scale: Optional[torch.Tensor] = None,
+                                  v_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
     """One decode step in one op: the new token of sequence b sits at position
     ``context_lens[b] - 1``; its rows ``k_new[b], v_new[b]`` ([B, Hkv, D]) are written to
     that position's slot and attended together with the earlier positions in the pages.
     Same result as :func:`kv_append` of those rows followed by
     :func:`paged_decode_attention`, in two launches (no separate append kernel).
+
+    FP8 pools (``torch.float8_e4m3fn`` with ``k_scale`` / ``v_scale``): ``q``, ``k_new``
+    and ``v_new`` are fp16 or bf16; the new rows are quantized as :func:`kv_append` does
+    (same codes and factors) and attended as their dequantized values.
 
     Fuses the append and the scoring of ``AttentionTorch.forward`` with a cache
     (src/core/attention.py:61-102).
@@ -346,9 +352,13 @@ def paged_decode_append_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: t
     for name, t in (("k_new", k_new), ("v_new", v_new)):
         if tuple(t.shape) != (batch, hkv, head_dim):
             raise ValueError(f"{name} must be [{batch}, {hkv}, {head_dim}]; got {tuple(t.shape)}")
+    fp8 = is_fp8(k_pool)
     for t in (q, k_new, v_new):
-        if t.dtype != k_pool.dtype:
-            raise TypeError(f"dtype {t.dtype} != pool dtype {k_pool.dtype}")
+        if fp8 and t.dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError(f"FP8 pools take float16 or bfloat16 q / k_new / v_new; got {t.dtype}")
+        if t.dtype != (q.dtype if fp8 else k_pool.dtype):
+            raise TypeError(f"dtype {t.dtype} != {q.dtype if fp8 else k_pool.dtype}")
+    scales = _scales(k_pool, k_scale, v_scale) if fp8 else None
     block_tables = _i32(block_tables, "block_tables")
     context_lens = _i32(context_lens, "context_lens").reshape(-1)
     if block_tables.dim() != 2 or block_tables.shape[0] != batch or context_lens.numel() != batch:
@@ -369,6 +379,15 @@ def paged_decode_append_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: t
     elif workspace.numel() * workspace.element_size() < nbytes:
         raise ValueError(f"workspace has {workspace.numel() * workspace.element_size()} bytes, "
                          f"{nbytes} needed")
+    if fp8:
+        _abi.call("ivakv_decode_append_attn_fp8", q.data_ptr(), k_new.data_ptr(),
+                  v_new.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), scales[0].data_ptr(),
+                  scales[1].data_ptr(), block_tables.data_ptr(), context_lens.data_ptr(),
+                  out.data_ptr(), workspace.data_ptr(),
+                  workspace.numel() * workspace.element_size(), batch, hq, hkv, head_dim, bs,
+                  max_blocks, num_pages, float(scale), window, n_sink, dtype_code(q.dtype),
+                  _stream(dev))
+        return out
     _abi.call("ivakv_decode_append_attn", q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
               k_pool.data_ptr(), v_pool.data_ptr(), block_tables.data_ptr(),
               context_lens.data_ptr(), out.data_ptr(), workspace.data_ptr(),

@@ -8,7 +8,9 @@
   * decode attention over FP8 pages (unit-scale data, as the other attention tests):
     within 2e-3 (+ one half-ulp of the output dtype times |exact|) of the fp64 oracle on
     the dequantized pages, fp16 and bf16 queries, windows and sinks, invalid page ids,
-    garbage (NaN included) codes past the context.
+    garbage (NaN included) codes past the context;
+  * the fused append + attend op on FP8 pages: pools and factors byte-identical to
+    the oracle's append of the new rows, output within the same bound.
 """
 from __future__ import annotations
 
@@ -143,6 +145,56 @@ def test_decode_fp8_vs_oracle(iva, dev, qdt, d, window, sink):
     assert (err <= bound).all(), f"max err {err.max():.3e}"
 
 
+@pytest.mark.parametrize("qdt", [torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("window,sink", [(0, 0), (70, 4)])
+def test_decode_append_fp8_fused_vs_oracle(iva, dev, qdt, d, window, sink):
+    """The fused op on FP8 pages: pools and factors afterwards byte-identical to the
+    oracle's append of the new rows (the same quantization as kv_append), output within
+    2e-3 of the oracle's decode over the dequantized pages.  An empty sequence (zero
+    row, nothing stored), a sequence of one token (the new token alone) and a new token
+    whose page id is invalid (neither stored nor attended)."""
+    lengths = [0, 1, 16, 17, 100, 257, 513]
+    hq, hkv = 8, 2
+    c = fp8_case(iva, lengths, hkv, d, torch.float32, seed=31 + d, decades=0)
+    offs = np.cumsum([0] + lengths[:-1]).tolist()
+    prev = torch.cat([torch.arange(o, o + n - 1) for o, n in zip(offs, lengths) if n > 1])
+    g, o = append_both(iva, dev, dict(c, k_new=c["k_new"][prev], v_new=c["v_new"][prev],
+                                      slots=c["slots"][prev]))
+    lay = c["layout"]
+    bt = lay.block_tables.clone()
+    bt[4, (lengths[4] - 1) // 16] = -1          # the new token's page of sequence 4
+    ctx = lay.context_lens
+    kn = torch.zeros(len(lengths), hkv, d)
+    vn = torch.zeros(len(lengths), hkv, d)
+    step_slots = torch.full((len(lengths),), -1, dtype=torch.int32)
+    for b, (off, n) in enumerate(zip(offs, lengths)):
+        if n == 0:
+            continue
+        kn[b], vn[b] = c["k_new"][off + n - 1], c["v_new"][off + n - 1]
+        page = int(bt[b, (n - 1) // 16])
+        if page >= 0:
+            step_slots[b] = page * 16 + (n - 1) % 16
+    kn, vn = kn.to(qdt), vn.to(qdt)
+    q = (torch.randn(len(lengths), hq, d, generator=torch.Generator().manual_seed(6)) * d ** -0.5).to(qdt)
+    out = iva.paged_decode_append_attention(q.to(dev), kn.to(dev), vn.to(dev), g["k_pool"],
+                                            g["v_pool"], bt.to(dev), ctx.to(dev), window=window,
+                                            n_sink=sink, k_scale=g["k_scale"],
+                                            v_scale=g["v_scale"])
+    orc.append_fp8(o["k_pool"], o["v_pool"], o["k_scale"], o["v_scale"], kn.float().numpy(),
+                   vn.float().numpy(), step_slots.numpy())
+    assert np.array_equal(u8(g["k_pool"]), o["k_pool"]) and np.array_equal(u8(g["v_pool"]), o["v_pool"])
+    assert np.array_equal(g["k_scale"].cpu().numpy(), o["k_scale"])
+    assert np.array_equal(g["v_scale"].cpu().numpy(), o["v_scale"])
+    ref = orc.decode_attention_fp8(q.float().numpy(), o["k_pool"], o["v_pool"], o["k_scale"],
+                                   o["v_scale"], bt.numpy(), ctx.numpy(), window=window,
+                                   n_sink=sink)
+    err = np.abs(out.float().cpu().numpy() - ref)
+    bound = 2e-3 + OUT_ULP[qdt] * np.abs(ref)
+    assert (err <= bound).all(), f"max err {err.max():.3e}"
+    assert not out[0].any()                      # empty sequence
+
+
 def test_fp8_argument_errors(iva, dev):
     c = fp8_case(iva, [20], 2, 64, torch.float16, seed=1)
     g, _ = append_both(iva, dev, c)
@@ -158,3 +210,9 @@ def test_fp8_argument_errors(iva, dev):
     with pytest.raises(ValueError, match="k_scale"):
         iva.kv_append(c["k_new"].to(dev), c["v_new"].to(dev), g["k_pool"], g["v_pool"],
                       c["slots"].to(dev))
+    rows = torch.zeros(1, 2, 64, device=dev).half()
+    with pytest.raises(ValueError, match="k_scale"):
+        iva.paged_decode_append_attention(q, rows, rows, *args[1:])
+    with pytest.raises(TypeError, match="float16 or bfloat16"):
+        iva.paged_decode_append_attention(q, rows.float(), rows, *args[1:], k_scale=g["k_scale"],
+                                          v_scale=g["v_scale"])
