@@ -451,6 +451,29 @@ def bench_prefill(args, iva, torch, dev):
         run(s)
     reps = 40
     t = measure(lambda: [run(sets[i % len(sets)]) for i in range(reps)]) / reps
+    # the same batch over FP8 pages (the fp16 rows quantized by the FP8 append)
+    sets8 = []
+    for s in sets:
+        lay_pages = s[1].shape[0]
+        ks, vs = iva.pool_shapes(lay_pages, hkv, d, 16, torch.float8_e4m3fn)
+        k8 = torch.zeros(ks, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+        v8 = torch.zeros(vs, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+        kss = torch.ones(iva.scale_shape(lay_pages, hkv), device=dev)
+        vss = torch.ones_like(kss)
+        kc, vc = iva.kv_gather(s[1], s[2], s[3], s[4])
+        slots = torch.cat([(s[3][b, torch.arange(n, device=dev) // 16].long() * 16 +
+                            torch.arange(n, device=dev) % 16) for b, n in enumerate(lengths)])
+        rows_k = torch.cat([kc[b, :, :n].transpose(0, 1) for b, n in enumerate(lengths)])
+        rows_v = torch.cat([vc[b, :, :n].transpose(0, 1) for b, n in enumerate(lengths)])
+        iva.kv_append(rows_k, rows_v, k8, v8, slots.int(), k_scale=kss, v_scale=vss)
+        del kc, vc, rows_k, rows_v
+        sets8.append((s[0], k8, v8, s[3], s[4], s[5], s[6], kss, vss))
+    run8 = lambda s: iva.paged_prefill_attention(s[0], s[1], s[2], s[3], s[4], s[5],
+                                                 max_query_len=512, out=s[6], k_scale=s[7],
+                                                 v_scale=s[8])
+    for s in sets8:
+        run8(s)
+    t8 = measure(lambda: [run8(sets8[i % len(sets8)]) for i in range(reps)]) / reps
     flops = sum(4 * d * hq * (L - n + i + 1) for L, n in zip(lengths, chunks) for i in range(n))
     tf = flops / t / 1e12
     return {"metric": "paged chunked-prefill attention TFLOP/s", "workload": "prefill",
@@ -459,7 +482,9 @@ def bench_prefill(args, iva, torch, dev):
                        "head_dim": 128, "launch": "eager"},
             "kernel_us": round(t * 1e6, 2), "algorithmic_flops": flops,
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0,
-                         "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4)}}
+                         "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4)},
+            "fp8_pages_kernel_us": round(t8 * 1e6, 2),
+            "fp8_pages_tflops": round(flops / t8 / 1e12, 1)}
 
 
 def main():

@@ -309,6 +309,22 @@ int ivakv_prefill_attn(const void* q, const void* k_pool, const void* v_pool,
                        int dtype, hipStream_t stream);
 
 /*
+ * ivakv_prefill_attn_fp8: ivakv_prefill_attn over FP8 pools (layout and factors as
+ * ivakv_append_fp8 writes them); q and out of dtype f16 or bf16 (`dtype`).  Keys and
+ * values are dequantized, code / sf rounded once to `dtype`, as they are staged into
+ * LDS; the attention is then the 16-bit kernel's.  k_scale / v_scale 16-byte aligned.
+ * Replaces: the same reference code as ivakv_prefill_attn on a kv_cache_dtype "fp8"
+ * cache (configs/quant_infer.yaml:22,52; scaling rule src/quant/fp8_runtime.py:66-76).
+ */
+int ivakv_prefill_attn_fp8(const void* q, const void* k_pool, const void* v_pool,
+                           const float* k_scale, const float* v_scale,
+                           const int32_t* block_tables, const int32_t* context_lens,
+                           const int32_t* query_start, void* out, int batch, int num_q_heads,
+                           int num_kv_heads, int head_dim, int block_size, int max_blocks,
+                           int num_pages, int max_query_len, float scale, int window,
+                           int n_sink, int dtype, hipStream_t stream);
+
+/*
  * Index gather on a contiguous-layout cache kv = [batch][n_heads][seq_len][D]
  * with element strides (s_b, s_h, s_s, s_d):
  *   out[b, h, j, :] = kv[b, h, indices[j], :]      out = [B][H][n_idx][D] dense

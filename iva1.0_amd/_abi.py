@@ -120,6 +120,16 @@ SIGNATURES = {
         c_void_p, c_void_p, c_int,             # src_pages, dst_pages, n_moves
         c_int, c_int, c_int, c_int, c_void_p,  # Hkv, D, block_size, elem_bytes, stream
     ]),
+    "ivakv_prefill_attn_fp8": (c_int, [
+        c_void_p, c_void_p, c_void_p,          # q, k_pool, v_pool
+        c_void_p, c_void_p,                    # k_scale, v_scale
+        c_void_p, c_void_p, c_void_p,          # block_tables, context_lens, query_start
+        c_void_p,                              # out
+        c_int, c_int, c_int, c_int,            # batch, num_q_heads, num_kv_heads, head_dim
+        c_int, c_int, c_int, c_int, c_float,   # block_size, max_blocks, num_pages, max_query_len, scale
+        c_int, c_int, c_int,                   # window, n_sink, dtype
+        c_void_p,                              # stream
+    ]),
     "ivakv_prefill_attn": (c_int, [
         c_void_p, c_void_p, c_void_p,          # q, k_pool, v_pool
         c_void_p, c_void_p, c_void_p,          # block_tables, context_lens, query_start

@@ -22,6 +22,12 @@
 // the V chunks of the two pages are paired the same way, so P never leaves
 // registers.  Online softmax in fp32, log2 domain, as in the decode kernel.
 // A wave skips pairs that lie entirely after its last row.
+//
+// FP8 pages (kFp8): the staging loads e4m3fn codes (half the bytes) and their
+// per-key scaling factors, and the LDS store converts them, code * (1 / sf) in
+// fp32 rounded once to the query dtype, into the same LDS layout; the loop over
+// pairs is the 16-bit one.  8-byte units (8 dims of one key of K, or 4 keys of
+// two dims of V) spread the conversion over all threads.
 #include "ivakv_tile.h"
 
 namespace ivakv {
@@ -40,6 +46,8 @@ struct PrefillArgs {
   float scale_log2;
   int window, n_sink;
   int blocks_x;  // row-block workgroups per (sequence, kv head)
+  const float* k_scale;  // FP8 pools: [num_pages][Hkv][16] fp32 scaling factors
+  const float* v_scale;
 };
 
 // Shape of the kernel instance.  fp16 / bf16 up to head_dim 128: 8 waves of
@@ -61,7 +69,7 @@ struct PrefillShape {
   static constexpr size_t kLdsBytes = 2 * (size_t)kPairElems * kESize;
 };
 
-template <int DT, int D>
+template <int DT, int D, bool kFp8>
 __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kernel(PrefillArgs a,
                                                              const int32_t* __restrict__ bt,
                                                              const int32_t* __restrict__ ctx,
@@ -210,6 +218,85 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
         dv[tid + S::kThreads * c] = stV[set][c];
   };
 
+  // FP8 staging.  A pair holds 4D 8-byte units of K codes and as many of V codes
+  // (units [0, 2D) page A, [2D, 4D) page B).  K unit j of a page: codes of dims
+  // 16(j/32) + 8(j%2) .. +8 of key (j/2)%16, which become the 16-bit pool layout's
+  // chunk (2(j/32) + j%2)*16 + key.  V unit j: words 2j, 2j+1 of the tile's FP8
+  // order [d%16][key/4][d/16][key%4] (ivakv_internal.h fp8_v_offset), i.e. keys
+  // 4g..4g+3 of dims dl + 16m and dl + 16(m+1), which become granule (g, page) of
+  // those two LDS V rows.
+  constexpr int kUnits = 4 * D;                                  // per pair, K or V
+  constexpr int kU8 = kFp8 ? (kUnits + S::kThreads - 1) / S::kThreads : 1;
+  constexpr int kNB8 = D / 16;
+  u32x2 st8K[S::kStages][kU8], st8V[S::kStages][kU8];
+  float sc8K[S::kStages][kU8];
+  f32x4 sc8V[S::kStages][kU8];
+  auto load_pair8 = [&](int pair, int set) {
+    if constexpr (kFp8) {
+    int lp;
+    bool ok;
+    const int64_t tA = page_of(2 * pair, lp, ok) * Hkv + h, tB = page_of(2 * pair + 1, lp, ok) * Hkv + h;
+    const uint8_t* k8 = static_cast<const uint8_t*>(a.k_pool);
+    const uint8_t* v8 = static_cast<const uint8_t*>(a.v_pool);
+#pragma unroll
+    for (int c = 0; c < kU8; ++c) {
+      const int u = min(tid + S::kThreads * c, kUnits - 1);
+      const int64_t t = u < 2 * D ? tA : tB;
+      const int j = u % (2 * D);
+      st8K[set][c] = *reinterpret_cast<const u32x2*>(k8 + t * kTile + 8 * j);
+      sc8K[set][c] = a.k_scale[t * kBS + ((j >> 1) & 15)];
+      st8V[set][c] = *reinterpret_cast<const u32x2*>(v8 + t * kTile + 8 * j);
+      sc8V[set][c] = *reinterpret_cast<const f32x4*>(a.v_scale + t * kBS + 4 * (((2 * j) / kNB8) & 3));
+    }
+    }
+  };
+  // Four codes (one 32-bit word) times four factors, as four values of E.
+  auto dequant4 = [&](uint32_t w, float s0, float s1, float s2, float s3) -> u32x2 {
+    if constexpr (kFp8) {
+      const f32x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, false);
+      const f32x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, true);
+      return u32x2{Tr::pack2(lo[0] * s0, lo[1] * s1), Tr::pack2(hi[0] * s2, hi[1] * s3)};
+    } else {
+      return u32x2{0u, 0u};
+    }
+  };
+  auto store_pair8 = [&](int buf, int set) {
+    if constexpr (kFp8) {
+    u32x4* dk = reinterpret_cast<u32x4*>(lds + buf * (4 * kPageChunks));
+    u32x2* dv = reinterpret_cast<u32x2*>(dk + 2 * kPageChunks);  // V rows of 8 granules
+#pragma unroll
+    for (int c = 0; c < kU8; ++c) {
+      if (kUnits % S::kThreads != 0 && tid + S::kThreads * c >= kUnits) continue;
+      const int u = tid + S::kThreads * c;
+      const int pg = u < 2 * D ? 0 : 1, j = u % (2 * D);
+      // K: one key's 8 dims, one 16-byte LDS chunk
+      const float ik = __builtin_amdgcn_rcpf(sc8K[set][c]);
+      const u32x2 k0 = dequant4(st8K[set][c][0], ik, ik, ik, ik);
+      const u32x2 k1 = dequant4(st8K[set][c][1], ik, ik, ik, ik);
+      const int key = (j >> 1) & 15, ch = (2 * (j >> 5) + (j & 1)) * 16 + key;
+      dk[pg * kPageChunks + ch] = u32x4{k0[0], k0[1], k1[0], k1[1]};
+      // V: keys 4g..4g+3 of two dims, one 8-byte granule in each of two rows
+      const f32x4 sv = sc8V[set][c];
+      const float i0 = __builtin_amdgcn_rcpf(sv[0]), i1 = __builtin_amdgcn_rcpf(sv[1]);
+      const float i2 = __builtin_amdgcn_rcpf(sv[2]), i3 = __builtin_amdgcn_rcpf(sv[3]);
+      const int w0 = 2 * j, m = w0 % kNB8, g = (w0 / kNB8) & 3, dl = w0 / (4 * kNB8);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int d = dl + 16 * (m + e);
+        dv[d * 8 + 2 * g + pg] = dequant4(st8V[set][c][e], i0, i1, i2, i3);
+      }
+    }
+    }
+  };
+  auto load = [&](int pair, int set) {
+    if constexpr (kFp8) load_pair8(pair, set);
+    else load_pair(pair, set);
+  };
+  auto store = [&](int buf, int set) {
+    if constexpr (kFp8) store_pair8(buf, set);
+    else store_pair(buf, set);
+  };
+
   // Interior pairs (every key inside every row's causal window, all keys inside
   // the context on valid pages) skip the per-key masks; that needs every row of
   // the wave to be a real row.
@@ -330,28 +417,28 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
       // i + 1 waits in registers for its LDS buffer.  Loads past the last pair
       // repeat the last page (an L2 hit) into buffers nobody reads; being
       // unconditional keeps the stage in registers.
-      load_pair(0, 0);
-      load_pair(1, 1);
-      store_pair(0, 0);
+      load(0, 0);
+      load(1, 1);
+      store(0, 0);
       __syncthreads();
       for (int i = 0; i < n_pairs; i += 2) {
-        load_pair(i + 2, 0);
+        load(i + 2, 0);
         compute(0, i);
-        store_pair(1, 1);
+        store(1, 1);
         __syncthreads();
-        load_pair(i + 3, 1);
+        load(i + 3, 1);
         compute(1, i + 1);
-        store_pair(0, 0);
+        store(0, 0);
         __syncthreads();
       }
     } else {
-      load_pair(0, 0);
-      store_pair(0, 0);
+      load(0, 0);
+      store(0, 0);
       __syncthreads();
       for (int i = 0; i < n_pairs; ++i) {
-        load_pair(i + 1, 0);
+        load(i + 1, 0);
         compute(i & 1, i);
-        store_pair((i + 1) & 1, 0);
+        store((i + 1) & 1, 0);
         __syncthreads();
       }
     }
@@ -374,24 +461,24 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   }
 }
 
-template <int DT, int D>
+template <int DT, int D, bool kFp8>
 void launch_prefill_d(dim3 grid, hipStream_t stream, const PrefillArgs& a, const int32_t* bt,
                       const int32_t* ctx, const int32_t* qs) {
   // LDS beyond 64 KiB (fp32 with head_dim 256) must be allowed per kernel once.
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&prefill_kernel<DT, D>),
+      reinterpret_cast<const void*>(&prefill_kernel<DT, D, kFp8>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)PrefillShape<DT, D>::kLdsBytes);
   (void)attr;
-  prefill_kernel<DT, D><<<grid, PrefillShape<DT, D>::kThreads, PrefillShape<DT, D>::kLdsBytes, stream>>>(a, bt, ctx, qs);
+  prefill_kernel<DT, D, kFp8><<<grid, PrefillShape<DT, D>::kThreads, PrefillShape<DT, D>::kLdsBytes, stream>>>(a, bt, ctx, qs);
 }
 
-template <int DT>
+template <int DT, bool kFp8 = false>
 void launch_prefill(int head_dim, dim3 grid, hipStream_t stream, const PrefillArgs& a,
                     const int32_t* bt, const int32_t* ctx, const int32_t* qs) {
   switch (head_dim) {
-    case 64: launch_prefill_d<DT, 64>(grid, stream, a, bt, ctx, qs); break;
-    case 128: launch_prefill_d<DT, 128>(grid, stream, a, bt, ctx, qs); break;
-    default: launch_prefill_d<DT, 256>(grid, stream, a, bt, ctx, qs); break;
+    case 64: launch_prefill_d<DT, 64, kFp8>(grid, stream, a, bt, ctx, qs); break;
+    case 128: launch_prefill_d<DT, 128, kFp8>(grid, stream, a, bt, ctx, qs); break;
+    default: launch_prefill_d<DT, 256, kFp8>(grid, stream, a, bt, ctx, qs); break;
   }
 }
 
@@ -412,19 +499,15 @@ int rows_per_workgroup(int dtype, int head_dim) {
   }
 }
 
-}  // namespace
-}  // namespace ivakv
-
-using namespace ivakv;
-
-extern "C" int ivakv_prefill_attn(const void* q, const void* k_pool, const void* v_pool,
-                                  const int32_t* block_tables, const int32_t* context_lens,
-                                  const int32_t* query_start, void* out, int batch,
-                                  int num_q_heads, int num_kv_heads, int head_dim, int block_size,
-                                  int max_blocks, int num_pages, int max_query_len, float scale,
-                                  int window, int n_sink, int dtype, hipStream_t stream) {
-  static const char* name = "ivakv_prefill_attn";
+int prefill_entry(const char* name, const void* q, const void* k_pool, const void* v_pool,
+                  const float* k_scale, const float* v_scale, const int32_t* block_tables,
+                  const int32_t* context_lens, const int32_t* query_start, void* out, int batch,
+                  int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                  int max_blocks, int num_pages, int max_query_len, float scale, int window,
+                  int n_sink, int dtype, hipStream_t stream, bool fp8) {
   if (dtype_size(dtype) == 0) return fail(IVAKV_E_DTYPE, "%s: unknown dtype code %d", name, dtype);
+  if (fp8 && dtype != IVAKV_F16 && dtype != IVAKV_BF16)
+    return fail(IVAKV_E_DTYPE, "%s: FP8 pools take fp16 or bf16 queries (dtype %d)", name, dtype);
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_blocks < 0 || max_query_len < 0)
     return fail(IVAKV_E_ARG, "%s: bad sizes B=%d Hq=%d Hkv=%d max_blocks=%d max_query_len=%d",
                 name, batch, num_q_heads, num_kv_heads, max_blocks, max_query_len);
@@ -443,6 +526,8 @@ extern "C" int ivakv_prefill_attn(const void* q, const void* k_pool, const void*
     return fail(IVAKV_E_ARG, "%s: null pointer argument", name);
   if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out))
     return fail(IVAKV_E_ARG, "%s: q, pools and out must be 16-byte aligned", name);
+  if (fp8 && (!k_scale || !v_scale || !aligned16(k_scale) || !aligned16(v_scale)))
+    return fail(IVAKV_E_ARG, "%s: k_scale / v_scale must be 16-byte aligned device pointers", name);
   if (!(scale == scale)) return fail(IVAKV_E_ARG, "%s: scale is NaN", name);
   const int G = num_q_heads / num_kv_heads;
   const int64_t rows = (int64_t)max_query_len * G;
@@ -464,15 +549,53 @@ extern "C" int ivakv_prefill_attn(const void* q, const void* k_pool, const void*
   a.window = window > 0 ? window : 0;
   a.n_sink = n_sink;
   a.blocks_x = (int)blocks_x;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
   // 1-D grid in XCD-aware order (see prefill_kernel): 8 interleaved unit streams.
   const int64_t units_per_xcd = ((int64_t)batch * num_kv_heads + 7) / 8;
   const int64_t n_wg = units_per_xcd * blocks_x * 8;
   if (n_wg > 0x7fffffff) return fail(IVAKV_E_SHAPE, "%s: launch too large", name);
   const dim3 grid((unsigned)n_wg);
+  if (fp8) {
+    if (dtype == IVAKV_F16) launch_prefill<IVAKV_F16, true>(head_dim, grid, stream, a, block_tables, context_lens, query_start);
+    else launch_prefill<IVAKV_BF16, true>(head_dim, grid, stream, a, block_tables, context_lens, query_start);
+    return launch_status(name);
+  }
   switch (dtype) {
     case IVAKV_F16: launch_prefill<IVAKV_F16>(head_dim, grid, stream, a, block_tables, context_lens, query_start); break;
     case IVAKV_BF16: launch_prefill<IVAKV_BF16>(head_dim, grid, stream, a, block_tables, context_lens, query_start); break;
     default: launch_prefill<IVAKV_F32>(head_dim, grid, stream, a, block_tables, context_lens, query_start); break;
   }
   return launch_status(name);
+}
+
+}  // namespace
+}  // namespace ivakv
+
+using namespace ivakv;
+
+extern "C" int ivakv_prefill_attn(const void* q, const void* k_pool, const void* v_pool,
+                                  const int32_t* block_tables, const int32_t* context_lens,
+                                  const int32_t* query_start, void* out, int batch,
+                                  int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                  int max_blocks, int num_pages, int max_query_len, float scale,
+                                  int window, int n_sink, int dtype, hipStream_t stream) {
+  return prefill_entry("ivakv_prefill_attn", q, k_pool, v_pool, nullptr, nullptr, block_tables,
+                       context_lens, query_start, out, batch, num_q_heads, num_kv_heads,
+                       head_dim, block_size, max_blocks, num_pages, max_query_len, scale, window,
+                       n_sink, dtype, stream, false);
+}
+
+extern "C" int ivakv_prefill_attn_fp8(const void* q, const void* k_pool, const void* v_pool,
+                                      const float* k_scale, const float* v_scale,
+                                      const int32_t* block_tables, const int32_t* context_lens,
+                                      const int32_t* query_start, void* out, int batch,
+                                      int num_q_heads, int num_kv_heads, int head_dim,
+                                      int block_size, int max_blocks, int num_pages,
+                                      int max_query_len, float scale, int window, int n_sink,
+                                      int dtype, hipStream_t stream) {
+  return prefill_entry("ivakv_prefill_attn_fp8", q, k_pool, v_pool, k_scale, v_scale,
+                       block_tables, context_lens, query_start, out, batch, num_q_heads,
+                       num_kv_heads, head_dim, block_size, max_blocks, num_pages, max_query_len,
+                       scale, window, n_sink, dtype, stream, true);
 }

@@ -14,6 +14,9 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 struct alignas(16) Chunk16 {
   uint32_t w[4];
@@ -62,6 +65,10 @@ struct Traits<IVAKV_F16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, v), p, acc, 0, 0, 0);
   }
   static __device__ inline E from_float(float x) { return (E)x; }
+  // Two values rounded to E (nearest even), packed low first.
+  static __device__ inline uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, f16x2{(_Float16)a, (_Float16)b});
+  }
   static __device__ inline void mask_rows(VChunk& v, const bool vis[4]) { mask_rows16(v, vis); }
 };
 
@@ -112,6 +119,9 @@ struct Traits<IVAKV_BF16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, p.lo, acc, 0, 0, 0);
   }
   static __device__ inline E from_float(float x) { return (E)x; }
+  static __device__ inline uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, bf16x2{(__bf16)a, (__bf16)b});
+  }
   static __device__ inline void mask_rows(VChunk& v, const bool vis[4]) { mask_rows16(v, vis); }
 };
 

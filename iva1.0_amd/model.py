@@ -366,16 +366,18 @@ class PagedAttention(_AttentionBase):
                     view.block_tables, view.context_lens, scale=self.scale, window=window or 0,
                     n_sink=n_sink if window else 0, **view.scales)
                 out = o.view(b, 1, self.n_heads, self.head_dim)
-            elif self.causal and not fp8:
+            elif self.causal and (not fp8 or q.dtype in (torch.float16, torch.bfloat16)):
                 # the chunk's rows sit at positions start .. start+s-1 of every sequence
+                # (FP8 pages: dequantized inside the kernel, ivakv_prefill_attn_fp8)
                 qs = torch.arange(0, (b + 1) * s, s, dtype=torch.int32, device=x.device)
                 o = paged_prefill_attention(
                     q.reshape(b * s, self.n_heads, self.head_dim), view.k_pool, view.v_pool,
                     view.block_tables, view.context_lens, qs, scale=self.scale,
-                    window=window or 0, n_sink=n_sink if window else 0, max_query_len=s)
+                    window=window or 0, n_sink=n_sink if window else 0, max_query_len=s,
+                    **view.scales)
                 out = o.view(b, s, self.n_heads, self.head_dim)
             else:
-                # non-causal, or a multi-token step over FP8 pages: gather (dequantized)
+                # non-causal (or fp32 queries on FP8 pages): gather (dequantized for FP8)
                 # and evaluate the masked attention of the new tokens in torch
                 total = view.start + s
                 kw = dict(view.scales, out_dtype=q.dtype) if fp8 else {}

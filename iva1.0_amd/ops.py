@@ -457,7 +457,9 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
                             query_start: torch.Tensor, scale: Optional[float] = None,
                             window: Optional[int] = None, n_sink: int = 0,
                             max_query_len: Optional[int] = None,
-                            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                            out: Optional[torch.Tensor] = None,
+                            k_scale: Optional[torch.Tensor] = None,
+                            v_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Causal multi-query attention of chunks of new tokens over paged K/V.
 
     ``q`` is ``[n_tok, Hq, D]``; the rows of sequence b are
@@ -467,6 +469,9 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
     within the window (``j > p - window``) or among the first ``n_sink`` positions.
     Returns ``[n_tok, Hq, D]``.  ``max_query_len`` (>= every chunk length) sizes the
     launch; when omitted it is read back from ``query_start`` (a device sync).
+    FP8 pools (``torch.float8_e4m3fn`` with ``k_scale`` / ``v_scale``) take fp16 or bf16
+    queries; keys and values are dequantized (code / sf, rounded to the query dtype)
+    on their way into LDS.
 
     Replaces ``AttentionTorch.forward`` with a cache and ``seq_len > 1``
     (src/core/attention.py:61-102), with the causal, window and sink masks
@@ -476,7 +481,12 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
     num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
     if q.dim() != 3 or q.shape[2] != head_dim:
         raise ValueError(f"q must be [n_tok, Hq, {head_dim}]; got {tuple(q.shape)}")
-    if q.dtype != k_pool.dtype:
+    fp8 = is_fp8(k_pool)
+    if fp8:
+        if q.dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError(f"FP8 pools take float16 or bfloat16 queries, got {q.dtype}")
+        scales = _scales(k_pool, k_scale, v_scale)
+    elif q.dtype != k_pool.dtype:
         raise TypeError(f"q dtype {q.dtype} != pool dtype {k_pool.dtype}")
     hq = q.shape[1]
     block_tables = _i32(block_tables, "block_tables")
@@ -498,6 +508,13 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
         out = torch.empty_like(q)
     elif tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous tensor shaped and typed like q")
+    if fp8:
+        _abi.call("ivakv_prefill_attn_fp8", q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+                  scales[0].data_ptr(), scales[1].data_ptr(), block_tables.data_ptr(),
+                  context_lens.data_ptr(), query_start.data_ptr(), out.data_ptr(), batch, hq,
+                  hkv, head_dim, bs, block_tables.shape[1], num_pages, int(max_query_len),
+                  float(scale), window, n_sink, dtype_code(q.dtype), _stream(dev))
+        return out
     _abi.call("ivakv_prefill_attn", q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
               block_tables.data_ptr(), context_lens.data_ptr(), query_start.data_ptr(),
               out.data_ptr(), batch, hq, hkv, head_dim, bs, block_tables.shape[1], num_pages,

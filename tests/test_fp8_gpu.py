@@ -10,7 +10,8 @@
     the dequantized pages, fp16 and bf16 queries, windows and sinks, invalid page ids,
     garbage (NaN included) codes past the context;
   * the fused append + attend op on FP8 pages: pools and factors byte-identical to
-    the oracle's append of the new rows, output within the same bound.
+    the oracle's append of the new rows, output within the same bound;
+  * chunked prefill over FP8 pages vs the oracle's prefill on the dequantized pages.
 """
 from __future__ import annotations
 
@@ -193,6 +194,34 @@ def test_decode_append_fp8_fused_vs_oracle(iva, dev, qdt, d, window, sink):
     bound = 2e-3 + OUT_ULP[qdt] * np.abs(ref)
     assert (err <= bound).all(), f"max err {err.max():.3e}"
     assert not out[0].any()                      # empty sequence
+
+
+@pytest.mark.parametrize("qdt", [torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("window,sink", [(0, 0), (50, 4)])
+def test_prefill_fp8_vs_oracle(iva, dev, qdt, d, window, sink):
+    """Chunked prefill over FP8 pages (garbage codes, NaN included, past every context;
+    an invalid page id inside one) vs the fp64 oracle's prefill over the dequantized
+    pages.  Keys and values are rounded once to the query dtype on their way into LDS,
+    so bf16 carries one more 2^-9 relative rounding of K and V than the decode walk."""
+    lengths, chunks = [1, 17, 300, 45, 130], [1, 17, 37, 0, 64]
+    hq, hkv = 8, 2
+    c = fp8_case(iva, lengths, hkv, d, torch.float32, seed=41 + d, decades=0)
+    g, o = append_both(iva, dev, c)
+    lay = c["layout"]
+    bt = lay.block_tables.clone()
+    bt[2, 5] = -1                               # an invalid page inside a context
+    qs = torch.tensor(np.cumsum([0] + chunks), dtype=torch.int32)
+    q = (torch.randn(int(qs[-1]), hq, d, generator=torch.Generator().manual_seed(9)) * d ** -0.5).to(qdt)
+    out = iva.paged_prefill_attention(q.to(dev), g["k_pool"], g["v_pool"], bt.to(dev),
+                                      lay.context_lens.to(dev), qs.to(dev), window=window,
+                                      n_sink=sink, k_scale=g["k_scale"], v_scale=g["v_scale"])
+    kd, vd = orc.dequantize_pools(o["k_pool"], o["v_pool"], o["k_scale"], o["v_scale"], np.float64)
+    ref = orc.prefill_attention(q.double().numpy(), kd, vd, bt.numpy(), lay.context_lens.numpy(),
+                                qs.numpy(), window=window, n_sink=sink)
+    err = np.abs(out.float().cpu().numpy() - ref)
+    bound = 2e-3 + OUT_ULP[qdt] * np.abs(ref)
+    assert (err <= bound).all(), f"max err {err.max():.3e}"
 
 
 def test_fp8_argument_errors(iva, dev):
