@@ -58,15 +58,29 @@ struct PrefillArgs {
 template <int DT, int D>
 struct PrefillShape {
   static constexpr int kESize = DT == IVAKV_F32 ? 4 : 2;
+#ifdef IVAKV_PF_WAVES
+  static constexpr int kWaves = (DT == IVAKV_F32 || D == 256) ? 4 : IVAKV_PF_WAVES;
+#else
   static constexpr int kWaves = (DT == IVAKV_F32 || D == 256) ? 4 : 8;
+#endif
   static constexpr int kThreads = 64 * kWaves;
+#ifdef IVAKV_PF_NR
+  static constexpr int NR = (DT == IVAKV_F32 || D == 256) ? 2 : IVAKV_PF_NR;
+#else
   static constexpr int NR = 2;
+#endif
+#ifdef IVAKV_PF_STAGES
+  static constexpr int kStages = (DT == IVAKV_F32 || D == 256) ? 1 : IVAKV_PF_STAGES;
+#else
   static constexpr int kStages = kWaves == 8 ? 2 : 1;  // pairs in flight in registers
+#endif
   static constexpr int kRowsWave = 16 * NR;
   static constexpr int kRowsWG = kRowsWave * kWaves;
   static constexpr int kPageElems = kBS * D;          // one K or V page tile
   static constexpr int kPairElems = 4 * kPageElems;   // K_A, K_B, V_A, V_B
-  static constexpr size_t kLdsBytes = 2 * (size_t)kPairElems * kESize;
+  // LDS pair buffers: three for the pipelined loop (two stage sets), else two.
+  static constexpr int kBufs = kStages == 2 ? 3 : 2;
+  static constexpr size_t kLdsBytes = kBufs * (size_t)kPairElems * kESize;
 };
 
 template <int DT, int D, bool kFp8>
@@ -303,24 +317,48 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   const bool rows_all_valid = r_w + S::kRowsWave <= rows && first_pos + r_w / G >= 0;
   const int wave_p_lo = first_pos + r_w / G;
 
-  auto compute = [&](int buf, int pair) {
-    int lpa, lpb;
-    bool oka, okb;
+  // A pair's step is split in two: qk_pair (K from LDS, the QK MFMAs of every row
+  // block) and sm_pv (V from LDS, softmax, PV MFMAs), so the pipelined loop can
+  // issue the next pair's QK before this pair's softmax.
+  struct PairS {
+    f32x4 sa[NR], sb[NR];
+  };
+  // Skip a pair past the walk or entirely after every row of the wave.
+  auto pair_live = [&](int pair, int& lpa, int& lpb, bool& oka, bool& okb) -> bool {
     page_of(2 * pair, lpa, oka);
     page_of(2 * pair + 1, lpb, okb);
-    // Skip a pair past the walk or entirely after every row of the wave.
-    if (pair < n_pairs && lpa * kBS <= wave_p_hi) {
-    const bool interior = rows_all_valid && oka && okb && lpb * kBS + kBS - 1 <= wave_p_lo &&
-                          (a.window <= 0 || lpa * kBS > wave_p_hi - a.window);
+    return pair < n_pairs && lpa * kBS <= wave_p_hi;
+  };
+  auto qk_pair = [&](int buf, int pair, PairS& sc) {
+    int lpa, lpb;
+    bool oka, okb;
+    if (!pair_live(pair, lpa, lpb, oka, okb)) return;
     const E* kA = reinterpret_cast<const E*>(lds + buf * (4 * kPageChunks));
     const E* kB = kA + S::kPageElems;
-    const char* vP = reinterpret_cast<const char*>(kB + S::kPageElems);
     Chunk16 ka[KLD], kb[KLD];
 #pragma unroll
     for (int j = 0; j < KLD; ++j) {
       ka[j] = *reinterpret_cast<const Chunk16*>(kA + ((4 * j + lq) * kBS + ln) * X);
       kb[j] = *reinterpret_cast<const Chunk16*>(kB + ((4 * j + lq) * kBS + ln) * X);
     }
+#pragma unroll
+    for (int rb = 0; rb < NR; ++rb) {
+      sc.sa[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      sc.sb[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < KLD; ++j) {
+        sc.sa[rb] = Tr::qk(ka[j], qr[rb][j], sc.sa[rb]);
+        sc.sb[rb] = Tr::qk(kb[j], qr[rb][j], sc.sb[rb]);
+      }
+    }
+  };
+  auto sm_pv = [&](int buf, int pair, const PairS& sc) {
+    int lpa, lpb;
+    bool oka, okb;
+    if (!pair_live(pair, lpa, lpb, oka, okb)) return;
+    const bool interior = rows_all_valid && oka && okb && lpb * kBS + kBS - 1 <= wave_p_lo &&
+                          (a.window <= 0 || lpa * kBS > wave_p_hi - a.window);
+    const char* vP = reinterpret_cast<const char*>(lds + buf * (4 * kPageChunks) + 2 * kPageChunks);
     VChunk va[NB], vb[NB];
 #pragma unroll
     for (int m = 0; m < NB; ++m) {
@@ -343,26 +381,13 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
         Tr::mask_rows(vb[m], vrb);
       }
     }
-    // All QK products first: the MFMAs of block rb + 1 run while block rb's
-    // softmax is on the VALU.
-    f32x4 sa[NR], sb[NR];
-#pragma unroll
-    for (int rb = 0; rb < NR; ++rb) {
-      sa[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      sb[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < KLD; ++j) {
-        sa[rb] = Tr::qk(ka[j], qr[rb][j], sa[rb]);
-        sb[rb] = Tr::qk(kb[j], qr[rb][j], sb[rb]);
-      }
-    }
 #pragma unroll
     for (int rb = 0; rb < NR; ++rb) {
       float sl[8];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sl[r] = sa[rb][r];
-        sl[4 + r] = sb[rb][r];
+        sl[r] = sc.sa[rb][r];
+        sl[4 + r] = sc.sb[rb][r];
       }
       if (!interior) {
         const int qp = qpos[rb];
@@ -406,29 +431,43 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
 #pragma unroll
       for (int m = 0; m < NB; ++m) acc[rb][m] = Tr::pv32(va[m], vb[m], p8, acc[rb][m]);
     }
-    }
+  };
+  auto compute = [&](int buf, int pair) {
+    PairS sc;
+    qk_pair(buf, pair, sc);
+    sm_pv(buf, pair, sc);
   };
 
   // Ring: pair i is in LDS buffer i % 2 while pair i + 1 travels from HBM / L2
   // into the staging registers; one barrier per pair.
   if (n_pairs > 0) {
     if constexpr (S::kStages == 2) {
-      // Two stage sets: pair i + 2 is loaded while pair i is computed and pair
-      // i + 1 waits in registers for its LDS buffer.  Loads past the last pair
-      // repeat the last page (an L2 hit) into buffers nobody reads; being
-      // unconditional keeps the stage in registers.
+      // Software pipeline over three LDS buffers (pair p in buffer p % 3) and two
+      // stage sets (pair p in set p % 2).  Step i stores pair i + 2 and loads pair
+      // i + 4 into the set it frees, issues the QK MFMAs of pair i + 1, then runs
+      // pair i's softmax (on the VALU while those MFMAs execute) and PV.  One
+      // barrier per step: it publishes pair i + 2 and retires pair i - 1's
+      // buffer.  Loads past the last pair repeat the last page (an L2 hit) into
+      // buffers nobody reads; being unconditional keeps the stage in registers.
+      PairS s0, s1;
       load(0, 0);
       load(1, 1);
       store(0, 0);
+      load(2, 0);
+      store(1, 1);
+      load(3, 1);
       __syncthreads();
+      qk_pair(0, 0, s0);
       for (int i = 0; i < n_pairs; i += 2) {
-        load(i + 2, 0);
-        compute(0, i);
-        store(1, 1);
+        store((i + 2) % 3, 0);
+        load(i + 4, 0);
+        qk_pair((i + 1) % 3, i + 1, s1);
+        sm_pv(i % 3, i, s0);
         __syncthreads();
-        load(i + 3, 1);
-        compute(1, i + 1);
-        store(0, 0);
+        store((i + 3) % 3, 1);
+        load(i + 5, 1);
+        qk_pair((i + 2) % 3, i + 2, s0);
+        sm_pv((i + 1) % 3, i + 1, s1);
         __syncthreads();
       }
     } else {
