@@ -494,7 +494,7 @@ def main():
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                          "(the multi-GPU sharding of the path is described in DESIGN.md)"}))
+                          "(sharding the path over several GPUs is not built)"}))
         sys.exit(2)
 
     import torch
