@@ -466,23 +466,27 @@ __global__ __launch_bounds__(kThreads, kPartialWGsPerCU) void decode_partial_ker
 }
 
 // Log-sum-exp fold of n partial (max, sum, acc) slots into one running state
-// (M, L, O) of output element idx (query head g); slot(i) gives the workspace slot
-// of the i-th partial.  One online pass loads 16 partials' (max, sum, acc)
-// together, so the merge costs one memory round trip per 16 partials instead of
-// separate max / sum / accumulate passes.
-template <typename SlotFn>
+// (M, L, O) of VEC consecutive output elements idx .. idx+VEC-1 (query head g; idx
+// a multiple of VEC, so they share the head); slot(i) gives the workspace slot of
+// the i-th partial.  One online pass loads 16 partials' (max, sum, acc) together,
+// so the merge costs one memory round trip per 16 partials instead of separate max
+// / sum / accumulate passes.
+template <int VEC, typename SlotFn>
 __device__ inline void fold_slots(const DecodeArgs& a, int g, int idx, int D, int n, SlotFn slot,
-                                  float& M, float& L, float& O) {
+                                  float& M, float& L,
+                                  typename std::conditional<VEC == 4, f32x4, float>::type& O) {
+  using OV = typename std::conditional<VEC == 4, f32x4, float>::type;
   const int G = a.G;
   constexpr int U = 16;
   for (int i0 = 0; i0 < n; i0 += U) {
-    float mv[U], lv[U], av[U];
+    float mv[U], lv[U];
+    OV av[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t sl = slot(min(i0 + u, n - 1));
       mv[u] = a.ws_ml[(sl * G + g) * 2];
       lv[u] = a.ws_ml[(sl * G + g) * 2 + 1];
-      av[u] = a.ws_acc[sl * G * D + idx];
+      av[u] = *reinterpret_cast<const OV*>(a.ws_acc + sl * G * D + idx);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) mv[u] = i0 + u < n ? mv[u] : kNegInf;
@@ -503,19 +507,31 @@ __device__ inline void fold_slots(const DecodeArgs& a, int g, int idx, int D, in
   }
 }
 
-// Merge of n partial slots into the out rows of unit (b, h).  Output elements are
-// spread over the workgroup and over grid z (a unit split across workgroups when
-// units are fewer than CUs).
-template <int DT, typename SlotFn>
+// Merges with VEC = 4 output elements per thread (16-byte partial loads, a quarter
+// of the threads) pay when units are many; with few, long units the merge needs
+// the parallelism of one element per thread.
+constexpr int kMergeVec4Units = 1024;
+
+// Merge of n partial slots into the out rows of unit (b, h).  Each thread owns VEC
+// consecutive output elements; they are spread over the workgroup and over grid z
+// (a unit split across workgroups when units are fewer than CUs).
+template <int DT, int VEC, typename SlotFn>
 __device__ inline void merge_slots(const DecodeArgs& a, int b, int h, int n, int D, SlotFn slot) {
   using E = typename Traits<DT>::E;
   const int G = a.G;
   const int Hq = a.Hkv * G;
-  for (int idx = threadIdx.x + blockIdx.z * blockDim.x; idx < G * D; idx += blockDim.x * gridDim.z) {
-    float M = kNegInf, L = 0.f, O = 0.f;
-    fold_slots(a, idx / D, idx, D, n, slot, M, L, O);
-    static_cast<E*>(a.out)[((int64_t)b * Hq + h * G) * D + idx] =
-        Traits<DT>::from_float(L > 0.f ? O / L : 0.f);
+  E* out = static_cast<E*>(a.out) + ((int64_t)b * Hq + h * G) * D;
+  for (int idx = VEC * (threadIdx.x + blockIdx.z * blockDim.x); idx < G * D;
+       idx += VEC * blockDim.x * gridDim.z) {
+    float M = kNegInf, L = 0.f;
+    typename std::conditional<VEC == 4, f32x4, float>::type O = {};
+    fold_slots<VEC>(a, idx / D, idx, D, n, slot, M, L, O);
+    if constexpr (VEC == 4) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) out[idx + r] = Traits<DT>::from_float(L > 0.f ? O[r] / L : 0.f);
+    } else {
+      out[idx] = Traits<DT>::from_float(L > 0.f ? O / L : 0.f);
+    }
   }
 }
 
@@ -527,7 +543,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a, int D) 
   const int n_parts = num_partitions(w, a);
   if (n_parts <= 1) return;
   const int64_t base = ((int64_t)b * a.Hkv + h) * a.n_parts_max;
-  merge_slots<DT>(a, b, h, n_parts, D, [&](int i) { return base + i; });
+  merge_slots<DT, 1>(a, b, h, n_parts, D, [&](int i) { return base + i; });
 }
 
 // ---------------------------------------------------------------------------
@@ -743,7 +759,7 @@ __global__ __launch_bounds__(kStreamThreads, Ops::kWGsPerCU) void decode_stream_
 // Stream walk's merge: grid (kv head, sequence, column split), 256 or 64 threads.  Writes zeros for
 // an empty unit, skips a unit one wave finished (written directly), and folds
 // the fragments of a split unit (slots k + u, k = first..last wave).
-template <int DT>
+template <int DT, int VEC>
 __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, int D) {
   using E = typename Traits<DT>::E;
   const int h = blockIdx.x, b = blockIdx.y;
@@ -764,7 +780,7 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, 
   const int64_t k0 = split.owner(first_tile), k1 = split.owner(first_tile + n - 1);
   if (k0 == k1) return;
   const int64_t base = k0 + (int64_t)b * Hkv + h;
-  merge_slots<DT>(a, b, h, (int)(k1 - k0 + 1), D, [&](int i) { return base + i; });
+  merge_slots<DT, VEC>(a, b, h, (int)(k1 - k0 + 1), D, [&](int i) { return base + i; });
 }
 
 // Fused append's merge: grid (kv head, sequence, column split), 256 or 64 threads.  Scores the new
@@ -778,7 +794,7 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, 
 // factor sf = row_sf(max |x|) from a wave reduction over the row, codes e4m3(x * sf)),
 // attended as their dequantized values code / sf -- what an append followed by the
 // walk would read -- and their codes and factors are stored into the slot.
-template <int DT, int D, bool kFp8>
+template <int DT, int D, bool kFp8, int VEC>
 __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
   using Tr = Traits<DT>;
   using E = typename Tr::E;
@@ -827,17 +843,15 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
     nf = split.owner(first_tile + n - 1) - k0 + 1;
   }
   const int64_t base = k0 + (int64_t)b * Hkv + h;
-  // The new K row, lane-strided (dims lane + 64j); FP8: its and the V row's factors
-  // (every lane ends with the row's max) and the dequantized K values.
-  float kv[DL];
-#pragma unroll
-  for (int j = 0; j < DL; ++j) kv[j] = (float)kn[lane + 64 * j];
+  // FP8: the new rows' factors, as ivakv_append_fp8 computes them (max |x| over the
+  // row; every wave reduces the whole row, lanes strided over the dims), so every
+  // thread holds them for the element loop and the append.
   float sfk = 1.f, sfv = 1.f;
   if constexpr (kFp8) {
     float ka = 0.f, va = 0.f;
 #pragma unroll
     for (int j = 0; j < DL; ++j) {
-      ka = fmaxf(ka, fabsf(kv[j]));
+      ka = fmaxf(ka, fabsf((float)kn[lane + 64 * j]));
       va = fmaxf(va, fabsf((float)vn[lane + 64 * j]));
     }
 #pragma unroll
@@ -847,40 +861,57 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
     }
     sfk = row_sf(ka);
     sfv = row_sf(va);
-#pragma unroll
-    for (int j = 0; j < DL; ++j) kv[j] = e4m3_decode(e4m3_encode(kv[j] * sfk)) / sfk;
   }
-  // D is a multiple of 64, so the 64 outputs of a wave share one query head g,
-  // and the wave scores the new token for g with a lane-strided dot product.
-  // Its operands (and the value element) are loaded before the partials, so
-  // every load of the element is in flight at once; then the partials are
-  // folded, then the new token.
-  for (int idx = idx0; idx < G * D; idx += stride) {
-    const int g = idx / D;
-    float qv[DL];
+  // Each thread owns VEC consecutive outputs idx .. of one query head g (D is a
+  // multiple of 64).  The new token's dot product q_g . k_new: with VEC == 1 the 64
+  // outputs of a wave share g and the wave sums lane-strided products (dims lane +
+  // 64j); with VEC == 4 each lane sums its own four dims and the D/4 lanes of the
+  // head reduce.  The operands (and the value elements) are loaded before the
+  // partials, so every load of the thread is in flight at once; then the partials
+  // are folded, then the new token.
+  constexpr int NQ = VEC == 4 ? 4 : D / 64;  // dot-product terms per lane
+  constexpr int kDotLanes = VEC == 4 ? D / 4 : 64;
+  for (int idx = VEC * idx0; idx < G * D; idx += VEC * stride) {
+    const int g = idx / D, col = idx - g * D;
+    float qv[NQ], kv[NQ], vv[VEC];
 #pragma unroll
-    for (int j = 0; j < DL; ++j) qv[j] = (float)qb[g * D + lane + 64 * j];
-    float vv = (float)vn[idx - g * D];
-    if constexpr (kFp8) vv = e4m3_decode(e4m3_encode(vv * sfv)) / sfv;
-    float M = kNegInf, L_sum = 0.f, O = 0.f;
-    fold_slots(a, g, idx, D, (int)nf, [&](int i) { return base + i; }, M, L_sum, O);
+    for (int j = 0; j < NQ; ++j) {
+      const int d = VEC == 4 ? col + j : lane + 64 * j;
+      qv[j] = (float)qb[g * D + d];
+      kv[j] = (float)kn[d];
+    }
+#pragma unroll
+    for (int r = 0; r < VEC; ++r) vv[r] = (float)vn[col + r];
+    if constexpr (kFp8) {
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) kv[j] = e4m3_decode(e4m3_encode(kv[j] * sfk)) / sfk;
+#pragma unroll
+      for (int r = 0; r < VEC; ++r) vv[r] = e4m3_decode(e4m3_encode(vv[r] * sfv)) / sfv;
+    }
+    float M = kNegInf, L_sum = 0.f;
+    typename std::conditional<VEC == 4, f32x4, float>::type O = {};
+    fold_slots<VEC>(a, g, idx, D, (int)nf, [&](int i) { return base + i; }, M, L_sum, O);
     float dot = 0.f;
 #pragma unroll
-    for (int j = 0; j < DL; ++j) dot += qv[j] * kv[j];
+    for (int j = 0; j < NQ; ++j) dot += qv[j] * kv[j];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o);
+    for (int o = 1; o < kDotLanes; o <<= 1) dot += __shfl_xor(dot, o);
     // Selects, not a branch: the page id's load is then waited for only here,
     // after the partials' loads were issued.
     const float sc = dot * a.scale_log2;
     const float mn = fmaxf(M, sc);
     const float f = new_ok ? exp2_fast(M - mn) : 1.f, w = new_ok ? exp2_fast(sc - mn) : 0.f;
     L_sum = L_sum * f + w;
-    O = O * f + vv * w;
-    out[idx] = Tr::from_float(L_sum > 0.f ? O / L_sum : 0.f);
+#pragma unroll
+    for (int r = 0; r < VEC; ++r) {
+      float o;
+      if constexpr (VEC == 4) o = O[r];
+      else o = O;
+      out[idx + r] = Tr::from_float(L_sum > 0.f ? (o * f + vv[r] * w) / L_sum : 0.f);
+    }
   }
 
-  // Append: the new rows go to the slot of position L-1.  (Threads d < D ran the
-  // element loop's wave, so their sfk / sfv are the row's.)
+  // Append: the new rows go to the slot of position L-1.
   if (new_ok && blockIdx.z == 0) {
     if constexpr (kFp8) {
       const int64_t tile = page * Hkv + h;
@@ -991,23 +1022,33 @@ void launch_stream(Stage stage, int D, dim3 grid, size_t smem, hipStream_t strea
       default: decode_stream_kernel<WalkOps<DT, kFp8, 256>><<<grid, kStreamThreads, smem, stream>>>(a, a.bt, a.ctx); break;
     }
   }
-  // Merge grid: (kv head, sequence, column split) with one output element per
-  // thread, so every partial load of a unit is in flight at once; 64-thread
+  // Merge grid: (kv head, sequence, column split) with one or four output elements
+  // per thread, so every partial load of a unit is in flight at once; 64-thread
   // workgroups when units are fewer than CUs, so few, long sequences still merge
   // on many CUs.
   const int units = a.Hkv * a.batch;
+  const bool vec4 = units >= kMergeVec4Units;
   const int threads = units >= 256 ? 256 : 64;
-  const int zsplit = cdiv(a.G * D, threads);
+  const int zsplit = cdiv(vec4 ? a.G * D / 4 : a.G * D, threads);
   const dim3 mgrid((unsigned)a.Hkv, (unsigned)a.batch, (unsigned)zsplit);
   if (stage == kFused) {
-    switch (D) {
-      case 64: decode_fused_merge_kernel<DT, 64, kFp8><<<mgrid, threads, 0, stream>>>(a); break;
-      case 128: decode_fused_merge_kernel<DT, 128, kFp8><<<mgrid, threads, 0, stream>>>(a); break;
-      default: decode_fused_merge_kernel<DT, 256, kFp8><<<mgrid, threads, 0, stream>>>(a); break;
+    if (vec4) {
+      switch (D) {
+        case 64: decode_fused_merge_kernel<DT, 64, kFp8, 4><<<mgrid, threads, 0, stream>>>(a); break;
+        case 128: decode_fused_merge_kernel<DT, 128, kFp8, 4><<<mgrid, threads, 0, stream>>>(a); break;
+        default: decode_fused_merge_kernel<DT, 256, kFp8, 4><<<mgrid, threads, 0, stream>>>(a); break;
+      }
+    } else {
+      switch (D) {
+        case 64: decode_fused_merge_kernel<DT, 64, kFp8, 1><<<mgrid, threads, 0, stream>>>(a); break;
+        case 128: decode_fused_merge_kernel<DT, 128, kFp8, 1><<<mgrid, threads, 0, stream>>>(a); break;
+        default: decode_fused_merge_kernel<DT, 256, kFp8, 1><<<mgrid, threads, 0, stream>>>(a); break;
+      }
     }
+  } else if (stage != kPartial) {
+    if (vec4) decode_stream_merge_kernel<DT, 4><<<mgrid, threads, 0, stream>>>(a, D);
+    else decode_stream_merge_kernel<DT, 1><<<mgrid, threads, 0, stream>>>(a, D);
   }
-  else if (stage != kPartial)
-    decode_stream_merge_kernel<DT><<<mgrid, threads, 0, stream>>>(a, D);
 }
 
 // Workgroups of the stream walk on the current device: what its CUs hold at

@@ -370,3 +370,36 @@ def test_fused_append_attention(iva, dev, dtype, window, n_sink):
     unfused = iva.paged_decode_attention(base["q"].to(dev), kp_a, vp_a, lay.block_tables.to(dev),
                                          lay.context_lens.to(dev), window=window, n_sink=n_sink)
     assert_close(unfused, ref, dtype, what="append + decode")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_many_units_merges(iva, dev, dtype, d):
+    """Batches of >= 1024 (sequence, kv head) units take the merges with four output
+    elements per thread (the fused op's new-token dot product then sums over the D/4
+    lanes of a head): 160 short ragged sequences x 8 kv heads.  Fused op: pools
+    bit-identical to append + decode; both outputs within the dtype's tolerance of the
+    fp64 oracle."""
+    gen = torch.Generator().manual_seed(11)
+    lengths = [1, 0, 17, 16, 300, 2] + torch.randint(0, 80, (154,), generator=gen).tolist()
+    hkv, g = 8, 4
+    base = iva.workloads.decode_batch(lengths, hkv * g, hkv, d, dtype, seed=60 + d,
+                                      scale=d ** -0.5, extra_pages=4)
+    lay = base["layout"]
+    bt = lay.block_tables
+    k_new = (torch.randn(len(lengths), hkv, d, generator=gen) * d ** -0.5).to(dtype)
+    v_new = (torch.randn(len(lengths), hkv, d, generator=gen) * d ** -0.5).to(dtype)
+    kp_a, vp_a = base["k_pool"].clone().to(dev), base["v_pool"].clone().to(dev)
+    slots = torch.tensor([int(bt[b, (n - 1) // 16]) * 16 + (n - 1) % 16 if n > 0 else -1
+                          for b, n in enumerate(lengths)], dtype=torch.int32)
+    iva.kv_append(k_new.to(dev), v_new.to(dev), kp_a, vp_a, slots.to(dev))
+    kp_f, vp_f = base["k_pool"].clone().to(dev), base["v_pool"].clone().to(dev)
+    out = iva.paged_decode_append_attention(base["q"].to(dev), k_new.to(dev), v_new.to(dev), kp_f,
+                                            vp_f, bt.to(dev), lay.context_lens.to(dev))
+    assert torch.equal(kp_a.view(torch.int16), kp_f.view(torch.int16))
+    assert torch.equal(vp_a.view(torch.int16), vp_f.view(torch.int16))
+    ref = oracle_out(dict(base, k_pool=kp_a.cpu(), v_pool=vp_a.cpu()))
+    assert_close(out, ref, dtype, what=f"fused many units d{d}")
+    unfused = iva.paged_decode_attention(base["q"].to(dev), kp_a, vp_a, bt.to(dev),
+                                         lay.context_lens.to(dev))
+    assert_close(unfused, ref, dtype, what=f"stream merge many units d{d}")
