@@ -141,3 +141,39 @@ def test_pool_shapes(iva):
     assert iva.pool_shapes(10, 8, 64, 16, torch.float32) == ((10, 8, 16, 16, 4), (10, 8, 64, 16))
     with pytest.raises(ValueError):
         iva.pool_shapes(1, 1, 12, 16, torch.bfloat16)
+
+
+def test_fp8_entry_argument_checks(iva):
+    """Host-side validation of the FP8 prefill and fused decode entry points (nothing is
+    launched: every call fails before a kernel would start)."""
+    a = iva._abi
+
+    def prefill8(**over):
+        args = dict(q=FAKE, k=FAKE, v=FAKE, ks=FAKE, vs=FAKE, bt=FAKE, ctx=FAKE, qs=FAKE,
+                    out=FAKE, batch=2, hq=8, hkv=2, d=128, bs=16, max_blocks=8,
+                    num_pages=16, max_q=4, scale=0.088, window=0, n_sink=0, dtype=a.F16,
+                    stream=None)
+        args.update(over)
+        return call(iva, "ivakv_prefill_attn_fp8", *args.values())
+
+    assert prefill8(dtype=a.F32) == a.E_DTYPE
+    assert "fp16 or bf16" in a.last_error()
+    assert prefill8(ks=None) == a.E_ARG
+    assert prefill8(vs=FAKE + 4) == a.E_ARG       # factors must be 16-byte aligned
+    assert prefill8(d=96) == a.E_SHAPE
+    assert prefill8(hq=9) == a.E_SHAPE
+    assert prefill8(max_q=0) == a.OK              # nothing to do
+
+    def fused8(**over):
+        args = dict(q=FAKE, kn=FAKE, vn=FAKE, k=FAKE, v=FAKE, ks=FAKE, vs=FAKE, bt=FAKE,
+                    ctx=FAKE, out=FAKE, ws=None, ws_bytes=0, batch=2, hq=8, hkv=2, d=128,
+                    bs=16, max_blocks=8, num_pages=16, scale=0.088, window=0, n_sink=0,
+                    dtype=a.F16, stream=None)
+        args.update(over)
+        return call(iva, "ivakv_decode_append_attn_fp8", *args.values())
+
+    assert fused8(dtype=a.F32) == a.E_DTYPE
+    assert fused8(ks=None) == a.E_ARG
+    assert fused8(kn=None) == a.E_ARG
+    assert fused8() == a.E_WORKSPACE              # the stream walk needs a workspace
+    assert fused8(bs=8) == a.E_SHAPE
