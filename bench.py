@@ -21,7 +21,10 @@ bytes + attention bytes) / step time.  `roofline` is for the dominant kernel
 duration measured here with HIP events over a graph of back-to-back launches on
 the launch stream.  `cpu_baseline` times the CPU restatement of the reference's
 torch path (contiguous cache + torch.cat append + AttentionTorch math, fp32) on
-this host's cores.
+this host's cores.  `target_4k` repeats the walk, attention and step measurements
+at the north-star target's own shape (the same batch with every sequence at
+context 4096); --no-target-4k skips it, and runs with --eager or
+--copy-calibration (the counter runs) never make it.
 
 Profiling helpers (no timing line):
   --copy-calibration   also launches a plain 256 MiB device copy 10 times after
@@ -57,6 +60,17 @@ WALK_KERNEL = "decode_stream_kernel"
 COPY_BYTES = 256 << 20
 
 
+def read_traffic(context: str):
+    """HBM bytes per walk launch from the committed counter summary, or None."""
+    path = traffic_path(context)
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -80,6 +94,9 @@ def parse_args():
                    help="c2 (default): context lengths U[512, 4096] seed 0 (the contract line); "
                         "an integer N: every sequence of the batch at context N (e.g. 4096, "
                         "the north-star target's 4k context)")
+    p.add_argument("--no-target-4k", dest="target_4k", action="store_false",
+                   help="skip the second measurement at the target shape (B 32, every "
+                        "sequence at context 4096) that the default line carries")
     p.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "prefill", "c2fp8"), default="c2",
                    help="c2 (default): the contract line; c3 dense-decoder tokens/s, c4 "
                         "long-context window+sinks decode, c5 ragged churn, prefill: 512-token "
@@ -515,36 +532,12 @@ def bench_prefill(args, iva, torch, dev):
             "fp8_pages_tflops": round(flops / t8 / 1e12, 1)}
 
 
-def main():
-    args = parse_args()
-    if args.summarize_pmc:
-        summarize_pmc(*args.summarize_pmc, context=args.context)
-        return
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                          "(sharding the path over several GPUs is not built)"}))
-        sys.exit(2)
-
-    import torch
-    import __graft_entry__
-
-    iva = __graft_entry__.load_package()
-    iva._abi.lib()
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
+def measure_decode(args, iva, torch, dev, lengths):
+    """Times the C2-shaped decode step (fused append + attention), the walk and the
+    attention over ``lengths`` on rotated pools: HIP graphs of back-to-back launches on
+    one stream.  Returns step ms, walk and attention µs per launch, and the pool bytes."""
     wl = iva.workloads
-    if args.workload != "c2":
-        fn = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "prefill": bench_prefill,
-              "c2fp8": bench_c2fp8}[args.workload]
-        print(json.dumps(fn(args, iva, torch, dev)), flush=True)
-        return
-
     hq, hkv, d, dtype, esize = 32, 8, 128, torch.float16, 2
-    lengths = wl.c2_lengths(seed=0)
-    context_desc = "U[512,4096] seed 0"
-    if args.context != "c2":
-        lengths = [int(args.context)] * len(lengths)
-        context_desc = f"{int(args.context)} (every sequence)"
     batch = len(lengths)
     sc = 1 / math.sqrt(d)
     sets = []
@@ -648,24 +641,72 @@ def main():
         walk_us = time_launches(walk_graph, walk)
         attn_us = time_launches(attn_graph, attention)
 
-        if args.copy_calibration:
-            src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(7)
-            dst = torch.empty_like(src)
-            for _ in range(10):
-                dst.copy_(src)
-            torch.cuda.synchronize(dev)
+    return {"step_ms": step_ms, "walk_us": walk_us, "attn_us": attn_us,
+            "pool_bytes": pool_bytes, "batch": batch}
+
+
+def main():
+    args = parse_args()
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc, context=args.context)
+        return
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                          "(sharding the path over several GPUs is not built)"}))
+        sys.exit(2)
+
+    import torch
+    import __graft_entry__
+
+    iva = __graft_entry__.load_package()
+    iva._abi.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = iva.workloads
+    if args.workload != "c2":
+        fn = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "prefill": bench_prefill,
+              "c2fp8": bench_c2fp8}[args.workload]
+        print(json.dumps(fn(args, iva, torch, dev)), flush=True)
+        return
+
+    hq, hkv, d, esize = 32, 8, 128, 2
+    lengths = wl.c2_lengths(seed=0)
+    context_desc = "U[512,4096] seed 0"
+    if args.context != "c2":
+        lengths = [int(args.context)] * len(lengths)
+        context_desc = f"{int(args.context)} (every sequence)"
+    m = measure_decode(args, iva, torch, dev, lengths)
+    step_ms, walk_us, attn_us, pool_bytes, batch = (
+        m["step_ms"], m["walk_us"], m["attn_us"], m["pool_bytes"], m["batch"])
+    target = None
+    if (args.context == "c2" and args.target_4k and not args.partition_pages
+            and not args.eager and not args.copy_calibration):
+        # the north-star target's own shape: every sequence at context 4096, on pools
+        # allocated afresh (the C2 pools' cached blocks returned to the device first)
+        torch.cuda.empty_cache()
+        t_len = [4096] * batch
+        mt = measure_decode(args, iva, torch, dev, t_len)
+        t_append, t_attn = algorithmic_bytes(t_len, 32, 8, 128, 2)
+        t_ach = t_attn / (mt["walk_us"] * 1e-6) / 1e9
+        target = {"context": 4096, "batch": batch, "kernel_us": round(mt["walk_us"], 3),
+                  "achieved": round(t_ach, 1), "frac": round(t_ach / HBM_PEAK_GBS, 4),
+                  "algorithmic_bytes": t_attn, "attention_us": round(mt["attn_us"], 3),
+                  "step_us": round(mt["step_ms"] * 1e3, 3),
+                  "step_gbs": round((t_append + t_attn) / (mt["step_ms"] * 1e-3) / 1e9, 1),
+                  "traffic": read_traffic("4096")}
+    if args.copy_calibration:
+        src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(7)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
 
     append_b, attn_b = algorithmic_bytes(lengths, hq, hkv, d, esize)
     step_s = step_ms * 1e-3
     value = (append_b + attn_b) / step_s / 1e9
     achieved = attn_b / (walk_us * 1e-6) / 1e9
 
-    traffic = None
-    if traffic_path(args.context).exists():
-        try:
-            traffic = json.loads(traffic_path(args.context).read_text()).get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+    traffic = read_traffic(args.context)
 
     cpu = None
     if args.cpu_reps > 0:
@@ -711,6 +752,7 @@ def main():
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "attention_us": round(attn_us, 3),
         "step_bytes": {"append": append_b, "attention": attn_b},
+        "target_4k": target,
     }
     print(json.dumps(line), flush=True)
 

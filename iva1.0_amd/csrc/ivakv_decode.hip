@@ -53,6 +53,16 @@ constexpr int kStreamThreads = 64 * kStreamWaves;
 constexpr int kMaxStreamWaves = 4096;
 constexpr int kMinTilesPerWave = 4;
 constexpr int kMaxStreamBatch = 8192;
+// Stream walk workgroups per CU from the bytes one ring slot holds (K + V of one
+// tile).  One 4-wave workgroup per CU keeps 2 x 8 KiB slots per wave in flight at
+// D 128 on 16-bit pages, enough to hold HBM busy; 4 KiB slots (D 64 at 16 bits,
+// D 128 on FP8 pages) need two workgroups per CU for as many bytes in flight.
+#ifndef IVAKV_WG2_SLOT_BYTES
+#define IVAKV_WG2_SLOT_BYTES 4096
+#endif
+constexpr int walk_wgs_per_cu(int64_t slot_bytes) {
+  return slot_bytes <= IVAKV_WG2_SLOT_BYTES ? 2 : 1;
+}
 
 struct DecodeArgs {
   const void* q;
@@ -165,10 +175,10 @@ struct TileOps {
   using E = typename Tr::E;
   using VChunk = typename Tr::VChunk;
   static constexpr int kD = D;
-  // Stream walk occupancy: one 4-wave workgroup per CU (one wave per SIMD, up to
-  // 512 registers).  1024 waves keep HBM as busy as 2048 (C2: 54.9 against
-  // 55.7 µs) with fewer partials; deeper rings measured slower.
-  static constexpr int kWGsPerCU = 1;
+  // Stream walk occupancy.  At D 128 (8 KiB slots) one workgroup per CU: 1024 waves
+  // keep HBM as busy as 2048 (C2: 54.9 against 55.7 µs) with fewer partials; deeper
+  // rings measured slower.
+  static constexpr int kWGsPerCU = walk_wgs_per_cu(2 * (int64_t)D * kBS * sizeof(E));
   static constexpr int X = 16 / (int)sizeof(E);  // elements per 16-byte K chunk
   static constexpr int KLD = D / X / 4;          // K loads per lane per tile
   static constexpr int NB = D / 16;              // 16-dim blocks (PV MFMAs per tile)
@@ -250,9 +260,8 @@ struct TileOps8 {
   using E = typename Tr::E;
   using VChunk = typename Tr::VChunk;
   static constexpr int kD = D;
-  // Two workgroups per CU: the FP8 walk, with half the bytes per tile, measured
-  // 41.6 µs on C2 against 44.6 µs at one.
-  static constexpr int kWGsPerCU = 2;
+  // At D 128 (4 KiB slots) two workgroups per CU: 41.6 µs on C2 against 44.6 µs at one.
+  static constexpr int kWGsPerCU = walk_wgs_per_cu(2 * (int64_t)D * kBS);
   static constexpr int KL = D / 64;   // 16-byte K loads (16 dims) per lane per tile
   static constexpr int NB = D / 16;
   static constexpr int64_t kTileBytes = (int64_t)D * kBS;
@@ -1130,8 +1139,8 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
   a.v_scale = v_scale;
 
   if (plan.stream) {
-    const int wgs = stream_workgroups(fp8 ? TileOps8<IVAKV_F16, 128>::kWGsPerCU
-                                          : TileOps<IVAKV_F16, 128>::kWGsPerCU);
+    const int esize = fp8 ? 1 : dtype_size(dtype);
+    const int wgs = stream_workgroups(walk_wgs_per_cu(2 * (int64_t)head_dim * kBS * esize));
     a.n_waves = wgs * kStreamWaves;
     const size_t smem = sizeof(int32_t) * ((size_t)batch + 1 + kStreamThreads);
     const dim3 grid((unsigned)wgs);
