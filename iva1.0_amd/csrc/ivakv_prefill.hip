@@ -184,17 +184,37 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   u32x4 stK[S::kStages][kKPer], stV[S::kStages][kVPer];  // vector types: kept in registers
-  auto page_of = [&](int v, int& lp, bool& ok) -> int64_t {
-    const int vc = v < n_eff ? v : n_eff - 1;
-    lp = logical_page(w, vc);
-    const int64_t pp = bt[(int64_t)b * a.max_blocks + lp];
-    ok = v < n_eff && pp >= 0 && pp < a.num_pages;
-    return (pp >= 0 && pp < a.num_pages) ? pp : 0;
+  // Page ids.  Lanes fetch the block-table entries of a pair two loads ahead
+  // with vector loads (no scalar-memory wait inside a step: the scalar and LDS
+  // counters are shared), into the slot of the pair's parity; load() moves them
+  // to scalar registers and records each page's validity (id in range, page
+  // inside the walk) in okmask, bits 2 (pair % 16) and + 1, which the pair's
+  // step reads.  Pages past n_eff are the last one (masked later); invalid ids
+  // read page 0.
+  auto lpage = [&](int v) __attribute__((always_inline)) -> int { return logical_page(w, v < n_eff ? v : n_eff - 1); };
+  const int32_t* bt_row = bt + (int64_t)b * a.max_blocks;
+  int ids_a[2], ids_b[2];
+  uint32_t okmask = 0;
+  auto fetch_ids = [&](int pair, int par) __attribute__((always_inline)) {
+    int z = 0;
+    asm volatile("" : "+v"(z));  // a vector-register offset: a vector load
+    ids_a[par] = bt_row[lpage(2 * pair) + z];
+    ids_b[par] = bt_row[lpage(2 * pair + 1) + z];
   };
-  auto load_pair = [&](int pair, int set) {
-    int lp;
-    bool ok;
-    const int64_t pa = page_of(2 * pair, lp, ok), pb = page_of(2 * pair + 1, lp, ok);
+  auto take_ids = [&](int pair, int par, int64_t& pa, int64_t& pb) __attribute__((always_inline)) {
+    const int ia = __builtin_amdgcn_readfirstlane(ids_a[par]);
+    const int ib = __builtin_amdgcn_readfirstlane(ids_b[par]);
+    const bool va = ia >= 0 && ia < a.num_pages, vb = ib >= 0 && ib < a.num_pages;
+    const int sh = 2 * (pair & 15);
+    okmask = (okmask & ~(3u << sh)) | ((uint32_t)(va && 2 * pair < n_eff) << sh) |
+             ((uint32_t)(vb && 2 * pair + 1 < n_eff) << (sh + 1));
+    pa = va ? ia : 0;
+    pb = vb ? ib : 0;
+  };
+  auto pair_ok = [&](int pair) __attribute__((always_inline)) -> uint32_t { return (okmask >> (2 * (pair & 15))) & 3u; };
+  auto load_pair = [&](int pair, int set, int par) __attribute__((always_inline)) {
+    int64_t pa, pb;
+    take_ids(pair, par, pa, pb);
     const E* kpa = static_cast<const E*>(a.k_pool) + (pa * Hkv + h) * kTile;
     const E* kpb = static_cast<const E*>(a.k_pool) + (pb * Hkv + h) * kTile;
     const E* vpa = static_cast<const E*>(a.v_pool) + (pa * Hkv + h) * kTile;
@@ -218,10 +238,43 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
         stV[set][c] = *reinterpret_cast<const u32x4*>(((v & 1) ? vpb : vpa) + off);
       }
     }
+    fetch_ids(pair + 2, par);
   };
-  auto store_pair = [&](int buf, int set) {
+  // V values of keys no row may see (past the context, on an invalid page) are
+  // zeroed as the pair enters LDS, once for the whole workgroup: 0 * NaN would
+  // poison the PV accumulator.  Only a pair that reaches past the context or
+  // holds an invalid page takes this branch.
+  auto pair_needs_vmask = [&](int pair) __attribute__((always_inline)) -> bool {
+    return pair_ok(pair) != 3u || lpage(2 * pair + 1) * kBS + kBS > L;
+  };
+  auto v_keys_ok = [&](int pair, int pg, int g, bool (&vis)[4]) __attribute__((always_inline)) {
+    const bool page_ok = ((pair_ok(pair) >> pg) & 1u) != 0;
+    const int k0 = lpage(2 * pair + pg) * kBS + 4 * g;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) vis[r] = page_ok && k0 + r < L;
+  };
+  auto store_pair = [&](int buf, int set, int pair) __attribute__((always_inline)) {
     u32x4* dk = reinterpret_cast<u32x4*>(lds + buf * (4 * kPageChunks));
     u32x4* dv = dk + 2 * kPageChunks;
+    if (pair_needs_vmask(pair)) {
+#pragma unroll
+      for (int c = 0; c < kVPer; ++c) {
+        const int v = min(tid + S::kThreads * c, 2 * kPageChunks - 1);
+        if constexpr (kGran == 8) {  // granule v%4 of pages A and B
+          bool va[4], vb[4];
+          v_keys_ok(pair, 0, v & 3, va);
+          v_keys_ok(pair, 1, v & 3, vb);
+          Chunk16 ch = __builtin_bit_cast(Chunk16, stV[set][c]);
+          mask_pair16(ch, va, vb);
+          stV[set][c] = __builtin_bit_cast(u32x4, ch);
+        } else {  // granule (v%8)/2 of page v%2
+          bool vis[4];
+          v_keys_ok(pair, v & 1, (v & 7) >> 1, vis);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) stV[set][c][r] = vis[r] ? stV[set][c][r] : 0u;
+        }
+      }
+    }
 #pragma unroll
     for (int c = 0; c < kKPer; ++c)
       if ((2 * kPageChunks) % S::kThreads == 0 || tid + S::kThreads * c < 2 * kPageChunks)
@@ -245,11 +298,11 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   u32x2 st8K[S::kStages][kU8], st8V[S::kStages][kU8];
   float sc8K[S::kStages][kU8];
   f32x4 sc8V[S::kStages][kU8];
-  auto load_pair8 = [&](int pair, int set) {
+  auto load_pair8 = [&](int pair, int set, int par) __attribute__((always_inline)) {
     if constexpr (kFp8) {
-    int lp;
-    bool ok;
-    const int64_t tA = page_of(2 * pair, lp, ok) * Hkv + h, tB = page_of(2 * pair + 1, lp, ok) * Hkv + h;
+    int64_t pa, pb;
+    take_ids(pair, par, pa, pb);
+    const int64_t tA = pa * Hkv + h, tB = pb * Hkv + h;
     const uint8_t* k8 = static_cast<const uint8_t*>(a.k_pool);
     const uint8_t* v8 = static_cast<const uint8_t*>(a.v_pool);
 #pragma unroll
@@ -262,10 +315,11 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
       st8V[set][c] = *reinterpret_cast<const u32x2*>(v8 + t * kTile + 8 * j);
       sc8V[set][c] = *reinterpret_cast<const f32x4*>(a.v_scale + t * kBS + 4 * (((2 * j) / kNB8) & 3));
     }
+    fetch_ids(pair + 2, par);
     }
   };
   // Four codes (one 32-bit word) times four factors, as four values of E.
-  auto dequant4 = [&](uint32_t w, float s0, float s1, float s2, float s3) -> u32x2 {
+  auto dequant4 = [&](uint32_t w, float s0, float s1, float s2, float s3) __attribute__((always_inline)) -> u32x2 {
     if constexpr (kFp8) {
       const f32x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, false);
       const f32x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, true);
@@ -274,7 +328,7 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
       return u32x2{0u, 0u};
     }
   };
-  auto store_pair8 = [&](int buf, int set) {
+  auto store_pair8 = [&](int buf, int set, int pair) __attribute__((always_inline)) {
     if constexpr (kFp8) {
     u32x4* dk = reinterpret_cast<u32x4*>(lds + buf * (4 * kPageChunks));
     u32x2* dv = reinterpret_cast<u32x2*>(dk + 2 * kPageChunks);  // V rows of 8 granules
@@ -294,53 +348,57 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
       const float i0 = __builtin_amdgcn_rcpf(sv[0]), i1 = __builtin_amdgcn_rcpf(sv[1]);
       const float i2 = __builtin_amdgcn_rcpf(sv[2]), i3 = __builtin_amdgcn_rcpf(sv[3]);
       const int w0 = 2 * j, m = w0 % kNB8, g = (w0 / kNB8) & 3, dl = w0 / (4 * kNB8);
+      u32x2 vv[2];
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int d = dl + 16 * (m + e);
-        dv[d * 8 + 2 * g + pg] = dequant4(st8V[set][c][e], i0, i1, i2, i3);
+      for (int e = 0; e < 2; ++e) vv[e] = dequant4(st8V[set][c][e], i0, i1, i2, i3);
+      if (pair_needs_vmask(pair)) {
+        bool vis[4];
+        v_keys_ok(pair, pg, g, vis);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          Chunk8 h = __builtin_bit_cast(Chunk8, vv[e]);
+          mask_rows16(h, vis);
+          vv[e] = __builtin_bit_cast(u32x2, h);
+        }
       }
+#pragma unroll
+      for (int e = 0; e < 2; ++e) dv[(dl + 16 * (m + e)) * 8 + 2 * g + pg] = vv[e];
     }
     }
   };
-  auto load = [&](int pair, int set) {
-    if constexpr (kFp8) load_pair8(pair, set);
-    else load_pair(pair, set);
+  auto load = [&](int pair, int set, int par) __attribute__((always_inline)) {
+    if constexpr (kFp8) load_pair8(pair, set, par);
+    else load_pair(pair, set, par);
   };
-  auto store = [&](int buf, int set) {
-    if constexpr (kFp8) store_pair8(buf, set);
-    else store_pair(buf, set);
+  auto store = [&](int buf, int set, int pair) __attribute__((always_inline)) {
+    if constexpr (kFp8) store_pair8(buf, set, pair);
+    else store_pair(buf, set, pair);
   };
 
-  // Interior pairs (every key inside every row's causal window, all keys inside
-  // the context on valid pages) skip the per-key masks; that needs every row of
-  // the wave to be a real row.
-  const bool rows_all_valid = r_w + S::kRowsWave <= rows && first_pos + r_w / G >= 0;
-  const int wave_p_lo = first_pos + r_w / G;
-
-  // A pair's step is split in two: qk_pair (K from LDS, the QK MFMAs of every row
-  // block) and sm_pv (V from LDS, softmax, PV MFMAs), so the pipelined loop can
-  // issue the next pair's QK before this pair's softmax.
+  // Scores of one pair (pages A, B) for every row block of the wave.
   struct PairS {
     f32x4 sa[NR], sb[NR];
   };
-  // Skip a pair past the walk or entirely after every row of the wave.
-  auto pair_live = [&](int pair, int& lpa, int& lpb, bool& oka, bool& okb) -> bool {
-    page_of(2 * pair, lpa, oka);
-    page_of(2 * pair + 1, lpb, okb);
-    return pair < n_pairs && lpa * kBS <= wave_p_hi;
+  // A pair past the walk or entirely after every row of the wave is skipped.
+  auto pair_live = [&](int pair) __attribute__((always_inline)) -> bool {
+    return pair < n_pairs && lpage(2 * pair) * kBS <= wave_p_hi;
   };
-  auto qk_pair = [&](int buf, int pair, PairS& sc) {
-    int lpa, lpb;
-    bool oka, okb;
-    if (!pair_live(pair, lpa, lpb, oka, okb)) return;
+  auto read_k = [&](int buf, Chunk16 (&ka)[KLD], Chunk16 (&kb)[KLD]) __attribute__((always_inline)) {
     const E* kA = reinterpret_cast<const E*>(lds + buf * (4 * kPageChunks));
     const E* kB = kA + S::kPageElems;
-    Chunk16 ka[KLD], kb[KLD];
 #pragma unroll
     for (int j = 0; j < KLD; ++j) {
       ka[j] = *reinterpret_cast<const Chunk16*>(kA + ((4 * j + lq) * kBS + ln) * X);
       kb[j] = *reinterpret_cast<const Chunk16*>(kB + ((4 * j + lq) * kBS + ln) * X);
     }
+  };
+  using VPair = typename Tr::VPair;
+  auto read_v = [&](int buf, VPair (&vp)[NB]) __attribute__((always_inline)) {
+    const char* vP = reinterpret_cast<const char*>(lds + buf * (4 * kPageChunks) + 2 * kPageChunks);
+#pragma unroll
+    for (int m = 0; m < NB; ++m) vp[m] = Tr::read_vpair(vP + (16 * m + ln) * (8 * kGran) + lq * (2 * kGran));
+  };
+  auto qk_mfma = [&](const Chunk16 (&ka)[KLD], const Chunk16 (&kb)[KLD], PairS& sc) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < NR; ++rb) {
       sc.sa[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -352,95 +410,133 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
       }
     }
   };
-  auto sm_pv = [&](int buf, int pair, const PairS& sc) {
-    int lpa, lpb;
-    bool oka, okb;
-    if (!pair_live(pair, lpa, lpb, oka, okb)) return;
-    const bool interior = rows_all_valid && oka && okb && lpb * kBS + kBS - 1 <= wave_p_lo &&
-                          (a.window <= 0 || lpa * kBS > wave_p_hi - a.window);
-    const char* vP = reinterpret_cast<const char*>(lds + buf * (4 * kPageChunks) + 2 * kPageChunks);
-    VChunk va[NB], vb[NB];
+  auto qk_pair = [&](int buf, PairS& sc) __attribute__((always_inline)) {
+    Chunk16 ka[KLD], kb[KLD];
+    read_k(buf, ka, kb);
+    qk_mfma(ka, kb, sc);
+  };
+  // This lane's 8 scores of row block rb (keys 4lq.. of page A, then of page B).
+  auto lane_scores = [&](const PairS& sc, int rb, float (&sl)[8]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int m = 0; m < NB; ++m) {
-      const VChunk* g = reinterpret_cast<const VChunk*>(vP + (16 * m + ln) * (8 * kGran) + lq * (2 * kGran));
-      va[m] = g[0];
-      vb[m] = g[1];
-    }
-    if (!interior) {
-      // V rows outside the context (tail of the last page, invalid pages) may hold
-      // any bits; zero them (0 * NaN would poison the accumulator).
-      bool vra[4], vrb[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        vra[r] = oka && lpa * kBS + 4 * lq + r < L;
-        vrb[r] = okb && lpb * kBS + 4 * lq + r < L;
-      }
-#pragma unroll
-      for (int m = 0; m < NB; ++m) {
-        Tr::mask_rows(va[m], vra);
-        Tr::mask_rows(vb[m], vrb);
-      }
-    }
-#pragma unroll
-    for (int rb = 0; rb < NR; ++rb) {
-      float sl[8];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        sl[r] = sc.sa[rb][r];
-        sl[4 + r] = sc.sb[rb][r];
-      }
-      if (!interior) {
-        const int qp = qpos[rb];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int ka_ = lpa * kBS + 4 * lq + r;
-          const int kb_ = lpb * kBS + 4 * lq + r;
-          const bool visa = oka && ka_ <= qp && (a.window <= 0 || ka_ > qp - a.window || ka_ < a.n_sink);
-          const bool visb = okb && kb_ <= qp && (a.window <= 0 || kb_ > qp - a.window || kb_ < a.n_sink);
-          sl[r] = visa ? sl[r] : kNegInf;
-          sl[4 + r] = visb ? sl[4 + r] : kNegInf;
-        }
-      }
-      // Lazy rescaling: the reference max m_run of a row (log2 units) only moves
-      // (with a cross-lane max and a rescale of acc and l) when a scaled score
-      // exceeds it by more than kLazyMax; otherwise p = exp2(s*c - m_run) <=
-      // 2^kLazyMax and the final O = acc / l is unchanged.
-      float lmx = sl[0];
-#pragma unroll
-      for (int i = 1; i < 8; ++i) lmx = fmaxf(lmx, sl[i]);
-      lmx *= c_log2;
-      if (__builtin_amdgcn_ballot_w64(lmx > m_run[rb] + kLazyMax) != 0) {
-        float mx = fmaxf(lmx, __shfl_xor(lmx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run[rb], mx);
-        const float alpha = m_new == kNegInf ? 1.f : exp2_fast(m_run[rb] - m_new);
-        l_run[rb] *= alpha;
-#pragma unroll
-        for (int m = 0; m < NB; ++m) acc[rb][m] *= alpha;
-        m_run[rb] = m_new;
-      }
-      const float m_use = m_run[rb] == kNegInf ? 0.f : m_run[rb];
-      float pa[4], pb[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pa[r] = exp2_fast(__builtin_fmaf(sl[r], c_log2, -m_use));
-        pb[r] = exp2_fast(__builtin_fmaf(sl[4 + r], c_log2, -m_use));
-      }
-      l_run[rb] += ((pa[0] + pa[1]) + (pa[2] + pa[3])) + ((pb[0] + pb[1]) + (pb[2] + pb[3]));
-      const typename Tr::P8 p8 = Tr::pack_p8(pa, pb);
-#pragma unroll
-      for (int m = 0; m < NB; ++m) acc[rb][m] = Tr::pv32(va[m], vb[m], p8, acc[rb][m]);
+    for (int r = 0; r < 4; ++r) {
+      sl[r] = sc.sa[rb][r];
+      sl[4 + r] = sc.sb[rb][r];
     }
   };
-  auto compute = [&](int buf, int pair) {
+  auto scaled_max = [&](const float (&sl)[8]) __attribute__((always_inline)) -> float {
+    float lmx = sl[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) lmx = fmaxf(lmx, sl[i]);
+    return lmx * c_log2;
+  };
+  // Lazy rescaling: the reference max m_run of a row (log2 units) only moves
+  // (with a cross-lane max and a rescale of acc and l) when a scaled score exceeds
+  // it by more than kLazyMax; otherwise p = exp2(s*c - m_run) <= 2^kLazyMax and
+  // the final O = acc / l is unchanged.
+  auto grows = [&](int rb, float lmx) __attribute__((always_inline)) -> bool { return lmx > m_run[rb] + kLazyMax; };
+  auto rescale = [&](int rb, float lmx) __attribute__((always_inline)) {
+    if (__builtin_amdgcn_ballot_w64(grows(rb, lmx)) != 0) {
+      float mx = fmaxf(lmx, __shfl_xor(lmx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run[rb], mx);
+      const float alpha = m_new == kNegInf ? 1.f : exp2_fast(m_run[rb] - m_new);
+      l_run[rb] *= alpha;
+#pragma unroll
+      for (int m = 0; m < NB; ++m) acc[rb][m] *= alpha;
+      m_run[rb] = m_new;
+    }
+  };
+  // p = exp2(s*c - m_run) of the lane's 8 scores, their sum into l, PV.
+  auto exp_pv = [&](int rb, const float (&sl)[8], const VPair (&vp)[NB]) __attribute__((always_inline)) {
+    const float m_use = m_run[rb] == kNegInf ? 0.f : m_run[rb];
+    float pa[4], pb[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pa[r] = exp2_fast(__builtin_fmaf(sl[r], c_log2, -m_use));
+      pb[r] = exp2_fast(__builtin_fmaf(sl[4 + r], c_log2, -m_use));
+    }
+    l_run[rb] += ((pa[0] + pa[1]) + (pa[2] + pa[3])) + ((pb[0] + pb[1]) + (pb[2] + pb[3]));
+    const typename Tr::P8 p8 = Tr::pack_p8(pa, pb);
+#pragma unroll
+    for (int m = 0; m < NB; ++m) acc[rb][m] = Tr::pv_pair(vp[m], p8, acc[rb][m]);
+  };
+  // Masks of a pair that is not interior for this wave, applied to its scores in
+  // place: keys a row must not see (after its position, outside its window and
+  // not a sink, past the context, on an invalid page) get score -inf.
+  auto mask_scores = [&](int pair, PairS& sc) __attribute__((always_inline)) {
+    const uint32_t ok = pair_ok(pair);
+    const bool oka = (ok & 1u) != 0, okb = (ok & 2u) != 0;
+    const int ka0 = lpage(2 * pair) * kBS + 4 * lq, kb0 = lpage(2 * pair + 1) * kBS + 4 * lq;
+#pragma unroll
+    for (int rb = 0; rb < NR; ++rb) {
+      const int qp = qpos[rb];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ka_ = ka0 + r, kb_ = kb0 + r;
+        const bool visa = oka && ka_ <= qp && (a.window <= 0 || ka_ > qp - a.window || ka_ < a.n_sink);
+        const bool visb = okb && kb_ <= qp && (a.window <= 0 || kb_ > qp - a.window || kb_ < a.n_sink);
+        sc.sa[rb][r] = visa ? sc.sa[rb][r] : kNegInf;
+        sc.sb[rb][r] = visb ? sc.sb[rb][r] : kNegInf;
+      }
+    }
+  };
+  // A pair is interior for this wave when every key is visible to every row of
+  // the wave: both pages valid and inside the walk, every key at or before the
+  // wave's first row position and inside the window of its last row.  (Rows past
+  // the chunk's end read row 0's query, so their scores stay finite; they are
+  // never stored.)
+  const int wave_pos_lo = first_pos + r_w / G;  // may be negative: then no pair is
+  auto interior = [&](int pair) __attribute__((always_inline)) -> bool {
+    return wave_pos_lo >= 0 && pair_ok(pair) == 3u &&
+           lpage(2 * pair + 1) * kBS + kBS - 1 <= wave_pos_lo &&
+           (a.window <= 0 || lpage(2 * pair) * kBS > wave_p_hi - a.window);
+  };
+  // Softmax and PV of a pair, with the next pair's QK (with_next): one test for
+  // any row max growing (rare), then one block with no branch: the next pair's K
+  // reads and QK MFMAs, this pair's V reads, exponentials and PV MFMAs.
+  auto softmax_pv = [&](auto with_next, int bn, PairS& sn, int bc, const PairS& sc) __attribute__((always_inline)) {
+    constexpr bool kNext = decltype(with_next)::value;
+    float sl[NR][8], lmx[NR];
+    bool any = false;
+#pragma unroll
+    for (int rb = 0; rb < NR; ++rb) {
+      lane_scores(sc, rb, sl[rb]);
+      lmx[rb] = scaled_max(sl[rb]);
+      any = any || grows(rb, lmx[rb]);
+    }
+    if (__builtin_amdgcn_ballot_w64(any) != 0) {
+#pragma unroll
+      for (int rb = 0; rb < NR; ++rb) rescale(rb, lmx[rb]);
+    }
+    if constexpr (kNext) qk_pair(bn, sn);
+    VPair vp[NB];
+    read_v(bc, vp);
+#pragma unroll
+    for (int rb = 0; rb < NR; ++rb) exp_pv(rb, sl[rb], vp);
+  };
+  // One step of the pipelined loop: this pair's softmax + PV and the next pair's
+  // QK (a pair past this wave's rows is skipped, and so is every later one; the
+  // next pair's QK is harmless when it is not live).
+  auto step = [&](int bn, PairS& sn, int bc, int pc, PairS& sc) __attribute__((always_inline)) {
+    if (!pair_live(pc)) return;
+    if (!interior(pc)) mask_scores(pc, sc);
+    softmax_pv(std::true_type{}, bn, sn, bc, sc);
+  };
+  // One pair, QK then softmax + PV (the unpipelined loop).
+  auto compute = [&](int buf, int pair) __attribute__((always_inline)) {
+    if (!pair_live(pair)) return;
     PairS sc;
-    qk_pair(buf, pair, sc);
-    sm_pv(buf, pair, sc);
+    qk_pair(buf, sc);
+    if (!interior(pair)) mask_scores(pair, sc);
+    softmax_pv(std::false_type{}, buf, sc, buf, sc);
   };
 
   // Ring: pair i is in LDS buffer i % 2 while pair i + 1 travels from HBM / L2
-  // into the staging registers; one barrier per pair.
+  // into the staging registers; one barrier per pair.  Page ids are fetched two
+  // loads ahead, in the slot of the pair's parity.
   if (n_pairs > 0) {
+    fetch_ids(0, 0);
+    fetch_ids(1, 1);
     if constexpr (S::kStages == 2) {
       // Software pipeline over three LDS buffers (pair p in buffer p % 3) and two
       // stage sets (pair p in set p % 2).  Step i stores pair i + 2 and loads pair
@@ -450,34 +546,38 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
       // buffer.  Loads past the last pair repeat the last page (an L2 hit) into
       // buffers nobody reads; being unconditional keeps the stage in registers.
       PairS s0, s1;
-      load(0, 0);
-      load(1, 1);
-      store(0, 0);
-      load(2, 0);
-      store(1, 1);
-      load(3, 1);
+      load(0, 0, 0);
+      load(1, 1, 1);
+      store(0, 0, 0);
+      load(2, 0, 0);
+      store(1, 1, 1);
+      load(3, 1, 1);
       __syncthreads();
-      qk_pair(0, 0, s0);
+      if (pair_live(0)) qk_pair(0, s0);
       for (int i = 0; i < n_pairs; i += 2) {
-        store((i + 2) % 3, 0);
-        load(i + 4, 0);
-        qk_pair((i + 1) % 3, i + 1, s1);
-        sm_pv(i % 3, i, s0);
+        store((i + 2) % 3, 0, i + 2);
+        load(i + 4, 0, 0);
+        step((i + 1) % 3, s1, i % 3, i, s0);
         __syncthreads();
-        store((i + 3) % 3, 1);
-        load(i + 5, 1);
-        qk_pair((i + 2) % 3, i + 2, s0);
-        sm_pv((i + 1) % 3, i + 1, s1);
+        store((i + 3) % 3, 1, i + 3);
+        load(i + 5, 1, 1);
+        step((i + 2) % 3, s0, (i + 1) % 3, i + 1, s1);
         __syncthreads();
       }
     } else {
-      load(0, 0);
-      store(0, 0);
+      // Two pairs per iteration so that the page-id slot (the pair's parity) is
+      // known at compile time; a pair past the walk is skipped.
+      load(0, 0, 0);
+      store(0, 0, 0);
       __syncthreads();
-      for (int i = 0; i < n_pairs; ++i) {
-        load(i + 1, 0);
-        compute(i & 1, i);
-        store((i + 1) & 1, 0);
+      for (int i = 0; i < n_pairs; i += 2) {
+        load(i + 1, 0, 1);
+        compute(0, i);
+        store(1, 0, i + 1);
+        __syncthreads();
+        load(i + 2, 0, 0);
+        compute(1, i + 1);
+        store(0, 0, i + 2);
         __syncthreads();
       }
     }

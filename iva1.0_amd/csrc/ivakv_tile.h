@@ -36,6 +36,15 @@ __device__ inline void mask_rows16(Chunk8& v, const bool vis[4]) {
   v.w[1] &= (vis[2] ? 0x0000FFFFu : 0u) | (vis[3] ? 0xFFFF0000u : 0u);
 }
 
+// The same over a page pair's operand: 4 rows of page A (words 0-1), then 4 of
+// page B (words 2-3).
+__device__ inline void mask_pair16(Chunk16& v, const bool va[4], const bool vb[4]) {
+  v.w[0] &= (va[0] ? 0x0000FFFFu : 0u) | (va[1] ? 0xFFFF0000u : 0u);
+  v.w[1] &= (va[2] ? 0x0000FFFFu : 0u) | (va[3] ? 0xFFFF0000u : 0u);
+  v.w[2] &= (vb[0] ? 0x0000FFFFu : 0u) | (vb[1] ? 0xFFFF0000u : 0u);
+  v.w[3] &= (vb[2] ? 0x0000FFFFu : 0u) | (vb[3] ? 0xFFFF0000u : 0u);
+}
+
 template <int DT>
 struct Traits;
 
@@ -63,6 +72,16 @@ struct Traits<IVAKV_F16> {
   static __device__ inline f32x4 pv32(const VChunk& va, const VChunk& vb, const P8& p, f32x4 acc) {
     const Chunk16 v{{va.w[0], va.w[1], vb.w[0], vb.w[1]}};
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, v), p, acc, 0, 0, 0);
+  }
+  // PV operand of one dim over a page pair: keys 4lq..4lq+3 of page A (words 0-1)
+  // then of page B (words 2-3), as one 16-byte read.
+  using VPair = Chunk16;
+  static __device__ inline VPair read_vpair(const char* g) { return *reinterpret_cast<const Chunk16*>(g); }
+  static __device__ inline f32x4 pv_pair(const VPair& v, const P8& p, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, v), p, acc, 0, 0, 0);
+  }
+  static __device__ inline void mask_pair(VPair& v, const bool va[4], const bool vb[4]) {
+    mask_pair16(v, va, vb);
   }
   static __device__ inline E from_float(float x) { return (E)x; }
   // Two values rounded to E (nearest even), packed low first.
@@ -118,6 +137,16 @@ struct Traits<IVAKV_BF16> {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, p.hi, acc, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, p.lo, acc, 0, 0, 0);
   }
+  using VPair = Chunk16;  // as for fp16: page A's granule, then page B's
+  static __device__ inline VPair read_vpair(const char* g) { return *reinterpret_cast<const Chunk16*>(g); }
+  static __device__ inline f32x4 pv_pair(const VPair& v, const P8& p, f32x4 acc) {
+    const bf16x8 vv = __builtin_bit_cast(bf16x8, v);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, p.hi, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, p.lo, acc, 0, 0, 0);
+  }
+  static __device__ inline void mask_pair(VPair& v, const bool va[4], const bool vb[4]) {
+    mask_pair16(v, va, vb);
+  }
   static __device__ inline E from_float(float x) { return (E)x; }
   static __device__ inline uint32_t pack2(float a, float b) {
     return __builtin_bit_cast(uint32_t, bf16x2{(__bf16)a, (__bf16)b});
@@ -153,10 +182,23 @@ struct Traits<IVAKV_F32> {
   static __device__ inline f32x4 pv32(const VChunk& va, const VChunk& vb, const P8& p, f32x4 acc) {
     return pv(vb, p.b, pv(va, p.a, acc));
   }
+  struct VPair {  // page A's granule (4 keys of one dim), then page B's
+    Chunk16 a, b;
+  };
+  static __device__ inline VPair read_vpair(const char* g) {
+    return VPair{reinterpret_cast<const Chunk16*>(g)[0], reinterpret_cast<const Chunk16*>(g)[1]};
+  }
+  static __device__ inline f32x4 pv_pair(const VPair& v, const P8& p, f32x4 acc) {
+    return pv32(v.a, v.b, p, acc);
+  }
   static __device__ inline E from_float(float x) { return x; }
   static __device__ inline void mask_rows(VChunk& v, const bool vis[4]) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) v.w[r] = vis[r] ? v.w[r] : 0u;
+  }
+  static __device__ inline void mask_pair(VPair& v, const bool va[4], const bool vb[4]) {
+    mask_rows(v.a, va);
+    mask_rows(v.b, vb);
   }
 };
 
