@@ -191,17 +191,17 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   // inside the walk) in okmask, bits 2 (pair % 16) and + 1, which the pair's
   // step reads.  Pages past n_eff are the last one (masked later); invalid ids
   // read page 0.
-  auto lpage = [&](int v) __attribute__((always_inline)) -> int { return logical_page(w, v < n_eff ? v : n_eff - 1); };
+  auto lpage = [&](int v) IVAKV_INLINE -> int { return logical_page(w, v < n_eff ? v : n_eff - 1); };
   const int32_t* bt_row = bt + (int64_t)b * a.max_blocks;
   int ids_a[2], ids_b[2];
   uint32_t okmask = 0;
-  auto fetch_ids = [&](int pair, int par) __attribute__((always_inline)) {
+  auto fetch_ids = [&](int pair, int par) IVAKV_INLINE {
     int z = 0;
     asm volatile("" : "+v"(z));  // a vector-register offset: a vector load
     ids_a[par] = bt_row[lpage(2 * pair) + z];
     ids_b[par] = bt_row[lpage(2 * pair + 1) + z];
   };
-  auto take_ids = [&](int pair, int par, int64_t& pa, int64_t& pb) __attribute__((always_inline)) {
+  auto take_ids = [&](int pair, int par, int64_t& pa, int64_t& pb) IVAKV_INLINE {
     const int ia = __builtin_amdgcn_readfirstlane(ids_a[par]);
     const int ib = __builtin_amdgcn_readfirstlane(ids_b[par]);
     const bool va = ia >= 0 && ia < a.num_pages, vb = ib >= 0 && ib < a.num_pages;
@@ -211,8 +211,8 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
     pa = va ? ia : 0;
     pb = vb ? ib : 0;
   };
-  auto pair_ok = [&](int pair) __attribute__((always_inline)) -> uint32_t { return (okmask >> (2 * (pair & 15))) & 3u; };
-  auto load_pair = [&](int pair, int set, int par) __attribute__((always_inline)) {
+  auto pair_ok = [&](int pair) IVAKV_INLINE -> uint32_t { return (okmask >> (2 * (pair & 15))) & 3u; };
+  auto load_pair = [&](int pair, int set, int par) IVAKV_INLINE {
     int64_t pa, pb;
     take_ids(pair, par, pa, pb);
     const E* kpa = static_cast<const E*>(a.k_pool) + (pa * Hkv + h) * kTile;
@@ -244,16 +244,16 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   // zeroed as the pair enters LDS, once for the whole workgroup: 0 * NaN would
   // poison the PV accumulator.  Only a pair that reaches past the context or
   // holds an invalid page takes this branch.
-  auto pair_needs_vmask = [&](int pair) __attribute__((always_inline)) -> bool {
+  auto pair_needs_vmask = [&](int pair) IVAKV_INLINE -> bool {
     return pair_ok(pair) != 3u || lpage(2 * pair + 1) * kBS + kBS > L;
   };
-  auto v_keys_ok = [&](int pair, int pg, int g, bool (&vis)[4]) __attribute__((always_inline)) {
+  auto v_keys_ok = [&](int pair, int pg, int g, bool (&vis)[4]) IVAKV_INLINE {
     const bool page_ok = ((pair_ok(pair) >> pg) & 1u) != 0;
     const int k0 = lpage(2 * pair + pg) * kBS + 4 * g;
 #pragma unroll
     for (int r = 0; r < 4; ++r) vis[r] = page_ok && k0 + r < L;
   };
-  auto store_pair = [&](int buf, int set, int pair) __attribute__((always_inline)) {
+  auto store_pair = [&](int buf, int set, int pair) IVAKV_INLINE {
     u32x4* dk = reinterpret_cast<u32x4*>(lds + buf * (4 * kPageChunks));
     u32x4* dv = dk + 2 * kPageChunks;
     if (pair_needs_vmask(pair)) {
@@ -298,7 +298,7 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   u32x2 st8K[S::kStages][kU8], st8V[S::kStages][kU8];
   float sc8K[S::kStages][kU8];
   f32x4 sc8V[S::kStages][kU8];
-  auto load_pair8 = [&](int pair, int set, int par) __attribute__((always_inline)) {
+  auto load_pair8 = [&](int pair, int set, int par) IVAKV_INLINE {
     if constexpr (kFp8) {
     int64_t pa, pb;
     take_ids(pair, par, pa, pb);
@@ -319,7 +319,7 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
     }
   };
   // Four codes (one 32-bit word) times four factors, as four values of E.
-  auto dequant4 = [&](uint32_t w, float s0, float s1, float s2, float s3) __attribute__((always_inline)) -> u32x2 {
+  auto dequant4 = [&](uint32_t w, float s0, float s1, float s2, float s3) IVAKV_INLINE -> u32x2 {
     if constexpr (kFp8) {
       const f32x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, false);
       const f32x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, true);
@@ -328,7 +328,7 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
       return u32x2{0u, 0u};
     }
   };
-  auto store_pair8 = [&](int buf, int set, int pair) __attribute__((always_inline)) {
+  auto store_pair8 = [&](int buf, int set, int pair) IVAKV_INLINE {
     if constexpr (kFp8) {
     u32x4* dk = reinterpret_cast<u32x4*>(lds + buf * (4 * kPageChunks));
     u32x2* dv = reinterpret_cast<u32x2*>(dk + 2 * kPageChunks);  // V rows of 8 granules
@@ -366,11 +366,11 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
     }
     }
   };
-  auto load = [&](int pair, int set, int par) __attribute__((always_inline)) {
+  auto load = [&](int pair, int set, int par) IVAKV_INLINE {
     if constexpr (kFp8) load_pair8(pair, set, par);
     else load_pair(pair, set, par);
   };
-  auto store = [&](int buf, int set, int pair) __attribute__((always_inline)) {
+  auto store = [&](int buf, int set, int pair) IVAKV_INLINE {
     if constexpr (kFp8) store_pair8(buf, set, pair);
     else store_pair(buf, set, pair);
   };
@@ -380,10 +380,10 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
     f32x4 sa[NR], sb[NR];
   };
   // A pair past the walk or entirely after every row of the wave is skipped.
-  auto pair_live = [&](int pair) __attribute__((always_inline)) -> bool {
+  auto pair_live = [&](int pair) IVAKV_INLINE -> bool {
     return pair < n_pairs && lpage(2 * pair) * kBS <= wave_p_hi;
   };
-  auto read_k = [&](int buf, Chunk16 (&ka)[KLD], Chunk16 (&kb)[KLD]) __attribute__((always_inline)) {
+  auto read_k = [&](int buf, Chunk16 (&ka)[KLD], Chunk16 (&kb)[KLD]) IVAKV_INLINE {
     const E* kA = reinterpret_cast<const E*>(lds + buf * (4 * kPageChunks));
     const E* kB = kA + S::kPageElems;
 #pragma unroll
@@ -393,12 +393,12 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
     }
   };
   using VPair = typename Tr::VPair;
-  auto read_v = [&](int buf, VPair (&vp)[NB]) __attribute__((always_inline)) {
+  auto read_v = [&](int buf, VPair (&vp)[NB]) IVAKV_INLINE {
     const char* vP = reinterpret_cast<const char*>(lds + buf * (4 * kPageChunks) + 2 * kPageChunks);
 #pragma unroll
     for (int m = 0; m < NB; ++m) vp[m] = Tr::read_vpair(vP + (16 * m + ln) * (8 * kGran) + lq * (2 * kGran));
   };
-  auto qk_mfma = [&](const Chunk16 (&ka)[KLD], const Chunk16 (&kb)[KLD], PairS& sc) __attribute__((always_inline)) {
+  auto qk_mfma = [&](const Chunk16 (&ka)[KLD], const Chunk16 (&kb)[KLD], PairS& sc) IVAKV_INLINE {
 #pragma unroll
     for (int rb = 0; rb < NR; ++rb) {
       sc.sa[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -410,20 +410,20 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
       }
     }
   };
-  auto qk_pair = [&](int buf, PairS& sc) __attribute__((always_inline)) {
+  auto qk_pair = [&](int buf, PairS& sc) IVAKV_INLINE {
     Chunk16 ka[KLD], kb[KLD];
     read_k(buf, ka, kb);
     qk_mfma(ka, kb, sc);
   };
   // This lane's 8 scores of row block rb (keys 4lq.. of page A, then of page B).
-  auto lane_scores = [&](const PairS& sc, int rb, float (&sl)[8]) __attribute__((always_inline)) {
+  auto lane_scores = [&](const PairS& sc, int rb, float (&sl)[8]) IVAKV_INLINE {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       sl[r] = sc.sa[rb][r];
       sl[4 + r] = sc.sb[rb][r];
     }
   };
-  auto scaled_max = [&](const float (&sl)[8]) __attribute__((always_inline)) -> float {
+  auto scaled_max = [&](const float (&sl)[8]) IVAKV_INLINE -> float {
     float lmx = sl[0];
 #pragma unroll
     for (int i = 1; i < 8; ++i) lmx = fmaxf(lmx, sl[i]);
@@ -433,8 +433,8 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   // (with a cross-lane max and a rescale of acc and l) when a scaled score exceeds
   // it by more than kLazyMax; otherwise p = exp2(s*c - m_run) <= 2^kLazyMax and
   // the final O = acc / l is unchanged.
-  auto grows = [&](int rb, float lmx) __attribute__((always_inline)) -> bool { return lmx > m_run[rb] + kLazyMax; };
-  auto rescale = [&](int rb, float lmx) __attribute__((always_inline)) {
+  auto grows = [&](int rb, float lmx) IVAKV_INLINE -> bool { return lmx > m_run[rb] + kLazyMax; };
+  auto rescale = [&](int rb, float lmx) IVAKV_INLINE {
     if (__builtin_amdgcn_ballot_w64(grows(rb, lmx)) != 0) {
       float mx = fmaxf(lmx, __shfl_xor(lmx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -447,7 +447,7 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
     }
   };
   // p = exp2(s*c - m_run) of the lane's 8 scores, their sum into l, PV.
-  auto exp_pv = [&](int rb, const float (&sl)[8], const VPair (&vp)[NB]) __attribute__((always_inline)) {
+  auto exp_pv = [&](int rb, const float (&sl)[8], const VPair (&vp)[NB]) IVAKV_INLINE {
     const float m_use = m_run[rb] == kNegInf ? 0.f : m_run[rb];
     float pa[4], pb[4];
 #pragma unroll
@@ -463,7 +463,7 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   // Masks of a pair that is not interior for this wave, applied to its scores in
   // place: keys a row must not see (after its position, outside its window and
   // not a sink, past the context, on an invalid page) get score -inf.
-  auto mask_scores = [&](int pair, PairS& sc) __attribute__((always_inline)) {
+  auto mask_scores = [&](int pair, PairS& sc) IVAKV_INLINE {
     const uint32_t ok = pair_ok(pair);
     const bool oka = (ok & 1u) != 0, okb = (ok & 2u) != 0;
     const int ka0 = lpage(2 * pair) * kBS + 4 * lq, kb0 = lpage(2 * pair + 1) * kBS + 4 * lq;
@@ -486,7 +486,7 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   // the chunk's end read row 0's query, so their scores stay finite; they are
   // never stored.)
   const int wave_pos_lo = first_pos + r_w / G;  // may be negative: then no pair is
-  auto interior = [&](int pair) __attribute__((always_inline)) -> bool {
+  auto interior = [&](int pair) IVAKV_INLINE -> bool {
     return wave_pos_lo >= 0 && pair_ok(pair) == 3u &&
            lpage(2 * pair + 1) * kBS + kBS - 1 <= wave_pos_lo &&
            (a.window <= 0 || lpage(2 * pair) * kBS > wave_p_hi - a.window);
@@ -494,7 +494,7 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   // Softmax and PV of a pair, with the next pair's QK (with_next): one test for
   // any row max growing (rare), then one block with no branch: the next pair's K
   // reads and QK MFMAs, this pair's V reads, exponentials and PV MFMAs.
-  auto softmax_pv = [&](auto with_next, int bn, PairS& sn, int bc, const PairS& sc) __attribute__((always_inline)) {
+  auto softmax_pv = [&](auto with_next, int bn, PairS& sn, int bc, const PairS& sc) IVAKV_INLINE {
     constexpr bool kNext = decltype(with_next)::value;
     float sl[NR][8], lmx[NR];
     bool any = false;
@@ -517,13 +517,13 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   // One step of the pipelined loop: this pair's softmax + PV and the next pair's
   // QK (a pair past this wave's rows is skipped, and so is every later one; the
   // next pair's QK is harmless when it is not live).
-  auto step = [&](int bn, PairS& sn, int bc, int pc, PairS& sc) __attribute__((always_inline)) {
+  auto step = [&](int bn, PairS& sn, int bc, int pc, PairS& sc) IVAKV_INLINE {
     if (!pair_live(pc)) return;
     if (!interior(pc)) mask_scores(pc, sc);
     softmax_pv(std::true_type{}, bn, sn, bc, sc);
   };
   // One pair, QK then softmax + PV (the unpipelined loop).
-  auto compute = [&](int buf, int pair) __attribute__((always_inline)) {
+  auto compute = [&](int buf, int pair) IVAKV_INLINE {
     if (!pair_live(pair)) return;
     PairS sc;
     qk_pair(buf, sc);

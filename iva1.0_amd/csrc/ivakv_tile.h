@@ -25,6 +25,11 @@ struct alignas(8) Chunk8 {
   uint32_t w[2];
 };
 
+// Forces a kernel's helper lambda inline.  A lambda called from several places
+// may otherwise stay a call, and the register arrays it takes by reference
+// (accumulators, operands) then live in scratch memory.
+#define IVAKV_INLINE __attribute__((always_inline))
+
 constexpr int kBS = 16;       // rows per page == MFMA tile edge
 constexpr float kNegInf = -__builtin_huge_valf();
 
