@@ -78,8 +78,8 @@ struct PrefillShape {
   static constexpr int kRowsWG = kRowsWave * kWaves;
   static constexpr int kPageElems = kBS * D;          // one K or V page tile
   static constexpr int kPairElems = 4 * kPageElems;   // K_A, K_B, V_A, V_B
-  // LDS pair buffers: three for the pipelined loop (two stage sets), else two.
-  static constexpr int kBufs = kStages == 2 ? 3 : 2;
+  // LDS pair buffers: five for the pipelined loop (two stage sets), else two.
+  static constexpr int kBufs = kStages == 2 ? 5 : 2;
   static constexpr size_t kLdsBytes = kBufs * (size_t)kPairElems * kESize;
 };
 
@@ -538,13 +538,16 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
     fetch_ids(0, 0);
     fetch_ids(1, 1);
     if constexpr (S::kStages == 2) {
-      // Software pipeline over three LDS buffers (pair p in buffer p % 3) and two
-      // stage sets (pair p in set p % 2).  Step i stores pair i + 2 and loads pair
-      // i + 4 into the set it frees, issues the QK MFMAs of pair i + 1, then runs
-      // pair i's softmax (on the VALU while those MFMAs execute) and PV.  One
-      // barrier per step: it publishes pair i + 2 and retires pair i - 1's
-      // buffer.  Loads past the last pair repeat the last page (an L2 hit) into
-      // buffers nobody reads; being unconditional keeps the stage in registers.
+      // Software pipeline over five LDS buffers (pair p in buffer p % 5) and two
+      // stage sets (pair p in set p % 2), two steps and one barrier per
+      // iteration.  Step i issues the QK MFMAs of pair i + 1, then runs pair i's
+      // softmax (on the VALU while those MFMAs execute) and PV.  An iteration
+      // (steps i, i + 1) reads pairs i .. i + 2, published by the barrier before
+      // it, and stores pairs i + 3 and i + 4 into the buffers of pairs i - 2 and
+      // i - 1, which that barrier retired; its own barrier publishes them.  Loads
+      // (pairs i + 5, i + 6) refill the stage sets just stored.  Loads past the
+      // last pair repeat the last page (an L2 hit) into buffers nobody reads;
+      // being unconditional keeps the stage in registers.
       PairS s0, s1;
       load(0, 0, 0);
       load(1, 1, 1);
@@ -552,16 +555,17 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
       load(2, 0, 0);
       store(1, 1, 1);
       load(3, 1, 1);
+      store(2, 0, 2);
+      load(4, 0, 0);
       __syncthreads();
       if (pair_live(0)) qk_pair(0, s0);
       for (int i = 0; i < n_pairs; i += 2) {
-        store((i + 2) % 3, 0, i + 2);
-        load(i + 4, 0, 0);
-        step((i + 1) % 3, s1, i % 3, i, s0);
-        __syncthreads();
-        store((i + 3) % 3, 1, i + 3);
+        store((i + 3) % 5, 1, i + 3);
         load(i + 5, 1, 1);
-        step((i + 2) % 3, s0, (i + 1) % 3, i + 1, s1);
+        step((i + 1) % 5, s1, i % 5, i, s0);
+        store((i + 4) % 5, 0, i + 4);
+        load(i + 6, 0, 0);
+        step((i + 2) % 5, s0, (i + 1) % 5, i + 1, s1);
         __syncthreads();
       }
     } else {
