@@ -11,9 +11,10 @@
 // rows spans as few positions as possible (tight causal ranges).  A workgroup
 // of W waves takes 32*W consecutive rows (two 16-row blocks per wave) and walks
 // the pages its rows can see two at a time (32 keys):
-// the pair's K and V tiles move HBM -> registers -> an LDS ring of two buffers
-// once per workgroup, and every wave reads them from LDS in MFMA operand order
-// (the pools' tile layout is kept in LDS):
+// the pair's K and V tiles move HBM -> registers -> an LDS ring (five buffers
+// for the pipelined loop, two otherwise) once per workgroup, and every wave
+// reads them from LDS in MFMA operand order (the pools' tile layout is kept in
+// LDS):
 //   S^T[key][row]  = K_page(16 x D) . Q^T(D x 16)        v_mfma 16x16x32, per page
 //   O^T[dim][row] += V^T_pair(D x 32) . P^T(32 x 16)     v_mfma 16x16x32, per pair
 // The QK accumulator of lane l holds keys 4*(l/16)+r of row l%16 for each page
@@ -21,7 +22,8 @@
 // operand (slot 8*(l/16)+r = page A key 4*(l/16)+r, slot +4 = page B key), and
 // the V chunks of the two pages are paired the same way, so P never leaves
 // registers.  Online softmax in fp32, log2 domain, as in the decode kernel.
-// A wave skips pairs that lie entirely after its last row.
+// A wave skips pairs that lie entirely after its last row; only the pairs on
+// its causal diagonal (or window edge, or the context's end) need masks.
 //
 // FP8 pages (kFp8): the staging loads e4m3fn codes (half the bytes) and their
 // per-key scaling factors, and the LDS store converts them, code * (1 / sf) in
