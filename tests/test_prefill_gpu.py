@@ -94,6 +94,33 @@ def test_prefill_invalid_pages_and_nan_tail(iva, dev):
     assert_close(out, oracle(c, bt=bt, window=24, n_sink=2), torch.float16, "invalid pages")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("chunked", [False, True], ids=["full", "chunk33"])
+def test_prefill_walk_lengths_and_mid_walk_holes(iva, dev, dtype, chunked):
+    """Causal walks of 1 to 8 page pairs (the pipelined loop loads past the last pair;
+    odd and even pair counts) with an invalid page id and an out-of-range one in the
+    middle of the longer walks, NaN bits on the pages those ids replaced and past every
+    context: pairs holding a hole or the context's end take masks, the rest none."""
+    lengths = [15, 16, 17, 32, 33, 64, 65, 96, 97, 128, 160, 161, 224, 250]
+    chunks = [min(n, 33) for n in lengths] if chunked else lengths
+    c = make(iva, lengths, chunks, 8, 2, 128, dtype, seed=13)
+    lay = c["layout"]
+    bt = lay.block_tables.clone()
+    for b, n in enumerate(lengths):
+        if n % 16:  # the tail of the last page
+            last = int(lay.block_tables[b, (n - 1) // 16])
+            c["k_pool"][last, :, :, n % 16:] = float("nan")
+            c["v_pool"][last, :, :, n % 16:] = float("nan")
+        if n >= 128:  # holes in the middle of the walk; the replaced pages hold NaN
+            for j, bad in ((3, -1), (6, lay.num_pages + 3)):
+                c["k_pool"][int(bt[b, j])] = float("nan")
+                c["v_pool"][int(bt[b, j])] = float("nan")
+                bt[b, j] = bad
+    out = run(iva, dev, c, bt=bt)
+    assert torch.isfinite(out).all()
+    assert_close(out, oracle(c, bt=bt), dtype, "walk lengths / holes")
+
+
 def test_chunked_equals_full_and_last_row_equals_decode(iva, dev):
     """Prefill in three chunks == one full prefill (both vs the oracle), and the last
     row equals the decode kernel's output for that position."""
