@@ -5,8 +5,6 @@ FFN's gate/up convention, and the paged backend refusing to run without the GPU
 library."""
 from __future__ import annotations
 
-import math
-
 import pytest
 import torch
 
