@@ -92,7 +92,6 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
                                                              const int32_t* __restrict__ qstart) {
   using Tr = Traits<DT>;
   using E = typename Tr::E;
-  using VChunk = typename Tr::VChunk;
   using S = PrefillShape<DT, D>;
   constexpr int X = 16 / (int)sizeof(E);
   constexpr int KLD = D / X / 4;  // 16-byte K reads per lane per page
