@@ -94,16 +94,18 @@ def test_prefill_invalid_pages_and_nan_tail(iva, dev):
     assert_close(out, oracle(c, bt=bt, window=24, n_sink=2), torch.float16, "invalid pages")
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("dtype,d", [(torch.float16, 128), (torch.bfloat16, 128),
+                                     (torch.float32, 128), (torch.float16, 256)], ids=str)
 @pytest.mark.parametrize("chunked", [False, True], ids=["full", "chunk33"])
-def test_prefill_walk_lengths_and_mid_walk_holes(iva, dev, dtype, chunked):
+def test_prefill_walk_lengths_and_mid_walk_holes(iva, dev, dtype, d, chunked):
     """Causal walks of 1 to 8 page pairs (the pipelined loop loads past the last pair;
     odd and even pair counts) with an invalid page id and an out-of-range one in the
     middle of the longer walks, NaN bits on the pages those ids replaced and past every
-    context: pairs holding a hole or the context's end take masks, the rest none."""
+    context: pairs holding a hole or the context's end take masks, the rest none.
+    fp32 and head_dim 256 run the unpipelined loop."""
     lengths = [15, 16, 17, 32, 33, 64, 65, 96, 97, 128, 160, 161, 224, 250]
     chunks = [min(n, 33) for n in lengths] if chunked else lengths
-    c = make(iva, lengths, chunks, 8, 2, 128, dtype, seed=13)
+    c = make(iva, lengths, chunks, 8, 2, d, dtype, seed=13)
     lay = c["layout"]
     bt = lay.block_tables.clone()
     for b, n in enumerate(lengths):
