@@ -518,28 +518,80 @@ __device__ inline void fold_slots(const DecodeArgs& a, int g, int idx, int D, in
 
 // Merges with VEC = 4 output elements per thread (16-byte partial loads, a quarter
 // of the threads) pay when units are many; with few, long units the merge needs
-// the parallelism of one element per thread.
+// the parallelism of one element per thread, and below kMergeSplitUnits units
+// (many partials per unit) four lanes share each element: lane l of a wave takes
+// element l % 16 of the wave's 16-element block and the quarter l / 16 of the
+// unit's partials, so each lane folds its quarter in one round trip of loads and
+// the four states are combined across lanes.
 constexpr int kMergeVec4Units = 1024;
+constexpr int kMergeSplitUnits = 256;
+constexpr int kSplitters = 4;
 
-// Merge of n partial slots into the out rows of unit (b, h).  Each thread owns VEC
-// consecutive output elements; they are spread over the workgroup and over grid z
-// (a unit split across workgroups when units are fewer than CUs).
-template <int DT, int VEC, typename SlotFn>
+// Log-sum-exp combine of the (M, L, O) states of lanes l, l ^ 16, l ^ 32, l ^ 48.
+__device__ inline void combine_splitters(float& M, float& L, float& O) {
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+    const float Mo = __shfl_xor(M, off), Lo = __shfl_xor(L, off), Oo = __shfl_xor(O, off);
+    const float mc = fmaxf(M, Mo);
+    const float m_use = mc == kNegInf ? 0.f : mc;
+    const float fa = exp2_fast(M - m_use), fb = exp2_fast(Mo - m_use);
+    L = L * fa + Lo * fb;
+    O = O * fa + Oo * fb;
+    M = mc;
+  }
+}
+
+// Output elements of a merge thread: VEC consecutive ones per thread over the
+// workgroup and grid z (S == 1), or one per lane with S lanes per element (S == 4,
+// see kMergeSplitUnits); `split` is the lane's quarter of the partials.  first
+// and step are uniform over a wave up to the lane's element offset, and G * D is a
+// multiple of 64, so every lane of a wave runs the same number of iterations.
+template <int VEC, int S>
+struct MergeLanes {
+  int first, step, split;
+  __device__ MergeLanes() {
+    if constexpr (S == 1) {
+      first = VEC * (threadIdx.x + blockIdx.z * blockDim.x);
+      step = VEC * blockDim.x * gridDim.z;
+      split = 0;
+    } else {
+      const int lane = threadIdx.x & 63;
+      const int waves = blockDim.x >> 6;
+      first = 16 * ((threadIdx.x >> 6) + waves * blockIdx.z) + (lane & 15);
+      step = 16 * waves * gridDim.z;
+      split = lane >> 4;
+    }
+  }
+  // Partials [begin, begin + count) of n this lane folds.
+  __device__ void range(int n, int& begin, int& count) const {
+    const int chunk = S == 1 ? n : (n + S - 1) / S;
+    begin = split * chunk;
+    count = max(0, min(chunk, n - begin));
+  }
+};
+
+// Merge of n partial slots into the out rows of unit (b, h), over the elements of
+// MergeLanes<VEC, S> (spread over the workgroup and grid z: a unit is split across
+// workgroups when units are fewer than CUs).
+template <int DT, int VEC, int S, typename SlotFn>
 __device__ inline void merge_slots(const DecodeArgs& a, int b, int h, int n, int D, SlotFn slot) {
   using E = typename Traits<DT>::E;
   const int G = a.G;
   const int Hq = a.Hkv * G;
   E* out = static_cast<E*>(a.out) + ((int64_t)b * Hq + h * G) * D;
-  for (int idx = VEC * (threadIdx.x + blockIdx.z * blockDim.x); idx < G * D;
-       idx += VEC * blockDim.x * gridDim.z) {
+  const MergeLanes<VEC, S> ml;
+  int i0, cnt;
+  ml.range(n, i0, cnt);
+  for (int idx = ml.first; idx < G * D; idx += ml.step) {
     float M = kNegInf, L = 0.f;
     typename std::conditional<VEC == 4, f32x4, float>::type O = {};
-    fold_slots<VEC>(a, idx / D, idx, D, n, slot, M, L, O);
+    fold_slots<VEC>(a, idx / D, idx, D, cnt, [&](int i) { return slot(i0 + i); }, M, L, O);
     if constexpr (VEC == 4) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) out[idx + r] = Traits<DT>::from_float(L > 0.f ? O[r] / L : 0.f);
     } else {
-      out[idx] = Traits<DT>::from_float(L > 0.f ? O / L : 0.f);
+      if constexpr (S > 1) combine_splitters(M, L, O);
+      if (ml.split == 0) out[idx] = Traits<DT>::from_float(L > 0.f ? O / L : 0.f);
     }
   }
 }
@@ -552,7 +604,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a, int D) 
   const int n_parts = num_partitions(w, a);
   if (n_parts <= 1) return;
   const int64_t base = ((int64_t)b * a.Hkv + h) * a.n_parts_max;
-  merge_slots<DT, 1>(a, b, h, n_parts, D, [&](int i) { return base + i; });
+  merge_slots<DT, 1, 1>(a, b, h, n_parts, D, [&](int i) { return base + i; });
 }
 
 // ---------------------------------------------------------------------------
@@ -768,7 +820,7 @@ __global__ __launch_bounds__(kStreamThreads, Ops::kWGsPerCU) void decode_stream_
 // Stream walk's merge: grid (kv head, sequence, column split), 256 or 64 threads.  Writes zeros for
 // an empty unit, skips a unit one wave finished (written directly), and folds
 // the fragments of a split unit (slots k + u, k = first..last wave).
-template <int DT, int VEC>
+template <int DT, int VEC, int S>
 __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, int D) {
   using E = typename Traits<DT>::E;
   const int h = blockIdx.x, b = blockIdx.y;
@@ -789,7 +841,7 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, 
   const int64_t k0 = split.owner(first_tile), k1 = split.owner(first_tile + n - 1);
   if (k0 == k1) return;
   const int64_t base = k0 + (int64_t)b * Hkv + h;
-  merge_slots<DT, VEC>(a, b, h, (int)(k1 - k0 + 1), D, [&](int i) { return base + i; });
+  merge_slots<DT, VEC, S>(a, b, h, (int)(k1 - k0 + 1), D, [&](int i) { return base + i; });
 }
 
 // Fused append's merge: grid (kv head, sequence, column split), 256 or 64 threads.  Scores the new
@@ -803,7 +855,7 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, 
 // factor sf = row_sf(max |x|) from a wave reduction over the row, codes e4m3(x * sf)),
 // attended as their dequantized values code / sf -- what an append followed by the
 // walk would read -- and their codes and factors are stored into the slot.
-template <int DT, int D, bool kFp8, int VEC>
+template <int DT, int D, bool kFp8, int VEC, int S>
 __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
   using Tr = Traits<DT>;
   using E = typename Tr::E;
@@ -821,9 +873,9 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
   const int n = p1 - p0;
   const int64_t T = (int64_t)Hkv * ptot;
   E* out = static_cast<E*>(a.out) + ((int64_t)b * Hq + h * G) * D;
-  const int idx0 = threadIdx.x + blockIdx.z * blockDim.x, stride = blockDim.x * gridDim.z;
   if (L <= 0) {
-    for (int idx = idx0; idx < G * D; idx += stride) out[idx] = Tr::from_float(0.f);
+    for (int idx = threadIdx.x + blockIdx.z * blockDim.x; idx < G * D; idx += blockDim.x * gridDim.z)
+      out[idx] = Tr::from_float(0.f);
     return;
   }
   // The new token's slot; an invalid page id there means it is neither stored nor
@@ -872,15 +924,19 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
     sfv = row_sf(va);
   }
   // Each thread owns VEC consecutive outputs idx .. of one query head g (D is a
-  // multiple of 64).  The new token's dot product q_g . k_new: with VEC == 1 the 64
+  // multiple of 64), or with S == 4 a quarter of one output's partials
+  // (MergeLanes).  The new token's dot product q_g . k_new: with VEC == 1 the
   // outputs of a wave share g and the wave sums lane-strided products (dims lane +
   // 64j); with VEC == 4 each lane sums its own four dims and the D/4 lanes of the
   // head reduce.  The operands (and the value elements) are loaded before the
   // partials, so every load of the thread is in flight at once; then the partials
-  // are folded, then the new token.
+  // are folded (and the splitters' states combined), then the new token.
   constexpr int NQ = VEC == 4 ? 4 : D / 64;  // dot-product terms per lane
   constexpr int kDotLanes = VEC == 4 ? D / 4 : 64;
-  for (int idx = VEC * idx0; idx < G * D; idx += VEC * stride) {
+  const MergeLanes<VEC, S> ml;
+  int f0, fcnt;
+  ml.range((int)nf, f0, fcnt);
+  for (int idx = ml.first; idx < G * D; idx += ml.step) {
     const int g = idx / D, col = idx - g * D;
     float qv[NQ], kv[NQ], vv[VEC];
 #pragma unroll
@@ -899,7 +955,8 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
     }
     float M = kNegInf, L_sum = 0.f;
     typename std::conditional<VEC == 4, f32x4, float>::type O = {};
-    fold_slots<VEC>(a, g, idx, D, (int)nf, [&](int i) { return base + i; }, M, L_sum, O);
+    fold_slots<VEC>(a, g, idx, D, fcnt, [&](int i) { return base + f0 + i; }, M, L_sum, O);
+    if constexpr (S > 1) combine_splitters(M, L_sum, O);
     float dot = 0.f;
 #pragma unroll
     for (int j = 0; j < NQ; ++j) dot += qv[j] * kv[j];
@@ -911,12 +968,14 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
     const float mn = fmaxf(M, sc);
     const float f = new_ok ? exp2_fast(M - mn) : 1.f, w = new_ok ? exp2_fast(sc - mn) : 0.f;
     L_sum = L_sum * f + w;
+    if (ml.split == 0) {
 #pragma unroll
-    for (int r = 0; r < VEC; ++r) {
-      float o;
-      if constexpr (VEC == 4) o = O[r];
-      else o = O;
-      out[idx + r] = Tr::from_float(L_sum > 0.f ? (o * f + vv[r] * w) / L_sum : 0.f);
+      for (int r = 0; r < VEC; ++r) {
+        float o;
+        if constexpr (VEC == 4) o = O[r];
+        else o = O;
+        out[idx + r] = Tr::from_float(L_sum > 0.f ? (o * f + vv[r] * w) / L_sum : 0.f);
+      }
     }
   }
 
@@ -1033,30 +1092,39 @@ void launch_stream(Stage stage, int D, dim3 grid, size_t smem, hipStream_t strea
   }
   // Merge grid: (kv head, sequence, column split) with one or four output elements
   // per thread, so every partial load of a unit is in flight at once; 64-thread
-  // workgroups when units are fewer than CUs, so few, long sequences still merge
-  // on many CUs.
+  // workgroups with four lanes per element when units are fewer than CUs, so few,
+  // long sequences (many partials each) still merge on many CUs in one round trip.
   const int units = a.Hkv * a.batch;
   const bool vec4 = units >= kMergeVec4Units;
-  const int threads = units >= 256 ? 256 : 64;
-  const int zsplit = cdiv(vec4 ? a.G * D / 4 : a.G * D, threads);
+  const bool split = units < kMergeSplitUnits;
+  const int threads = split ? 64 : 256;
+  const int elems_per_wg = vec4 ? 4 * threads : split ? 16 * (threads / 64) : threads;
+  const int zsplit = cdiv(a.G * D, elems_per_wg);
   const dim3 mgrid((unsigned)a.Hkv, (unsigned)a.batch, (unsigned)zsplit);
   if (stage == kFused) {
     if (vec4) {
       switch (D) {
-        case 64: decode_fused_merge_kernel<DT, 64, kFp8, 4><<<mgrid, threads, 0, stream>>>(a); break;
-        case 128: decode_fused_merge_kernel<DT, 128, kFp8, 4><<<mgrid, threads, 0, stream>>>(a); break;
-        default: decode_fused_merge_kernel<DT, 256, kFp8, 4><<<mgrid, threads, 0, stream>>>(a); break;
+        case 64: decode_fused_merge_kernel<DT, 64, kFp8, 4, 1><<<mgrid, threads, 0, stream>>>(a); break;
+        case 128: decode_fused_merge_kernel<DT, 128, kFp8, 4, 1><<<mgrid, threads, 0, stream>>>(a); break;
+        default: decode_fused_merge_kernel<DT, 256, kFp8, 4, 1><<<mgrid, threads, 0, stream>>>(a); break;
+      }
+    } else if (split) {
+      switch (D) {
+        case 64: decode_fused_merge_kernel<DT, 64, kFp8, 1, kSplitters><<<mgrid, threads, 0, stream>>>(a); break;
+        case 128: decode_fused_merge_kernel<DT, 128, kFp8, 1, kSplitters><<<mgrid, threads, 0, stream>>>(a); break;
+        default: decode_fused_merge_kernel<DT, 256, kFp8, 1, kSplitters><<<mgrid, threads, 0, stream>>>(a); break;
       }
     } else {
       switch (D) {
-        case 64: decode_fused_merge_kernel<DT, 64, kFp8, 1><<<mgrid, threads, 0, stream>>>(a); break;
-        case 128: decode_fused_merge_kernel<DT, 128, kFp8, 1><<<mgrid, threads, 0, stream>>>(a); break;
-        default: decode_fused_merge_kernel<DT, 256, kFp8, 1><<<mgrid, threads, 0, stream>>>(a); break;
+        case 64: decode_fused_merge_kernel<DT, 64, kFp8, 1, 1><<<mgrid, threads, 0, stream>>>(a); break;
+        case 128: decode_fused_merge_kernel<DT, 128, kFp8, 1, 1><<<mgrid, threads, 0, stream>>>(a); break;
+        default: decode_fused_merge_kernel<DT, 256, kFp8, 1, 1><<<mgrid, threads, 0, stream>>>(a); break;
       }
     }
   } else if (stage != kPartial) {
-    if (vec4) decode_stream_merge_kernel<DT, 4><<<mgrid, threads, 0, stream>>>(a, D);
-    else decode_stream_merge_kernel<DT, 1><<<mgrid, threads, 0, stream>>>(a, D);
+    if (vec4) decode_stream_merge_kernel<DT, 4, 1><<<mgrid, threads, 0, stream>>>(a, D);
+    else if (split) decode_stream_merge_kernel<DT, 1, kSplitters><<<mgrid, threads, 0, stream>>>(a, D);
+    else decode_stream_merge_kernel<DT, 1, 1><<<mgrid, threads, 0, stream>>>(a, D);
   }
 }
 
