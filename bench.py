@@ -81,7 +81,8 @@ def parse_args():
                    help="0 = default (stream) walk; > 0 = partitioned walk of that size")
     p.add_argument("--kernel-launches", type=int, default=200,
                    help="launches of the paged walk timed for the roofline figure")
-    p.add_argument("--cpu-reps", type=int, default=10, help="timed CPU-baseline reps (0 = skip)")
+    p.add_argument("--cpu-reps", type=int, default=40,
+                   help="timed CPU-baseline reps, about 10 s of CPU work at C2 (0 = skip)")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of graphs")
     p.add_argument("--unfused", action="store_true",
                    help="step = ivakv_append + ivakv_decode_attn instead of the fused op")
