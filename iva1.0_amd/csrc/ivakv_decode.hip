@@ -382,7 +382,7 @@ __global__ __launch_bounds__(kThreads, kPartialWGsPerCU) void decode_partial_ker
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ln = lane & 15;
   const int lq = lane >> 4;
-  const PageWalk w = make_walk(ctx[b], a.window, a.n_sink, kBS);
+  const PageWalk w = seq_walk(a, ctx[b]);  // fused: the positions before the new token
   const int n_parts = num_partitions(w, a);
   if (part >= n_parts) return;
 
@@ -394,6 +394,31 @@ __global__ __launch_bounds__(kThreads, kPartialWGsPerCU) void decode_partial_ker
   Ops::load_q(a, b, h, ln, lq, qr);
   typename Ops::State st;
   st.reset();
+
+  // Fused (one partition per sequence): the new token's operands are loaded before
+  // the walk, so they arrive with its first tiles: the slot's page id, for the
+  // dot products q_g . k_new the lane-strided dims of k_new and of the wave's
+  // heads g = wave + 4t (G <= 16), and this thread's element of v_new (the output
+  // loop's dim is threadIdx.x % D in every round).  Every load is unconditional
+  // (valid addresses when not fused, values then unused): a conditional load
+  // would be waited for at the branch's join.
+  constexpr int DJ = D / 64;
+  const int L_ctx = ctx[b];
+  const bool slot_in_table = a.fused && L_ctx > 0 && (L_ctx - 1) / kBS < a.max_blocks;
+  const int32_t slot_entry = slot_in_table ? bt[(int64_t)b * a.max_blocks + (L_ctx - 1) / kBS]
+                                           : ctx[b];
+  const int64_t row_nh = ((int64_t)b * a.Hkv + h) * D;
+  const E* qb = static_cast<const E*>(a.q) + ((int64_t)b * Hq + h * G) * D;
+  const E* kn = a.fused ? static_cast<const E*>(a.k_new) + row_nh : qb;
+  const E* vn = a.fused ? static_cast<const E*>(a.v_new) + row_nh : qb;
+  float kd[DJ], qd[4][DJ];
+#pragma unroll
+  for (int j = 0; j < DJ; ++j) kd[j] = (float)kn[lane + 64 * j];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int j = 0; j < DJ; ++j) qd[t][j] = (float)qb[min(wave + 4 * t, G - 1) * D + lane + 64 * j];
+  const float v_own = (float)vn[threadIdx.x % D];
 
   const int v_begin = part * a.part_pages + wave;
   const int v_end = min(min((part + 1) * a.part_pages, w.n_eff), table_pages(w, a.max_blocks));
@@ -429,6 +454,7 @@ __global__ __launch_bounds__(kThreads, kPartialWGsPerCU) void decode_partial_ker
   float* s_fin = s_l + kWaves * 16;        // [16][2] merged (max, sum)
   float* s_acc = s_fin + 32;               // [kWaves][G][D + 4]
   constexpr int kRow = D + 4;
+  float* s_dot = s_acc + kWaves * G * kRow;  // [G] fused: q_g . k_new
   if (lq == 0) {
     s_m[wave * 16 + ln] = st.m_run;
     s_l[wave * 16 + ln] = l_tot;
@@ -451,9 +477,27 @@ __global__ __launch_bounds__(kThreads, kPartialWGsPerCU) void decode_partial_ker
       s_fin[2 * ln + 1] = L;
     }
   }
+  // Fused: the new token's scores q_g . k_new from the prefetched operands, one
+  // head per wave in turn, a wave reduction each.
+  if (a.fused) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (wave + 4 * t >= G) break;
+      float dot = 0.f;
+#pragma unroll
+      for (int j = 0; j < DJ; ++j) dot += qd[t][j] * kd[j];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o);
+      if (lane == 0) s_dot[wave + 4 * t] = dot;
+    }
+  }
   __syncthreads();
 
   const bool direct = n_parts == 1;
+  // The new token's slot (position L-1); an invalid page id there means it is
+  // neither stored nor attended, as in the stream walk's fused merge.
+  const int64_t new_page = slot_in_table ? (int64_t)slot_entry : -1;
+  const bool new_ok = new_page >= 0 && new_page < a.num_pages;
   const int64_t part_base = (((int64_t)b * a.Hkv + h) * a.n_parts_max + part) * G;
   for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
     const int gg = idx / D, d = idx - (idx / D) * D;
@@ -461,7 +505,16 @@ __global__ __launch_bounds__(kThreads, kPartialWGsPerCU) void decode_partial_ker
 #pragma unroll
     for (int u = 0; u < kWaves; ++u) o += s_acc[(u * G + gg) * kRow + d];
     if (direct) {
-      const float L = s_fin[2 * gg + 1];
+      float L = s_fin[2 * gg + 1];
+      if (a.fused) {  // fold the new token (o and L are relative to max(M, 0 if none))
+        const float M = s_fin[2 * gg];
+        const float sc = s_dot[gg] * a.scale_log2;
+        const float mn = fmaxf(M, sc);
+        const float f = !new_ok ? 1.f : (M == kNegInf ? 0.f : exp2_fast(M - mn));
+        const float wn = new_ok ? exp2_fast(sc - mn) : 0.f;
+        L = L * f + wn;
+        o = o * f + v_own * wn;
+      }
       const float r = L > 0.f ? o / L : 0.f;
       static_cast<E*>(a.out)[((int64_t)b * Hq + h * G + gg) * D + d] = Ops::Tr::from_float(r);
     } else {
@@ -470,6 +523,19 @@ __global__ __launch_bounds__(kThreads, kPartialWGsPerCU) void decode_partial_ker
         a.ws_ml[(part_base + gg) * 2] = s_fin[2 * gg];
         a.ws_ml[(part_base + gg) * 2 + 1] = s_fin[2 * gg + 1];
       }
+    }
+  }
+  // Fused: the new rows go to the slot of position L-1 (after every wave's reads
+  // of that page, which the barriers above order).
+  if (new_ok) {
+    constexpr int X = 16 / (int)sizeof(E);
+    const int row = (L_ctx - 1) % kBS;
+    const int64_t tile = (new_page * a.Hkv + h) * (int64_t)D * kBS;
+    E* kp = static_cast<E*>(const_cast<void*>(a.k_pool)) + tile;
+    E* vp = static_cast<E*>(const_cast<void*>(a.v_pool)) + tile;
+    for (int d = threadIdx.x; d < D; d += kThreads) {
+      kp[((d / X) * kBS + row) * X + d % X] = kn[d];
+      vp[d * kBS + row] = vn[d];
     }
   }
 }
@@ -1033,9 +1099,6 @@ int make_plan(const char* name, Stage stage, int batch, int num_q_heads, int num
   if (n_sink < 0) return fail(IVAKV_E_ARG, "%s: negative n_sink", name);
   plan->G = G;
   plan->stream = partition_pages <= 0 && batch <= kMaxStreamBatch;
-  if (stage == kFused && !plan->stream)
-    return fail(IVAKV_E_SHAPE, "%s: the fused append runs on the default walk: partition_pages "
-                "must be <= 0 and batch <= %d", name, kMaxStreamBatch);
   const size_t units = (size_t)batch * num_kv_heads;
   if (plan->stream) {
     plan->part_pages = 0;
@@ -1053,6 +1116,9 @@ int make_plan(const char* name, Stage stage, int batch, int num_q_heads, int num
   if (n_parts_max > 65535)
     return fail(IVAKV_E_SHAPE, "%s: %d partitions per sequence exceed 65535; raise partition_pages",
                 name, n_parts_max);
+  if (stage == kFused && n_parts_max > 1)
+    return fail(IVAKV_E_SHAPE, "%s: the fused append runs on the stream walk (batch <= %d) or "
+                "on one partition per sequence", name, kMaxStreamBatch);
   plan->part_pages = pp;
   plan->n_parts_max = n_parts_max;
   plan->pref_elems = 0;
@@ -1140,6 +1206,22 @@ int stream_workgroups(int per_cu) {
   return wgs < kMaxStreamWaves / kStreamWaves ? wgs : kMaxStreamWaves / kStreamWaves;
 }
 
+// Fused calls on short tables whose batch has at least one (sequence, kv head)
+// unit per CU take one partition per sequence: a workgroup per unit walks it,
+// merges its waves in LDS, folds the new token and writes out, with no merge
+// kernel (C3's decode shape: 9.9 against 14.9 us for walk + merge).  Returns
+// the partition size for that, or 0 for the stream walk.
+constexpr int kSinglePartitionMaxPages = 64;
+int single_partition_pages(int batch, int num_kv_heads, int max_blocks, int window, int n_sink) {
+  const int max_eff = max_effective_pages(max_blocks, window, n_sink, kBS);
+  if (max_eff <= 0 || max_eff > kSinglePartitionMaxPages || batch > 65535) return 0;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  return (int64_t)batch * num_kv_heads >= cus ? max_eff : 0;
+}
+
 int decode_entry(Stage stage, const char* name, const void* q, const void* k_pool,
                  const void* v_pool, const int32_t* block_tables, const int32_t* context_lens,
                  void* out, void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
@@ -1157,6 +1239,8 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
     if (batch > 0 && (!k_scale || !v_scale || !aligned16(k_scale) || !aligned16(v_scale)))
       return fail(IVAKV_E_ARG, "%s: k_scale / v_scale must be 16-byte aligned device pointers", name);
   }
+  if (stage == kFused && !fp8 && partition_pages <= 0 && block_size == kBS && n_sink >= 0)
+    partition_pages = single_partition_pages(batch, num_kv_heads, max_blocks, window, n_sink);
   Plan plan;
   int st = make_plan(name, stage, batch, num_q_heads, num_kv_heads, head_dim, block_size,
                      max_blocks, window, n_sink, partition_pages, &plan);
@@ -1224,12 +1308,13 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
     }
     return launch_status(name);
   }
-  if (stage == kFull || stage == kPartial) {
+  if (stage == kFull || stage == kPartial || stage == kFused) {
     // Partition slowest: consecutive workgroups (which the dispatcher deals
     // round-robin to the 8 XCDs) are different kv heads / sequences of equal
     // partition index, so every XCD gets an even share of the pages.
     dim3 grid((unsigned)num_kv_heads, (unsigned)batch, (unsigned)plan.n_parts_max);
-    const size_t smem = sizeof(float) * (2 * kWaves * 16 + 32 + (size_t)kWaves * plan.G * (head_dim + 4));
+    const size_t smem =
+        sizeof(float) * (2 * kWaves * 16 + 32 + (size_t)kWaves * plan.G * (head_dim + 4) + 16);
     switch (dtype) {
       case IVAKV_F16: launch_partial<IVAKV_F16>(head_dim, grid, smem, stream, a); break;
       case IVAKV_BF16: launch_partial<IVAKV_BF16>(head_dim, grid, smem, stream, a); break;

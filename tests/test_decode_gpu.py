@@ -372,16 +372,56 @@ def test_fused_append_attention(iva, dev, dtype, window, n_sink):
     assert_close(unfused, ref, dtype, what="append + decode")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("window,n_sink", [(0, 0), (100, 4)])
+def test_fused_one_partition_per_sequence(iva, dev, dtype, d, window, n_sink):
+    """Batches with at least one (sequence, kv head) unit per CU whose tables hold at
+    most 64 pages run the fused op on one partition per sequence (a workgroup per unit,
+    its waves merged in LDS, the new token folded in, no merge kernel): 128 ragged
+    sequences of up to 1000 tokens x 4 kv heads, with a new token alone (L=1), an empty
+    sequence, a new token opening and closing a page, and an invalid page id under a
+    new token.  Pools bit-identical to append + decode, output within the dtype's
+    tolerance of the fp64 oracle."""
+    gen = torch.Generator().manual_seed(23 + d)
+    lengths = [1, 0, 17, 16, 1000, 2, 33] + torch.randint(0, 1000, (121,), generator=gen).tolist()
+    hkv, g = 4, 4
+    base = iva.workloads.decode_batch(lengths, hkv * g, hkv, d, dtype, seed=70 + d,
+                                      scale=d ** -0.5, extra_pages=4)
+    lay = base["layout"]
+    assert lay.block_tables.shape[1] <= 64
+    bt = lay.block_tables.clone()
+    bt[6, 2] = -1                      # the new token of sequence 6 (L=33) sits on an invalid page
+    lay = iva.workloads.PagedLayout(lay.lengths, bt, lay.num_pages)
+    k_new = (torch.randn(len(lengths), hkv, d, generator=gen) * d ** -0.5).to(dtype)
+    v_new = (torch.randn(len(lengths), hkv, d, generator=gen) * d ** -0.5).to(dtype)
+    kp_a, vp_a = base["k_pool"].clone().to(dev), base["v_pool"].clone().to(dev)
+    slots = torch.tensor([int(bt[b, (n - 1) // 16]) * 16 + (n - 1) % 16
+                          if n > 0 and bt[b, (n - 1) // 16] >= 0 else -1
+                          for b, n in enumerate(lengths)], dtype=torch.int32)
+    iva.kv_append(k_new.to(dev), v_new.to(dev), kp_a, vp_a, slots.to(dev))
+    kp_f, vp_f = base["k_pool"].clone().to(dev), base["v_pool"].clone().to(dev)
+    out = iva.paged_decode_append_attention(base["q"].to(dev), k_new.to(dev), v_new.to(dev), kp_f,
+                                            vp_f, bt.to(dev), lay.context_lens.to(dev),
+                                            window=window, n_sink=n_sink)
+    ti = {torch.float32: torch.int32}.get(dtype, torch.int16)
+    assert torch.equal(kp_a.view(ti), kp_f.view(ti)) and torch.equal(vp_a.view(ti), vp_f.view(ti))
+    ref = oracle_out(dict(base, k_pool=kp_a.cpu(), v_pool=vp_a.cpu()), window=window,
+                     n_sink=n_sink, layout=lay)
+    assert_close(out, ref, dtype, what=f"fused one partition d{d} w{window}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("d", [64, 128, 256])
 def test_many_units_merges(iva, dev, dtype, d):
     """Batches of >= 1024 (sequence, kv head) units take the merges with four output
     elements per thread (the fused op's new-token dot product then sums over the D/4
-    lanes of a head): 160 short ragged sequences x 8 kv heads.  Fused op: pools
-    bit-identical to append + decode; both outputs within the dtype's tolerance of the
-    fp64 oracle."""
+    lanes of a head): 160 short ragged sequences x 8 kv heads, one of 1100 tokens so
+    that the table is wider than one partition's limit and the fused op keeps the
+    stream walk.  Fused op: pools bit-identical to append + decode; both outputs within
+    the dtype's tolerance of the fp64 oracle."""
     gen = torch.Generator().manual_seed(11)
-    lengths = [1, 0, 17, 16, 300, 2] + torch.randint(0, 80, (154,), generator=gen).tolist()
+    lengths = [1, 0, 17, 16, 1100, 2] + torch.randint(0, 80, (154,), generator=gen).tolist()
     hkv, g = 8, 4
     base = iva.workloads.decode_batch(lengths, hkv * g, hkv, d, dtype, seed=60 + d,
                                       scale=d ** -0.5, extra_pages=4)
