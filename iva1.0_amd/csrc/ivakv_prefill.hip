@@ -457,7 +457,7 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
       pb[r] = exp2_fast(__builtin_fmaf(sl[4 + r], c_log2, -m_use));
     }
     l_run[rb] += ((pa[0] + pa[1]) + (pa[2] + pa[3])) + ((pb[0] + pb[1]) + (pb[2] + pb[3]));
-    const typename Tr::P8 p8 = Tr::pack_p8(pa, pb);
+    const typename Tr::PP8 p8 = Tr::pack_pp8(pa, pb);
 #pragma unroll
     for (int m = 0; m < NB; ++m) acc[rb][m] = Tr::pv_pair(vp[m], p8, acc[rb][m]);
   };

@@ -82,7 +82,10 @@ struct Traits<IVAKV_F16> {
   // then of page B (words 2-3), as one 16-byte read.
   using VPair = Chunk16;
   static __device__ inline VPair read_vpair(const char* g) { return *reinterpret_cast<const Chunk16*>(g); }
-  static __device__ inline f32x4 pv_pair(const VPair& v, const P8& p, f32x4 acc) {
+  // P of the prefill's PV product: rounded once to the value dtype.
+  using PP8 = P8;
+  static __device__ inline PP8 pack_pp8(const float pa[4], const float pb[4]) { return pack_p8(pa, pb); }
+  static __device__ inline f32x4 pv_pair(const VPair& v, const PP8& p, f32x4 acc) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, v), p, acc, 0, 0, 0);
   }
   static __device__ inline void mask_pair(VPair& v, const bool va[4], const bool vb[4]) {
@@ -144,10 +147,16 @@ struct Traits<IVAKV_BF16> {
   }
   using VPair = Chunk16;  // as for fp16: page A's granule, then page B's
   static __device__ inline VPair read_vpair(const char* g) { return *reinterpret_cast<const Chunk16*>(g); }
-  static __device__ inline f32x4 pv_pair(const VPair& v, const P8& p, f32x4 acc) {
-    const bf16x8 vv = __builtin_bit_cast(bf16x8, v);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, p.hi, acc, 0, 0, 0);
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, p.lo, acc, 0, 0, 0);
+  // The prefill's P is rounded once to bf16, as the reference's bf16 softmax output
+  // is (max error vs the exact output ~1e-4 on unit-scale data, <= 2^-9 max|v| with
+  // one dominant key): one PV MFMA instead of two, where the MFMA-bound prefill pays.
+  using PP8 = bf16x8;
+  static __device__ inline PP8 pack_pp8(const float pa[4], const float pb[4]) {
+    return PP8{(__bf16)pa[0], (__bf16)pa[1], (__bf16)pa[2], (__bf16)pa[3],
+               (__bf16)pb[0], (__bf16)pb[1], (__bf16)pb[2], (__bf16)pb[3]};
+  }
+  static __device__ inline f32x4 pv_pair(const VPair& v, const PP8& p, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, v), p, acc, 0, 0, 0);
   }
   static __device__ inline void mask_pair(VPair& v, const bool va[4], const bool vb[4]) {
     mask_pair16(v, va, vb);
@@ -193,7 +202,9 @@ struct Traits<IVAKV_F32> {
   static __device__ inline VPair read_vpair(const char* g) {
     return VPair{reinterpret_cast<const Chunk16*>(g)[0], reinterpret_cast<const Chunk16*>(g)[1]};
   }
-  static __device__ inline f32x4 pv_pair(const VPair& v, const P8& p, f32x4 acc) {
+  using PP8 = P8;
+  static __device__ inline PP8 pack_pp8(const float pa[4], const float pb[4]) { return pack_p8(pa, pb); }
+  static __device__ inline f32x4 pv_pair(const VPair& v, const PP8& p, f32x4 acc) {
     return pv32(v.a, v.b, p, acc);
   }
   static __device__ inline E from_float(float x) { return x; }
