@@ -124,7 +124,7 @@ int ivakv_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
  * instead splits each sequence into partitions of that many pages (one
  * workgroup each) merged the same way.
  * Supported: block_size 16, head_dim 64/128/256, num_q_heads/num_kv_heads
- * in {1,2,4,8,16}.
+ * (the GQA group) any integer from 1 to 16.
  * Replaces: the cache branch of AttentionTorch.forward -- scores, causal /
  * sliding-window / sink masks, softmax, PV (src/core/attention.py:77-102,
  * 115-148) -- on the paged cache.

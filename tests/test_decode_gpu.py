@@ -90,11 +90,16 @@ def test_small_vs_oracle(iva, dev, dtype, head_dim, group):
     assert_close(out, oracle_out(d), dtype, what=f"{dtype} D{head_dim} G{group}")
 
 
-@pytest.mark.parametrize("group", [2, 8])
+@pytest.mark.parametrize("group", [2, 3, 5, 6, 8, 12])
 def test_other_groups(iva, dev, group):
+    """GQA groups other than the sweep's, powers of two or not (any group up to 16):
+    stream walk and partitioned walk."""
     d = iva.workloads.decode_batch([5, 300, 999], 3 * group, 3, 128, torch.float16, seed=group,
                                    scale=128 ** -0.5)
-    assert_close(run_gpu(iva, dev, d), oracle_out(d), torch.float16, rel_ulp=False)
+    ref = oracle_out(d)
+    assert_close(run_gpu(iva, dev, d), ref, torch.float16, rel_ulp=False, what=f"G{group}")
+    assert_close(run_gpu(iva, dev, d, partition_pages=7), ref, torch.float16, rel_ulp=False,
+                 what=f"G{group} partitioned")
 
 
 @pytest.mark.parametrize("pp", [1, 2, 3, 5, 16, 64])
