@@ -74,10 +74,6 @@ struct Traits<IVAKV_F16> {
     return P8{(_Float16)pa[0], (_Float16)pa[1], (_Float16)pa[2], (_Float16)pa[3],
               (_Float16)pb[0], (_Float16)pb[1], (_Float16)pb[2], (_Float16)pb[3]};
   }
-  static __device__ inline f32x4 pv32(const VChunk& va, const VChunk& vb, const P8& p, f32x4 acc) {
-    const Chunk16 v{{va.w[0], va.w[1], vb.w[0], vb.w[1]}};
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, v), p, acc, 0, 0, 0);
-  }
   // PV operand of one dim over a page pair: keys 4lq..4lq+3 of page A (words 0-1)
   // then of page B (words 2-3), as one 16-byte read.
   using VPair = Chunk16;
@@ -124,26 +120,6 @@ struct Traits<IVAKV_BF16> {
     const i16x4 va = __builtin_bit_cast(i16x4, v);
     acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, p.hi, acc, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, p.lo, acc, 0, 0, 0);
-  }
-  struct P8 {
-    bf16x8 hi, lo;
-  };
-  static __device__ inline P8 pack_p8(const float pa[4], const float pb[4]) {
-    P8 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      r.hi[i] = (__bf16)pa[i];
-      r.hi[4 + i] = (__bf16)pb[i];
-      r.lo[i] = (__bf16)(pa[i] - (float)r.hi[i]);
-      r.lo[4 + i] = (__bf16)(pb[i] - (float)r.hi[4 + i]);
-    }
-    return r;
-  }
-  static __device__ inline f32x4 pv32(const VChunk& va, const VChunk& vb, const P8& p, f32x4 acc) {
-    const Chunk16 v{{va.w[0], va.w[1], vb.w[0], vb.w[1]}};
-    const bf16x8 vv = __builtin_bit_cast(bf16x8, v);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, p.hi, acc, 0, 0, 0);
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv, p.lo, acc, 0, 0, 0);
   }
   using VPair = Chunk16;  // as for fp16: page A's granule, then page B's
   static __device__ inline VPair read_vpair(const char* g) { return *reinterpret_cast<const Chunk16*>(g); }
