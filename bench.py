@@ -98,10 +98,12 @@ def parse_args():
     p.add_argument("--no-target-4k", dest="target_4k", action="store_false",
                    help="skip the second measurement at the target shape (B 32, every "
                         "sequence at context 4096) that the default line carries")
-    p.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "prefill", "c2fp8"), default="c2",
+    p.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "prefill", "c2fp8", "ops"),
+                   default="c2",
                    help="c2 (default): the contract line; c3 dense-decoder tokens/s, c4 "
                         "long-context window+sinks decode, c5 ragged churn, prefill: 512-token "
-                        "chunks over paged context, c2fp8: C2 over FP8 pages (informational lines)")
+                        "chunks over paged context, c2fp8: C2 over FP8 pages, ops: the append / "
+                        "gather / kv_ops / page-move kernels (informational lines)")
     return p.parse_args()
 
 
@@ -646,6 +648,82 @@ def measure_decode(args, iva, torch, dev, lengths):
             "pool_bytes": pool_bytes, "batch": batch}
 
 
+def bench_ops(args, iva, torch, dev):
+    """The hot path's data-movement kernels at realistic sizes (fp16, 8 kv heads, D 128),
+    each as average time over back-to-back launches on one stream: the append of
+    16 x 512-token chunks (8192 rows; plain and with RoPE fused), the gather of the C2
+    batch into contiguous K/V, the kv_ops index gather / scatter on a [32, 8, 4096, 128]
+    cache, and the compaction's page moves (4096 pages).  Bytes are what each op must
+    read and write; GB/s against the 8 TB/s HBM peak."""
+    wl = iva.workloads
+    hkv, d, es = 8, 128, 2
+    gen = torch.Generator(device=dev).manual_seed(3)
+    out = {}
+
+    def timed(name, fn, nbytes, reps=50):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 2), "bytes": int(nbytes), "gbps": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+    # append: 8192 new rows into a 64k-page pool (read the rows, write their slots)
+    n = 16 * 512
+    pages = 65536
+    ks, vs = iva.pool_shapes(pages, hkv, d, 16, torch.float16)
+    k_pool = torch.zeros(ks, dtype=torch.float16, device=dev)
+    v_pool = torch.zeros(vs, dtype=torch.float16, device=dev)
+    k_new = torch.randn(n, hkv, d, generator=gen, device=dev).half()
+    v_new = torch.randn(n, hkv, d, generator=gen, device=dev).half()
+    slots = (torch.randperm(pages, generator=torch.Generator().manual_seed(4))[: n // 16]
+             .repeat_interleave(16) * 16 + torch.arange(n) % 16).int().to(dev)
+    pos = (torch.arange(n) % 2048).int().to(dev)
+    app_bytes = 4 * n * hkv * d * es + 4 * n
+    timed("append", lambda: iva.kv_append(k_new, v_new, k_pool, v_pool, slots), app_bytes)
+    timed("append_rope", lambda: iva.kv_append(k_new, v_new, k_pool, v_pool, slots,
+                                               rope_positions=pos), app_bytes + 4 * n)
+    # compaction's page moves: 4096 pages (K and V tiles of all kv heads) to free ids
+    src = torch.arange(0, 8192, 2, dtype=torch.int32, device=dev)
+    dst = torch.arange(32768, 32768 + 4096, dtype=torch.int32, device=dev)
+    timed("copy_pages", lambda: iva.copy_pages(k_pool, v_pool, src, dst),
+          2 * 4096 * 2 * hkv * 16 * d * es + 8 * 4096)
+    del k_pool, v_pool
+    # gather of the C2 batch into contiguous [B, Hkv, max L, D]
+    lengths = wl.c2_lengths(seed=0)
+    dd = wl.decode_batch(lengths, 32, hkv, d, torch.float16, seed=100, device=dev)
+    lay = dd["layout"]
+    bt, ctx = lay.block_tables.to(dev), lay.context_lens.to(dev)
+    lmax = max(lengths)
+    kg = torch.empty(len(lengths), hkv, lmax, d, dtype=torch.float16, device=dev)
+    vg = torch.empty_like(kg)
+    timed("gather", lambda: iva.kv_gather(dd["k_pool"], dd["v_pool"], bt, ctx, out_len=lmax,
+                                          out=(kg, vg)),
+          2 * sum(lengths) * hkv * d * es + 2 * kg.numel() * es)
+    del dd, kg, vg
+    # kv_ops on a contiguous cache: gather 1024 positions, scatter 1024 rows (the op
+    # returns a new cache: a full copy plus the scattered rows)
+    cache = torch.randn(32, hkv, 4096, d, generator=gen, device=dev).half()
+    idx = torch.randperm(4096, generator=torch.Generator().manual_seed(5))[:1024].to(dev)
+    vals = torch.randn(32, hkv, 1024, d, generator=gen, device=dev).half()
+    rows = 32 * hkv * 1024 * d * es
+    timed("kv_ops_gather", lambda: iva.kv_ops(cache, idx, operation="gather"), 2 * rows, reps=20)
+    timed("kv_ops_scatter", lambda: iva.kv_ops(cache, idx, vals, operation="scatter"),
+          2 * cache.numel() * es + 2 * rows, reps=20)
+    return {"metric": "hot-path data-movement kernels GB/s (fraction of 8 TB/s HBM)",
+            "workload": "ops", "dtype": "f16", "data": "synthetic",
+            "config": {"num_kv_heads": hkv, "head_dim": d, "block_size": 16,
+                       "launch": "eager, back-to-back on one stream"},
+            "kernels": out}
+
+
 def main():
     args = parse_args()
     if args.summarize_pmc:
@@ -666,7 +744,7 @@ def main():
     wl = iva.workloads
     if args.workload != "c2":
         fn = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "prefill": bench_prefill,
-              "c2fp8": bench_c2fp8}[args.workload]
+              "c2fp8": bench_c2fp8, "ops": bench_ops}[args.workload]
         print(json.dumps(fn(args, iva, torch, dev)), flush=True)
         return
 

@@ -35,13 +35,20 @@ template <typename E, bool VEC>
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   constexpr int X = 16 / sizeof(E);
   const int nch = a.D / X;
+  // Thread order (token % 16, chunk, head, token / 16): the 16 lanes of a token
+  // group cover 16 consecutive tokens, which a chunk append puts in consecutive
+  // slots of one page, so their K chunks are 256 contiguous bytes and each V dim's
+  // elements one 32-byte row, instead of 2-byte stores 32 bytes apart.
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)a.n_tok * a.Hkv * nch;
+  const int64_t total = (int64_t)cdiv(a.n_tok, 16) * 16 * a.Hkv * nch;
   if (gid >= total) return;
-  const int c = (int)(gid % nch);
-  const int64_t th = gid / nch;
-  const int h = (int)(th % a.Hkv);
-  const int64_t t = th / a.Hkv;
+  const int t_lo = (int)(gid & 15);
+  const int64_t g1 = gid >> 4;
+  const int c = (int)(g1 % nch);
+  const int64_t g2 = g1 / nch;
+  const int h = (int)(g2 % a.Hkv);
+  const int64_t t = (g2 / a.Hkv) * 16 + t_lo;
+  if (t >= a.n_tok) return;
   const int64_t slot = a.slots[t];
   if (slot < 0 || slot >= a.n_slots) return;
   const int64_t page = slot / a.bs;
@@ -215,7 +222,7 @@ extern "C" int ivakv_append(const void* k_new, const void* v_new, int64_t k_tok_
   const bool vec = aligned16(k_new) && aligned16(v_new) && aligned16(k_pool) && aligned16(v_pool) &&
                    (k_tok_stride % X == 0) && (k_head_stride % X == 0) &&
                    (v_tok_stride % X == 0) && (v_head_stride % X == 0);
-  const int64_t total = (int64_t)n_tok * num_kv_heads * (head_dim / X);
+  const int64_t total = (int64_t)cdiv(n_tok, 16) * 16 * num_kv_heads * (head_dim / X);
   const unsigned grid = blocks_for(total, 256);
   if ((int64_t)grid > kMaxGrid) return fail(IVAKV_E_SHAPE, "ivakv_append: too many rows");
   if (es == 4) {

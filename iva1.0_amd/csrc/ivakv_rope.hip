@@ -74,12 +74,18 @@ template <typename E>
 __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
   constexpr int X = 16 / sizeof(E);
   const int nch = a.D / X;
+  // Thread order (token % 16, chunk, head, token / 16), as in append_kernel: 16
+  // consecutive tokens (consecutive slots of a page in a chunk append) per lane
+  // group, so K and V stores coalesce.
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (int64_t)a.n_tok * a.Hkv * nch) return;
-  const int c = (int)(gid % nch);
-  const int64_t th = gid / nch;
-  const int h = (int)(th % a.Hkv);
-  const int64_t t = th / a.Hkv;
+  if (gid >= (int64_t)cdiv(a.n_tok, 16) * 16 * a.Hkv * nch) return;
+  const int t_lo = (int)(gid & 15);
+  const int64_t g1 = gid >> 4;
+  const int c = (int)(g1 % nch);
+  const int64_t g2 = g1 / nch;
+  const int h = (int)(g2 % a.Hkv);
+  const int64_t t = (g2 / a.Hkv) * 16 + t_lo;
+  if (t >= a.n_tok) return;
   const int64_t slot = a.slots[t];
   if (slot < 0 || slot >= a.n_slots) return;
   const int64_t page = slot / a.bs;
@@ -186,7 +192,7 @@ extern "C" int ivakv_append_rope(const void* k_new, const void* v_new, int64_t k
   AppendRopeArgs a{k_new, v_new, k_tok_stride, k_head_stride, v_tok_stride, v_head_stride,
                    k_pool, v_pool, slot_mapping, positions, n_tok, num_kv_heads, head_dim,
                    block_size, (int64_t)num_pages * block_size, theta};
-  const int64_t total = (int64_t)n_tok * num_kv_heads * (head_dim / X);
+  const int64_t total = (int64_t)cdiv(n_tok, 16) * 16 * num_kv_heads * (head_dim / X);
   const int64_t blocks = (total + 255) / 256;
   if (blocks > kMaxGridR) return fail(IVAKV_E_SHAPE, "%s: too many rows", name);
   switch (dtype) {
