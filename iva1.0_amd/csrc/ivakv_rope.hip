@@ -29,10 +29,27 @@ __device__ inline void rotate_pair(E& x0, E& x1, float c, float s) {
   x1 = (E)(a * s + b * c);
 }
 
+// f_i = 1 / theta^(2i / D), in double, stored as float.
+__device__ inline float inv_freq(int i, int D, float theta) {
+  return (float)(1.0 / pow((double)theta, (double)(2 * i) / (double)D));
+}
+
+// Each workgroup computes f_i once into LDS (head_dim up to 2 * kFreqTable) instead of
+// once per (token, head, pair): the double pow costs more than the row's memory traffic.
+// Pairs past the table compute f_i directly, to the same float.
+constexpr int kFreqTable = 1024;
+
+// Fills f[0, min(half, kFreqTable)); every thread of the workgroup must call it.
+__device__ inline void fill_freqs(float* f, int half, int D, float theta) {
+  for (int i = threadIdx.x; i < half && i < kFreqTable; i += blockDim.x) f[i] = inv_freq(i, D, theta);
+  __syncthreads();
+}
+
 // cos / sin of pair i at position p (accurate library sin / cos of the float angle).
-__device__ inline void pair_angle(int p, int i, int D, float theta, float& c, float& s) {
-  const float f = (float)(1.0 / pow((double)theta, (double)(2 * i) / (double)D));
-  const float ang = (float)p * f;
+__device__ inline void pair_angle(const float* f, int p, int i, int D, float theta, float& c,
+                                  float& s) {
+  const float fi = i < kFreqTable ? f[i] : inv_freq(i, D, theta);
+  const float ang = (float)p * fi;
   sincosf(ang, &s, &c);
 }
 
@@ -42,21 +59,23 @@ template <typename E>
 __global__ __launch_bounds__(256) void rope_kernel(E* x, int64_t ts, int64_t hs,
                                                    const int32_t* pos, int n_tok, int H, int D,
                                                    float theta) {
+  __shared__ float s_freq[kFreqTable];
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int half = D / 2;
+  fill_freqs(s_freq, half, D, theta);
   if (gid >= (int64_t)n_tok * H * half) return;
   const int i = (int)(gid % half);
   const int64_t th = gid / half;
   const int h = (int)(th % H);
   const int64_t t = th / H;
   float c, s;
-  pair_angle(pos[t], i, D, theta, c, s);
+  pair_angle(s_freq, pos[t], i, D, theta, c, s);
   E* row = x + t * ts + h * hs;
   rotate_pair(row[2 * i], row[2 * i + 1], c, s);
 }
 
-// Paged append with K rotated: one thread per (token, kv head, 16-byte chunk) as
-// ivakv_append, the chunk's pairs rotated before the store.
+// Paged append with K rotated: one thread per (token, group of up to four kv heads,
+// 16-byte chunk), the chunk's pairs rotated before the store.
 struct AppendRopeArgs {
   const void* k_new;
   const void* v_new;
@@ -70,45 +89,67 @@ struct AppendRopeArgs {
   float theta;
 };
 
+// Lanes rotate up to kRopeHeads kv heads of one (token, chunk): cos / sin depend on the
+// position and the pair only, so they are computed once per lane, not once per head.
+constexpr int kRopeHeads = 4;
+
 template <typename E>
 __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
   constexpr int X = 16 / sizeof(E);
   const int nch = a.D / X;
-  // Thread order (token % 16, chunk, head, token / 16), as in append_kernel: 16
-  // consecutive tokens (consecutive slots of a page in a chunk append) per lane
-  // group, so K and V stores coalesce.
+  const int ngrp = cdiv(a.Hkv, kRopeHeads);
+  // Thread order (token % 16, chunk, head group, token / 16), as in append_kernel: 16
+  // consecutive tokens (consecutive slots of a page in a chunk append) per lane group,
+  // so K and V stores coalesce.
+  __shared__ float s_freq[kFreqTable];
+  fill_freqs(s_freq, a.D / 2, a.D, a.theta);
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (int64_t)cdiv(a.n_tok, 16) * 16 * a.Hkv * nch) return;
+  if (gid >= (int64_t)cdiv(a.n_tok, 16) * 16 * ngrp * nch) return;
   const int t_lo = (int)(gid & 15);
   const int64_t g1 = gid >> 4;
   const int c = (int)(g1 % nch);
   const int64_t g2 = g1 / nch;
-  const int h = (int)(g2 % a.Hkv);
-  const int64_t t = (g2 / a.Hkv) * 16 + t_lo;
+  const int h0 = (int)(g2 % ngrp) * kRopeHeads;
+  const int64_t t = (g2 / ngrp) * 16 + t_lo;
   if (t >= a.n_tok) return;
   const int64_t slot = a.slots[t];
   if (slot < 0 || slot >= a.n_slots) return;
   const int64_t page = slot / a.bs;
   const int off = (int)(slot - page * a.bs);
-  const int64_t head_base = page * a.Hkv + h;
-  const E* ks = static_cast<const E*>(a.k_new) + t * a.kts + h * a.khs + (int64_t)c * X;
-  const E* vs = static_cast<const E*>(a.v_new) + t * a.vts + h * a.vhs + (int64_t)c * X;
-  E k[X];
+  const int nh = min(kRopeHeads, a.Hkv - h0);
+  const E* __restrict__ kb = static_cast<const E*>(a.k_new) + t * a.kts + (int64_t)c * X;
+  const E* __restrict__ vb = static_cast<const E*>(a.v_new) + t * a.vts + (int64_t)c * X;
+  E* __restrict__ kp = static_cast<E*>(a.k_pool);
+  E* __restrict__ vp = static_cast<E*>(a.v_pool);
+  E k[kRopeHeads][X], v[kRopeHeads][X];
 #pragma unroll
-  for (int j = 0; j < X; ++j) k[j] = ks[j];
-  const int p = a.pos[t];
+  for (int u = 0; u < kRopeHeads; ++u) {
+    if (u < nh) {
 #pragma unroll
-  for (int j = 0; j < X; j += 2) {
-    float cs, sn;
-    pair_angle(p, (c * X + j) / 2, a.D, a.theta, cs, sn);
-    rotate_pair(k[j], k[j + 1], cs, sn);
+      for (int j = 0; j < X; ++j) {
+        k[u][j] = kb[(h0 + u) * a.khs + j];
+        v[u][j] = vb[(h0 + u) * a.vhs + j];
+      }
+    }
   }
-  E* kd = static_cast<E*>(a.k_pool) + ((head_base * nch + c) * a.bs + off) * X;
-  E* vd = static_cast<E*>(a.v_pool) + head_base * a.D * a.bs + (int64_t)c * X * a.bs + off;
+  const int p = a.pos[t];
+  float cs[X / 2], sn[X / 2];
 #pragma unroll
-  for (int j = 0; j < X; ++j) {
-    kd[j] = k[j];
-    vd[(int64_t)j * a.bs] = vs[j];
+  for (int j = 0; j < X / 2; ++j) pair_angle(s_freq, p, c * (X / 2) + j, a.D, a.theta, cs[j], sn[j]);
+#pragma unroll
+  for (int u = 0; u < kRopeHeads; ++u) {
+    if (u < nh) {
+#pragma unroll
+      for (int j = 0; j < X / 2; ++j) rotate_pair(k[u][2 * j], k[u][2 * j + 1], cs[j], sn[j]);
+      const int64_t head_base = page * a.Hkv + h0 + u;
+      E* kd = kp + ((head_base * nch + c) * a.bs + off) * X;
+      E* vd = vp + head_base * a.D * a.bs + (int64_t)c * X * a.bs + off;
+#pragma unroll
+      for (int j = 0; j < X; ++j) {
+        kd[j] = k[u][j];
+        vd[(int64_t)j * a.bs] = v[u][j];
+      }
+    }
   }
 }
 
@@ -192,7 +233,7 @@ extern "C" int ivakv_append_rope(const void* k_new, const void* v_new, int64_t k
   AppendRopeArgs a{k_new, v_new, k_tok_stride, k_head_stride, v_tok_stride, v_head_stride,
                    k_pool, v_pool, slot_mapping, positions, n_tok, num_kv_heads, head_dim,
                    block_size, (int64_t)num_pages * block_size, theta};
-  const int64_t total = (int64_t)cdiv(n_tok, 16) * 16 * num_kv_heads * (head_dim / X);
+  const int64_t total = (int64_t)cdiv(n_tok, 16) * 16 * cdiv(num_kv_heads, kRopeHeads) * (head_dim / X);
   const int64_t blocks = (total + 255) / 256;
   if (blocks > kMaxGridR) return fail(IVAKV_E_SHAPE, "%s: too many rows", name);
   switch (dtype) {

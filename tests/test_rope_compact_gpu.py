@@ -50,26 +50,39 @@ def test_rope_in_place_vs_oracle(iva, dev, dtype, d):
     assert torch.equal(y[0].cpu(), x[0])                           # position 0: identity
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
-def test_append_rope_vs_oracle(iva, dev, dtype):
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("hkv,d", [(8, 64), (3, 128), (5, 64), (1, 128), (6, 256)])
+def test_append_rope_vs_oracle(iva, dev, dtype, hkv, d):
+    """Lanes rotate groups of up to four kv heads: head counts that are not a multiple
+    of four leave a partial last group.  A row with slot -1 and one past the pool are
+    skipped (pools keep the fill value)."""
     lengths = [7, 33, 20]
-    c = iva.workloads.c1_append_gather(seed=2, dtype=dtype)
     lay = iva.workloads.permuted_layout(lengths, 12, torch.Generator().manual_seed(3))
     n = sum(lengths)
-    k_new, v_new = c["k_new"][:n], c["v_new"][:n]
+    gen = torch.Generator().manual_seed(2 + hkv)
+    k_new = torch.randn(n, hkv, d, generator=gen).to(dtype)
+    v_new = torch.randn(n, hkv, d, generator=gen).to(dtype)
     slots = torch.cat([lay.slots(b, torch.arange(m)) for b, m in enumerate(lengths)])
+    slots[5], slots[40] = -1, 12 * 16 + 3
     positions = torch.cat([torch.arange(m) + 1000 * b for b, m in enumerate(lengths)]).to(torch.int32)
-    ks, vs = iva.pool_shapes(12, 8, 64, 16, dtype)
+    ks, vs = iva.pool_shapes(12, hkv, d, 16, dtype)
     kp = torch.full(ks, 3.0, dtype=dtype, device=dev)
     vp = torch.full(vs, 3.0, dtype=dtype, device=dev)
     iva.kv_append(k_new.to(dev), v_new.to(dev), kp, vp, slots.to(dev),
                   rope_positions=positions.to(dev), rope_theta=10000.0)
     # expected pools: the oracle append of the rotated K rows (rounded once), V as is
     k_rot = orc.rope(k_new.float().numpy(), positions.numpy(), 10000.0)
-    ek = np.full(ks, 3.0)  # fp64 values in the pools' fp16 / bf16 layout
+    ek = np.full(ks, 3.0)  # fp64 values in the pools' layout
     ev = np.full(vs, 3.0)
     orc.append(ek, ev, k_rot, v_new.float().numpy(), slots.numpy())
-    assert ulp_diff(kp, ek, dtype) <= 1
+    if dtype == torch.float32:  # 4 ulp of the pair's magnitude, as for ivakv_rope
+        kn = k_new.numpy()
+        mag = np.full(ks, 0.0)
+        orc.append(mag, np.full(vs, 0.0), np.repeat(np.hypot(kn[..., 0::2], kn[..., 1::2]), 2, -1),
+                   v_new.numpy(), slots.numpy())
+        assert (np.abs(kp.cpu().numpy() - ek) <= 4 * 2.0 ** -23 * mag + 1e-30).all()
+    else:
+        assert ulp_diff(kp, ek, dtype) <= 1
     assert torch.equal(vp.cpu(), torch.from_numpy(ev).to(dtype))
 
 
