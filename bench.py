@@ -650,10 +650,10 @@ def measure_decode(args, iva, torch, dev, lengths):
 
 def bench_ops(args, iva, torch, dev):
     """The hot path's data-movement kernels at realistic sizes (fp16, 8 kv heads, D 128),
-    each as average time over back-to-back launches on one stream: the append of
+    each as average time over back-to-back launches captured in one HIP graph: the append of
     16 x 512-token chunks (8192 rows; plain and with RoPE fused), the gather of the C2
-    batch into contiguous K/V, the kv_ops index gather / scatter on a [32, 8, 4096, 128]
-    cache, and the compaction's page moves (4096 pages).  Bytes are what each op must
+    batch into contiguous K/V, the kv_ops index gather / scatter kernels on a [32, 8, 4096,
+    128] cache, and the compaction's page moves (4096 pages).  Bytes are what each op must
     read and write; GB/s against the 8 TB/s HBM peak."""
     wl = iva.workloads
     hkv, d, es = 8, 128, 2
@@ -661,15 +661,23 @@ def bench_ops(args, iva, torch, dev):
     out = {}
 
     def timed(name, fn, nbytes, reps=50):
+        # reps launches captured in one HIP graph: the replay times the device work, not
+        # the Python validation and allocation around each call
         for _ in range(3):
             fn()
         torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize(dev)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(reps):
-            fn()
+        graph.replay()
         e1.record()
         torch.cuda.synchronize(dev)
+        del graph
         us = e0.elapsed_time(e1) * 1e3 / reps
         gbs = nbytes / (us * 1e-6) / 1e9
         out[name] = {"us": round(us, 2), "bytes": int(nbytes), "gbps": round(gbs, 1),
@@ -708,19 +716,30 @@ def bench_ops(args, iva, torch, dev):
                                           out=(kg, vg)),
           2 * sum(lengths) * hkv * d * es + 2 * kg.numel() * es)
     del dd, kg, vg
-    # kv_ops on a contiguous cache: gather 1024 positions, scatter 1024 rows (the op
-    # returns a new cache: a full copy plus the scattered rows)
+    # kv_ops' index kernels on a contiguous cache: gather 1024 positions, scatter 1024
+    # rows, through the C ABI on preallocated buffers (kv_ops itself checks the indices
+    # on the host, a synchronisation per call, and its scatter copies the whole cache
+    # first, a torch copy)
     cache = torch.randn(32, hkv, 4096, d, generator=gen, device=dev).half()
     idx = torch.randperm(4096, generator=torch.Generator().manual_seed(5))[:1024].to(dev)
     vals = torch.randn(32, hkv, 1024, d, generator=gen, device=dev).half()
+    gout = torch.empty_like(vals)
+    code = iva.dtype_code(torch.float16)
     rows = 32 * hkv * 1024 * d * es
-    timed("kv_ops_gather", lambda: iva.kv_ops(cache, idx, operation="gather"), 2 * rows, reps=20)
-    timed("kv_ops_scatter", lambda: iva.kv_ops(cache, idx, vals, operation="scatter"),
-          2 * cache.numel() * es + 2 * rows, reps=20)
+
+    def stream():
+        return torch.cuda.current_stream(dev).cuda_stream
+
+    timed("index_gather", lambda: iva._abi.call(
+        "ivakv_index_gather", cache.data_ptr(), *cache.stride(), idx.data_ptr(), 1024, 32, hkv,
+        4096, d, gout.data_ptr(), code, stream()), 2 * rows + 8 * 1024)
+    timed("index_scatter", lambda: iva._abi.call(
+        "ivakv_index_scatter", cache.data_ptr(), *cache.stride(), idx.data_ptr(), 1024,
+        vals.data_ptr(), *vals.stride(), 32, hkv, 4096, d, code, stream()), 2 * rows + 8 * 1024)
     return {"metric": "hot-path data-movement kernels GB/s (fraction of 8 TB/s HBM)",
             "workload": "ops", "dtype": "f16", "data": "synthetic",
             "config": {"num_kv_heads": hkv, "head_dim": d, "block_size": 16,
-                       "launch": "eager, back-to-back on one stream"},
+                       "launch": "hip graph of back-to-back launches"},
             "kernels": out}
 
 
