@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define IVAKV_ABI_VERSION 1
+#define IVAKV_ABI_VERSION 2
 
 /* status codes */
 #define IVAKV_OK            0
@@ -280,15 +280,16 @@ int ivakv_append_rope(const void* k_new, const void* v_new, int64_t k_tok_stride
                       int block_size, int num_pages, float theta, int dtype, hipStream_t stream);
 /*
  * ivakv_copy_pages: page moves src_pages[i] -> dst_pages[i] (int32, n_moves <= 65535) of a
- * pool pair, K and V tiles of every kv head (elem_bytes 1, 2 or 4), plus the FP8 scaling
- * factors when k_scale / v_scale are given (both or neither).  The source and destination
- * sets must be disjoint.  Used by pool compaction (PagedKVPool.compact), the paged
- * counterpart of kv_compact_triton (src/kernels_t/kv_ops_triton.py:68-92,159-181).
+ * pool pair of num_pages pages, K and V tiles of every kv head (elem_bytes 1, 2 or 4), plus
+ * the FP8 scaling factors when k_scale / v_scale are given (both or neither).  The source
+ * and destination sets must be disjoint.  A move whose source or destination id lies
+ * outside [0, num_pages) is skipped.  Used by pool compaction (PagedKVPool.compact), the
+ * paged counterpart of kv_compact_triton (src/kernels_t/kv_ops_triton.py:68-92,159-181).
  */
 int ivakv_copy_pages(void* k_pool, void* v_pool, float* k_scale, float* v_scale,
                      const int32_t* src_pages, const int32_t* dst_pages, int n_moves,
-                     int num_kv_heads, int head_dim, int block_size, int elem_bytes,
-                     hipStream_t stream);
+                     int num_pages, int num_kv_heads, int head_dim, int block_size,
+                     int elem_bytes, hipStream_t stream);
 
 /*
  * Paged multi-query causal attention (prefill / chunked prefill).  Sequence b owns
@@ -300,17 +301,20 @@ int ivakv_copy_pages(void* k_pool, void* v_pool, float* k_scale, float* v_scale,
  * over valid page ids; out has q's shape.  A row at a negative position (n_b > L)
  * and a row that sees no key are written as zeros.  max_query_len must be >= every
  * n_b (rows past it are not computed).  query_start is int32 [batch+1], non-
- * decreasing.  Geometry: head_dim in {64, 128, 256}, block_size 16, any GQA group.
+ * decreasing, query_start[0] = 0 and query_start[batch] <= n_tok (the rows of q and
+ * out).  The kernel reads it from device memory and skips (writes nothing for) a
+ * sequence whose rows [query_start[b], query_start[b+1]) do not lie in [0, n_tok).
+ * Geometry: head_dim in {64, 128, 256}, block_size 16, any GQA group.
  * Replaces: AttentionTorch.forward with a cache and seq_len > 1
  * (src/core/attention.py:61-102): torch.cat of the chunk's K/V, scores, causal /
  * window / sink masks (attention.py:79-93,115-148) at absolute positions, softmax, PV.
  */
 int ivakv_prefill_attn(const void* q, const void* k_pool, const void* v_pool,
                        const int32_t* block_tables, const int32_t* context_lens,
-                       const int32_t* query_start, void* out, int batch, int num_q_heads,
-                       int num_kv_heads, int head_dim, int block_size, int max_blocks,
-                       int num_pages, int max_query_len, float scale, int window, int n_sink,
-                       int dtype, hipStream_t stream);
+                       const int32_t* query_start, int n_tok, void* out, int batch,
+                       int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                       int max_blocks, int num_pages, int max_query_len, float scale,
+                       int window, int n_sink, int dtype, hipStream_t stream);
 
 /*
  * ivakv_prefill_attn_fp8: ivakv_prefill_attn over FP8 pools (layout and factors as
@@ -323,10 +327,10 @@ int ivakv_prefill_attn(const void* q, const void* k_pool, const void* v_pool,
 int ivakv_prefill_attn_fp8(const void* q, const void* k_pool, const void* v_pool,
                            const float* k_scale, const float* v_scale,
                            const int32_t* block_tables, const int32_t* context_lens,
-                           const int32_t* query_start, void* out, int batch, int num_q_heads,
-                           int num_kv_heads, int head_dim, int block_size, int max_blocks,
-                           int num_pages, int max_query_len, float scale, int window,
-                           int n_sink, int dtype, hipStream_t stream);
+                           const int32_t* query_start, int n_tok, void* out, int batch,
+                           int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                           int max_blocks, int num_pages, int max_query_len, float scale,
+                           int window, int n_sink, int dtype, hipStream_t stream);
 
 /*
  * Index gather on a contiguous-layout cache kv = [batch][n_heads][seq_len][D]

@@ -18,6 +18,7 @@ from .ops import (
     kv_compact,
     kv_gather,
     kv_ops,
+    KVOps,
     paged_decode_append_attention,
     paged_decode_attention,
     paged_decode_attention_merge,
@@ -48,6 +49,7 @@ __all__ = [
     "kv_compact",
     "kv_gather",
     "kv_ops",
+    "KVOps",
     "paged_decode_append_attention",
     "paged_decode_attention",
     "paged_decode_attention_merge",

@@ -16,7 +16,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p, POINTER
 from pathlib import Path
 from typing import Optional
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK = 0
 E_ARG = -1
@@ -117,14 +117,14 @@ SIGNATURES = {
     ]),
     "ivakv_copy_pages": (c_int, [
         c_void_p, c_void_p, c_void_p, c_void_p,  # k_pool, v_pool, k_scale, v_scale
-        c_void_p, c_void_p, c_int,             # src_pages, dst_pages, n_moves
+        c_void_p, c_void_p, c_int, c_int,      # src_pages, dst_pages, n_moves, num_pages
         c_int, c_int, c_int, c_int, c_void_p,  # Hkv, D, block_size, elem_bytes, stream
     ]),
     "ivakv_prefill_attn_fp8": (c_int, [
         c_void_p, c_void_p, c_void_p,          # q, k_pool, v_pool
         c_void_p, c_void_p,                    # k_scale, v_scale
         c_void_p, c_void_p, c_void_p,          # block_tables, context_lens, query_start
-        c_void_p,                              # out
+        c_int, c_void_p,                       # n_tok, out
         c_int, c_int, c_int, c_int,            # batch, num_q_heads, num_kv_heads, head_dim
         c_int, c_int, c_int, c_int, c_float,   # block_size, max_blocks, num_pages, max_query_len, scale
         c_int, c_int, c_int,                   # window, n_sink, dtype
@@ -133,7 +133,7 @@ SIGNATURES = {
     "ivakv_prefill_attn": (c_int, [
         c_void_p, c_void_p, c_void_p,          # q, k_pool, v_pool
         c_void_p, c_void_p, c_void_p,          # block_tables, context_lens, query_start
-        c_void_p,                              # out
+        c_int, c_void_p,                       # n_tok, out
         c_int, c_int, c_int, c_int,            # batch, num_q_heads, num_kv_heads, head_dim
         c_int, c_int, c_int, c_int, c_float,   # block_size, max_blocks, num_pages, max_query_len, scale
         c_int, c_int, c_int,                   # window, n_sink, dtype

@@ -44,6 +44,7 @@ struct PrefillArgs {
   const void* k_pool;
   const void* v_pool;
   void* out;      // like q
+  int n_tok;      // rows of q and out
   int batch, Hkv, G, max_blocks, num_pages;
   float scale_log2;
   int window, n_sink;
@@ -60,22 +61,10 @@ struct PrefillArgs {
 template <int DT, int D>
 struct PrefillShape {
   static constexpr int kESize = DT == IVAKV_F32 ? 4 : 2;
-#ifdef IVAKV_PF_WAVES
-  static constexpr int kWaves = (DT == IVAKV_F32 || D == 256) ? 4 : IVAKV_PF_WAVES;
-#else
   static constexpr int kWaves = (DT == IVAKV_F32 || D == 256) ? 4 : 8;
-#endif
   static constexpr int kThreads = 64 * kWaves;
-#ifdef IVAKV_PF_NR
-  static constexpr int NR = (DT == IVAKV_F32 || D == 256) ? 2 : IVAKV_PF_NR;
-#else
   static constexpr int NR = 2;
-#endif
-#ifdef IVAKV_PF_STAGES
-  static constexpr int kStages = (DT == IVAKV_F32 || D == 256) ? 1 : IVAKV_PF_STAGES;
-#else
   static constexpr int kStages = kWaves == 8 ? 2 : 1;  // pairs in flight in registers
-#endif
   static constexpr int kRowsWave = 16 * NR;
   static constexpr int kRowsWG = kRowsWave * kWaves;
   static constexpr int kPageElems = kBS * D;          // one K or V page tile
@@ -113,8 +102,12 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   const int lane = tid & 63, ln = lane & 15, lq = lane >> 4;
   const int wave = uni(tid >> 6);
   const int G = a.G, Hkv = a.Hkv, Hq = Hkv * G;
-  const int q0 = qstart[b];
-  const int n = qstart[b + 1] - q0;
+  // The sequence's rows [q0, q1) must lie inside q / out; a range that does not is
+  // skipped (its rows are not written).
+  const int64_t q0l = qstart[b], q1l = qstart[b + 1];
+  if (q0l < 0 || q1l <= q0l || q1l > a.n_tok) return;  // uniform over the workgroup
+  const int q0 = (int)q0l;
+  const int n = (int)(q1l - q0l);
   const int L = ctx[b];
   const int rows = n * G;
   const int r_wg = xb * S::kRowsWG;
@@ -645,16 +638,18 @@ int rows_per_workgroup(int dtype, int head_dim) {
 
 int prefill_entry(const char* name, const void* q, const void* k_pool, const void* v_pool,
                   const float* k_scale, const float* v_scale, const int32_t* block_tables,
-                  const int32_t* context_lens, const int32_t* query_start, void* out, int batch,
-                  int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                  const int32_t* context_lens, const int32_t* query_start, int n_tok, void* out,
+                  int batch, int num_q_heads, int num_kv_heads, int head_dim, int block_size,
                   int max_blocks, int num_pages, int max_query_len, float scale, int window,
                   int n_sink, int dtype, hipStream_t stream, bool fp8) {
   if (dtype_size(dtype) == 0) return fail(IVAKV_E_DTYPE, "%s: unknown dtype code %d", name, dtype);
   if (fp8 && dtype != IVAKV_F16 && dtype != IVAKV_BF16)
     return fail(IVAKV_E_DTYPE, "%s: FP8 pools take fp16 or bf16 queries (dtype %d)", name, dtype);
-  if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_blocks < 0 || max_query_len < 0)
-    return fail(IVAKV_E_ARG, "%s: bad sizes B=%d Hq=%d Hkv=%d max_blocks=%d max_query_len=%d",
-                name, batch, num_q_heads, num_kv_heads, max_blocks, max_query_len);
+  if (batch < 0 || n_tok < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_blocks < 0 ||
+      max_query_len < 0)
+    return fail(IVAKV_E_ARG,
+                "%s: bad sizes B=%d n_tok=%d Hq=%d Hkv=%d max_blocks=%d max_query_len=%d", name,
+                batch, n_tok, num_q_heads, num_kv_heads, max_blocks, max_query_len);
   if (num_q_heads % num_kv_heads != 0)
     return fail(IVAKV_E_SHAPE, "%s: num_q_heads %d not a multiple of num_kv_heads %d", name,
                 num_q_heads, num_kv_heads);
@@ -663,7 +658,7 @@ int prefill_entry(const char* name, const void* q, const void* k_pool, const voi
   if (block_size != kBS)
     return fail(IVAKV_E_SHAPE, "%s: block_size %d != %d", name, block_size, kBS);
   if (n_sink < 0) return fail(IVAKV_E_ARG, "%s: negative n_sink", name);
-  if (batch == 0 || max_query_len == 0) return IVAKV_OK;
+  if (batch == 0 || max_query_len == 0 || n_tok == 0) return IVAKV_OK;
   if (num_pages < 1) return fail(IVAKV_E_ARG, "%s: num_pages must be >= 1", name);
   if (!q || !k_pool || !v_pool || !context_lens || !query_start || !out ||
       (max_blocks > 0 && !block_tables))
@@ -684,6 +679,7 @@ int prefill_entry(const char* name, const void* q, const void* k_pool, const voi
   a.k_pool = k_pool;
   a.v_pool = v_pool;
   a.out = out;
+  a.n_tok = n_tok;
   a.batch = batch;
   a.Hkv = num_kv_heads;
   a.G = G;
@@ -720,12 +716,12 @@ using namespace ivakv;
 
 extern "C" int ivakv_prefill_attn(const void* q, const void* k_pool, const void* v_pool,
                                   const int32_t* block_tables, const int32_t* context_lens,
-                                  const int32_t* query_start, void* out, int batch,
+                                  const int32_t* query_start, int n_tok, void* out, int batch,
                                   int num_q_heads, int num_kv_heads, int head_dim, int block_size,
                                   int max_blocks, int num_pages, int max_query_len, float scale,
                                   int window, int n_sink, int dtype, hipStream_t stream) {
   return prefill_entry("ivakv_prefill_attn", q, k_pool, v_pool, nullptr, nullptr, block_tables,
-                       context_lens, query_start, out, batch, num_q_heads, num_kv_heads,
+                       context_lens, query_start, n_tok, out, batch, num_q_heads, num_kv_heads,
                        head_dim, block_size, max_blocks, num_pages, max_query_len, scale, window,
                        n_sink, dtype, stream, false);
 }
@@ -733,13 +729,13 @@ extern "C" int ivakv_prefill_attn(const void* q, const void* k_pool, const void*
 extern "C" int ivakv_prefill_attn_fp8(const void* q, const void* k_pool, const void* v_pool,
                                       const float* k_scale, const float* v_scale,
                                       const int32_t* block_tables, const int32_t* context_lens,
-                                      const int32_t* query_start, void* out, int batch,
-                                      int num_q_heads, int num_kv_heads, int head_dim,
+                                      const int32_t* query_start, int n_tok, void* out,
+                                      int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                       int block_size, int max_blocks, int num_pages,
                                       int max_query_len, float scale, int window, int n_sink,
                                       int dtype, hipStream_t stream) {
   return prefill_entry("ivakv_prefill_attn_fp8", q, k_pool, v_pool, k_scale, v_scale,
-                       block_tables, context_lens, query_start, out, batch, num_q_heads,
+                       block_tables, context_lens, query_start, n_tok, out, batch, num_q_heads,
                        num_kv_heads, head_dim, block_size, max_blocks, num_pages, max_query_len,
                        scale, window, n_sink, dtype, stream, true);
 }

@@ -155,12 +155,15 @@ __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
 
 // Page moves: page src[i] -> dst[i] of every pool tensor (K and V tiles of all kv
 // heads, and the FP8 scaling factors when given).  Grid (chunk block, move), 16
-// bytes per thread.
+// bytes per thread.  A move whose source or destination id lies outside
+// [0, num_pages) is skipped.
 __global__ __launch_bounds__(256) void copy_pages_kernel(Chunk16* k, Chunk16* v, Chunk16* ks,
                                                          Chunk16* vs, const int32_t* src,
-                                                         const int32_t* dst, int64_t page_chunks,
+                                                         const int32_t* dst, int num_pages,
+                                                         int64_t page_chunks,
                                                          int64_t scale_chunks) {
   const int64_t s = src[blockIdx.y], d = dst[blockIdx.y];
+  if (s < 0 || s >= num_pages || d < 0 || d >= num_pages) return;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < page_chunks;
        i += (int64_t)gridDim.x * blockDim.x) {
     k[d * page_chunks + i] = k[s * page_chunks + i];
@@ -246,13 +249,14 @@ extern "C" int ivakv_append_rope(const void* k_new, const void* v_new, int64_t k
 
 extern "C" int ivakv_copy_pages(void* k_pool, void* v_pool, float* k_scale, float* v_scale,
                                 const int32_t* src_pages, const int32_t* dst_pages, int n_moves,
-                                int num_kv_heads, int head_dim, int block_size, int elem_bytes,
-                                hipStream_t stream) {
+                                int num_pages, int num_kv_heads, int head_dim, int block_size,
+                                int elem_bytes, hipStream_t stream) {
   static const char* name = "ivakv_copy_pages";
-  if (n_moves < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
+  if (n_moves < 0 || num_pages < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
       (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4))
-    return fail(IVAKV_E_ARG, "%s: bad sizes moves=%d Hkv=%d D=%d block_size=%d elem_bytes=%d",
-                name, n_moves, num_kv_heads, head_dim, block_size, elem_bytes);
+    return fail(IVAKV_E_ARG,
+                "%s: bad sizes moves=%d pages=%d Hkv=%d D=%d block_size=%d elem_bytes=%d", name,
+                n_moves, num_pages, num_kv_heads, head_dim, block_size, elem_bytes);
   const int64_t page_bytes = (int64_t)num_kv_heads * head_dim * block_size * elem_bytes;
   const int64_t scale_bytes = (int64_t)num_kv_heads * block_size * 4;
   if (page_bytes % 16 || (k_scale && scale_bytes % 16))
@@ -269,6 +273,6 @@ extern "C" int ivakv_copy_pages(void* k_pool, void* v_pool, float* k_scale, floa
   copy_pages_kernel<<<dim3(bx, (unsigned)n_moves), 256, 0, stream>>>(
       static_cast<Chunk16*>(k_pool), static_cast<Chunk16*>(v_pool),
       reinterpret_cast<Chunk16*>(k_scale), reinterpret_cast<Chunk16*>(v_scale), src_pages,
-      dst_pages, chunks, k_scale ? scale_bytes / 16 : 0);
+      dst_pages, num_pages, chunks, k_scale ? scale_bytes / 16 : 0);
   return launch_status(name);
 }

@@ -15,8 +15,9 @@ meaning, return contracts, errors) for the path ``Transformer.forward(kv_cache=.
   PagedAttention      same constructor/forward contract (:37-45,110) on a PagedKVCache:
                       single-token decode appends and attends in one op
                       (ivakv_decode_append_attn); multi-token (prefill) steps append
-                      with ivakv_append, gather the context (ivakv_gather) and evaluate
-                      the masked attention.
+                      with ivakv_append and run ivakv_prefill_attn.  Builds from the
+                      reference's own TransformerConfig (fields it lacks take their
+                      defaults) and takes over the reference's contiguous KVCache.
   KVCache             src/core/rope_kv.py:71-137 (contiguous cache of AttentionTorch).
   RMSNorm / FFN       src/core/norms.py:14-36, src/core/ffn.py:16-64 (needed by the
                       dense decoder of config C3; not part of the paged hot path).
@@ -49,9 +50,18 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .ops import (kv_gather, paged_decode_append_attention,
+from .ops import (FP8, kv_gather, paged_decode_append_attention,
                   paged_prefill_attention, rope_)
 from .paged_cache import PagedKVCache
+
+
+def _cfg(config: Any, name: str, default: Any) -> Any:
+    """A field of the paged backend that the reference's TransformerConfig
+    (src/core/transformer.py:25-78) does not have: read with its default, so every module
+    here builds from the reference config unchanged (n_kv_heads = n_heads, no sinks, no
+    RoPE inside attention, pages of 16 in the model dtype)."""
+    value = getattr(config, name, None)
+    return default if value is None else value
 
 
 @dataclass
@@ -234,10 +244,14 @@ class _AttentionBase(nn.Module):
         self.config = config
         self.d_model = config.d_model
         self.n_heads = config.n_heads
-        self.n_kv_heads = config.n_kv_heads
+        self.n_kv_heads = int(_cfg(config, "n_kv_heads", config.n_heads))
+        if self.n_heads % self.n_kv_heads:
+            raise ValueError(f"n_heads ({self.n_heads}) must be a multiple of n_kv_heads "
+                             f"({self.n_kv_heads})")
         self.head_dim = config.d_model // config.n_heads
         self.dropout = config.dropout
         self.causal = config.causal
+        self.sink_tokens = int(_cfg(config, "sink_tokens", 0))
         kv_dim = self.n_kv_heads * self.head_dim
         self.q_proj = nn.Linear(self.d_model, self.d_model, bias=False)
         self.k_proj = nn.Linear(self.d_model, kv_dim, bias=False)
@@ -245,7 +259,7 @@ class _AttentionBase(nn.Module):
         self.o_proj = nn.Linear(self.d_model, self.d_model, bias=False)
         self.dropout_layer = nn.Dropout(self.dropout)
         self.scale = 1.0 / math.sqrt(self.head_dim)
-        self.rope = bool(config.rope_in_attention)
+        self.rope = bool(_cfg(config, "rope_in_attention", False))
         self.rope_theta = float(config.rope_theta)
 
     def _project(self, x):
@@ -300,7 +314,7 @@ class AttentionTorch(_AttentionBase):
         q_pos = torch.arange(start, start + s, device=x.device)
         k_pos = torch.arange(k.shape[2], device=x.device)
         if self.causal:
-            allowed = _visible(q_pos, k_pos, sliding_window, _sink_count(sink_cfg, self.config.sink_tokens))
+            allowed = _visible(q_pos, k_pos, sliding_window, _sink_count(sink_cfg, self.sink_tokens))
         else:
             allowed = torch.ones(s, k.shape[2], dtype=torch.bool, device=x.device)
         out = _attend(q, k, v, self.scale, allowed[None, None])
@@ -317,7 +331,11 @@ class PagedAttention(_AttentionBase):
     new row and attends over the pages in one op (ivakv_decode_append_attn); a
     multi-token step (prefill / chunked prefill) appends with ivakv_append and runs
     the causal attention of the new tokens over the pages (ivakv_prefill_attn).
-    Without a cache the new tokens attend to themselves (causal).
+    A contiguous ``KVCache`` is taken over as a PagedKVCache (:meth:`_adopt`), which is
+    returned in its place.  Without a cache a causal step runs the same kernels on a
+    one-layer paged cache of its own tokens, and None is returned, as the reference
+    returns (attention.py:74-75).  Non-causal attention (``config.causal`` False) is
+    evaluated in torch on the gathered pages: the paged kernels are causal.
     """
 
     def forward(self, x: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
@@ -327,12 +345,15 @@ class PagedAttention(_AttentionBase):
         if self.training and self.dropout > 0:
             raise NotImplementedError("the paged attention path is for inference (model.eval())")
         if kv_cache is not None and not isinstance(kv_cache, PagedKVCache):
-            raise TypeError("attn_impl='hip_paged' needs a PagedKVCache "
-                            f"(got {type(kv_cache).__name__})")
+            kv_cache = self._adopt(kv_cache, x)
         self._check_mask(attention_mask)
         b, s, _ = x.shape
+        returned = kv_cache
+        if kv_cache is None and self.causal:
+            kv_cache = PagedKVCache(b, self.n_kv_heads, self.head_dim, 0, x.device, x.dtype,
+                                    num_layers=1, max_seq_len=s)
         q, k, v = self._project(x)
-        n_sink = _sink_count(sink_cfg, self.config.sink_tokens)
+        n_sink = _sink_count(sink_cfg, self.sink_tokens)
         window = sliding_window if sliding_window and sliding_window > 0 else None
         rope_pos = None  # K rows rotated inside the append instead of separately
         if self.rope:
@@ -344,10 +365,8 @@ class PagedAttention(_AttentionBase):
                 rope_(k.reshape(b * s, self.n_kv_heads, self.head_dim), pos, self.rope_theta)
             else:
                 rope_pos = pos
-        if kv_cache is None:
-            qp = torch.arange(s, device=x.device)
-            allowed = _visible(qp, qp, window, n_sink) if self.causal else \
-                torch.ones(s, s, dtype=torch.bool, device=x.device)
+        if kv_cache is None:  # non-causal without a cache
+            allowed = torch.ones(s, s, dtype=torch.bool, device=x.device)
             out = _attend(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), self.scale,
                           allowed[None, None])
             out = out.transpose(1, 2)
@@ -390,15 +409,53 @@ class PagedAttention(_AttentionBase):
                 out = _attend(q.transpose(1, 2), kc, vc, self.scale, allowed[None, None])
                 out = out.transpose(1, 2)
         out = out.reshape(b, s, self.d_model)
-        return self.o_proj(out), kv_cache
+        return self.o_proj(out), (kv_cache if returned is not None else None)
+
+    def _adopt(self, cache: Any, x: torch.Tensor) -> PagedKVCache:
+        """Takes over a contiguous cache (the reference's ``KVCache``, src/core/rope_kv.py:
+        71-137: ``k`` / ``v`` of ``[B, H, seq_len, D]``), as the reference's
+        ``Transformer.generate`` passes one: a new ``KVCache(seq_len=0)`` whose whole
+        sequence is fed again on every step (transformer.py:273-290).
+
+        Returns a PagedKVCache with one layer per block of the model (``config.n_layers``),
+        every layer starting with the cache's ``seq_len`` rows.  The block returns it in
+        place of the contiguous cache, so the following blocks of the same forward take
+        their own layers from it through the layer cursor, each layer attending to its own
+        keys and values (the reference threads one cache through all blocks,
+        transformer.py:229-238).  After the last block the paged cache holds every layer's
+        rows and its ``seq_len`` has advanced by the forward's tokens."""
+        for name in ("k", "v", "seq_len", "batch_size"):
+            if not hasattr(cache, name):
+                raise TypeError(f"kv_cache of type {type(cache).__name__} has no {name!r}: "
+                                "expected a PagedKVCache or a KVCache")
+        b, s, _ = x.shape
+        s0 = int(cache.seq_len)
+        if int(cache.batch_size) != b:
+            raise ValueError(f"kv_cache holds {cache.batch_size} sequences, input has {b}")
+        if s0 > 0 and (tuple(cache.k.shape[1:]) != (self.n_kv_heads, s0, self.head_dim)
+                       or cache.v.shape != cache.k.shape):
+            raise ValueError(f"kv_cache k / v are {tuple(cache.k.shape)}, expected "
+                             f"[{b}, {self.n_kv_heads}, {s0}, {self.head_dim}]")
+        page_dtype = FP8 if _cfg(self.config, "kv_cache_dtype", None) == "fp8" else x.dtype
+        paged = PagedKVCache(b, self.n_kv_heads, self.head_dim, 0, x.device, page_dtype,
+                             num_layers=int(getattr(self.config, "n_layers", 1)),
+                             block_size=int(_cfg(self.config, "kv_block_size", 16)),
+                             max_seq_len=s0 + s, compute_dtype=x.dtype)
+        if s0 > 0:
+            k0, v0 = cache.k.to(x.dtype), cache.v.to(x.dtype)
+            for layer in range(paged.num_layers):
+                paged.select_layer(layer)
+                paged.update(k0, v0, 0)
+            paged.select_layer(0)
+        return paged
 
 
-def get_attention(config: TransformerConfig) -> nn.Module:
-    """src/core/attention.py:190-194 plus the paged backend."""
+def get_attention(config: Any) -> nn.Module:
+    """src/core/attention.py:190-194 plus the paged backend.  ``"triton"`` gives the torch
+    module, as the reference's ``AttentionTriton`` does: its forward copies its weights
+    into a new ``AttentionTorch`` and runs that (attention.py:151-187)."""
     if config.attn_impl == "hip_paged":
         return PagedAttention(config)
-    if config.attn_impl == "triton":
-        raise NotImplementedError("the Triton attention backend is not part of this build")
     return AttentionTorch(config)
 
 
@@ -495,15 +552,17 @@ class Transformer(nn.Module):
         cfg = self.config
         device = device or self.token_embedding.weight.device
         dtype = dtype or self.token_embedding.weight.dtype
+        n_kv = int(_cfg(cfg, "n_kv_heads", cfg.n_heads))
+        head_dim = cfg.d_model // cfg.n_heads
         if cfg.attn_impl == "hip_paged":
-            page_dtype = torch.float8_e4m3fn if cfg.kv_cache_dtype == "fp8" else dtype
-            cache = PagedKVCache(batch_size, cfg.n_kv_heads, cfg.head_dim, 0, device, page_dtype,
-                                 num_layers=cfg.n_layers, block_size=cfg.kv_block_size,
-                                 max_seq_len=max_seq_len, num_pages=cfg.kv_num_pages,
+            page_dtype = FP8 if _cfg(cfg, "kv_cache_dtype", None) == "fp8" else dtype
+            cache = PagedKVCache(batch_size, n_kv, head_dim, 0, device, page_dtype,
+                                 num_layers=cfg.n_layers, block_size=_cfg(cfg, "kv_block_size", 16),
+                                 max_seq_len=max_seq_len, num_pages=_cfg(cfg, "kv_num_pages", None),
                                  compute_dtype=dtype)
             cache.resize(max_seq_len)
             return cache
-        return LayeredKVCache(batch_size, cfg.n_kv_heads, cfg.head_dim, cfg.n_layers, device, dtype)
+        return LayeredKVCache(batch_size, n_kv, head_dim, cfg.n_layers, device, dtype)
 
     def logits(self, x: torch.Tensor) -> torch.Tensor:
         w = self.token_embedding.weight if self.lm_head is None else self.lm_head.weight
@@ -523,7 +582,8 @@ class Transformer(nn.Module):
         x = self.token_embedding(input_ids) + self.position_embedding(position_ids)
         # attention_mask None means all ones (transformer.py:212-213 builds ones_like)
         sliding_window = self.config.sliding_window
-        sink_cfg = {"sink_tokens": self.config.sink_tokens} if self.config.sink_tokens else None
+        n_sink = int(_cfg(self.config, "sink_tokens", 0))
+        sink_cfg = {"sink_tokens": n_sink} if n_sink else None
         for block in self.blocks:
             x, kv_cache, _ = block(x, attention_mask=attention_mask, kv_cache=kv_cache,
                                    sliding_window=sliding_window, sink_cfg=sink_cfg)

@@ -468,7 +468,9 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
     be in the pages (:func:`kv_append`).  Row at position p attends to keys ``j <= p``
     within the window (``j > p - window``) or among the first ``n_sink`` positions.
     Returns ``[n_tok, Hq, D]``.  ``max_query_len`` (>= every chunk length) sizes the
-    launch; when omitted it is read back from ``query_start`` (a device sync).
+    launch; when omitted it is read back from ``query_start`` (a device sync), and
+    ``query_start`` is then checked: 0-based, non-decreasing, ending at ``n_tok``.  The
+    kernel skips a sequence whose rows do not lie inside ``q`` either way.
     FP8 pools (``torch.float8_e4m3fn`` with ``k_scale`` / ``v_scale``) take fp16 or bf16
     queries; keys and values are dequantized (code / sf, rounded to the query dtype)
     on their way into LDS.
@@ -498,7 +500,11 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
     if query_start.numel() != batch + 1:
         raise ValueError(f"query_start must have B+1 = {batch + 1} entries")
     if max_query_len is None:
-        max_query_len = int((query_start[1:] - query_start[:-1]).max().item()) if batch else 0
+        qs = query_start.tolist()
+        if qs[0] != 0 or qs[-1] != q.shape[0] or any(b < a for a, b in zip(qs, qs[1:])):
+            raise ValueError(f"query_start must rise from 0 to n_tok = {q.shape[0]}; got "
+                             f"{qs if len(qs) <= 8 else qs[:4] + ['...'] + qs[-4:]}")
+        max_query_len = max((b - a for a, b in zip(qs, qs[1:])), default=0)
     q = q.contiguous()
     if scale is None:
         scale = 1.0 / math.sqrt(head_dim)
@@ -511,14 +517,15 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
     if fp8:
         _abi.call("ivakv_prefill_attn_fp8", q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
                   scales[0].data_ptr(), scales[1].data_ptr(), block_tables.data_ptr(),
-                  context_lens.data_ptr(), query_start.data_ptr(), out.data_ptr(), batch, hq,
-                  hkv, head_dim, bs, block_tables.shape[1], num_pages, int(max_query_len),
-                  float(scale), window, n_sink, dtype_code(q.dtype), _stream(dev))
+                  context_lens.data_ptr(), query_start.data_ptr(), q.shape[0], out.data_ptr(),
+                  batch, hq, hkv, head_dim, bs, block_tables.shape[1], num_pages,
+                  int(max_query_len), float(scale), window, n_sink, dtype_code(q.dtype),
+                  _stream(dev))
         return out
     _abi.call("ivakv_prefill_attn", q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
               block_tables.data_ptr(), context_lens.data_ptr(), query_start.data_ptr(),
-              out.data_ptr(), batch, hq, hkv, head_dim, bs, block_tables.shape[1], num_pages,
-              int(max_query_len), float(scale), window, n_sink, dtype_code(q.dtype),
+              q.shape[0], out.data_ptr(), batch, hq, hkv, head_dim, bs, block_tables.shape[1],
+              num_pages, int(max_query_len), float(scale), window, n_sink, dtype_code(q.dtype),
               _stream(dev))
     return out
 
@@ -543,13 +550,20 @@ def copy_pages(k_pool: torch.Tensor, v_pool: torch.Tensor, src_pages: torch.Tens
                dst_pages: torch.Tensor, k_scale: Optional[torch.Tensor] = None,
                v_scale: Optional[torch.Tensor] = None) -> None:
     """Moves pages ``src_pages[i] -> dst_pages[i]`` (int32, disjoint sets) of a pool pair,
-    with the FP8 scaling factors when the pools are FP8."""
+    with the FP8 scaling factors when the pools are FP8.  Every id must lie in
+    ``[0, num_pages)`` (checked here, with one device read; the kernel also skips a move
+    outside the pool)."""
     dev = _require_gpu(k_pool, v_pool, src_pages, dst_pages)
     num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
     src = _i32(src_pages, "src_pages").reshape(-1)
     dst = _i32(dst_pages, "dst_pages").reshape(-1)
     if src.numel() != dst.numel():
         raise ValueError("src_pages and dst_pages differ in length")
+    if src.numel():
+        ids = torch.cat([src, dst])
+        lo, hi = (int(v) for v in torch.stack([ids.min(), ids.max()]).tolist())
+        if lo < 0 or hi >= num_pages:
+            raise IndexError(f"page ids in [{lo}, {hi}] outside the pool of {num_pages} pages")
     ks = vs = None
     if is_fp8(k_pool):
         ks, vs = _scales(k_pool, k_scale, v_scale)
@@ -558,8 +572,8 @@ def copy_pages(k_pool: torch.Tensor, v_pool: torch.Tensor, src_pages: torch.Tens
         _abi.call("ivakv_copy_pages", k_pool.data_ptr(), v_pool.data_ptr(),
                   ks.data_ptr() if ks is not None else None,
                   vs.data_ptr() if vs is not None else None,
-                  src[start:].data_ptr(), dst[start:].data_ptr(), n, hkv, head_dim, bs,
-                  k_pool.element_size(), _stream(dev))
+                  src[start:].data_ptr(), dst[start:].data_ptr(), n, num_pages, hkv, head_dim,
+                  bs, k_pool.element_size(), _stream(dev))
 
 
 def kv_compact(kv_cache: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
@@ -578,6 +592,21 @@ def kv_compact(kv_cache: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
     return kv_ops(kv_cache, idx, operation="gather")
 
 
+class KVOps(torch.autograd.Function):
+    """``KVOpsTriton`` (src/kernels_t/kv_ops_triton.py:95-147): the index op as an autograd
+    function whose backward gives no gradient to any input (an output of an input that
+    requires grad is part of the graph, and backward through it stops there)."""
+
+    @staticmethod
+    def forward(ctx, kv_cache: torch.Tensor, indices: torch.Tensor,
+                values: Optional[torch.Tensor] = None, operation: str = "gather") -> torch.Tensor:
+        return _kv_ops(kv_cache, indices, values, operation)
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor):
+        return None, None, None, None
+
+
 def kv_ops(kv_cache: torch.Tensor, indices: torch.Tensor, values: Optional[torch.Tensor] = None,
            operation: str = "gather") -> torch.Tensor:
     """Index gather / scatter along the sequence axis of a contiguous ``[B, H, S, D]`` cache.
@@ -592,7 +621,14 @@ def kv_ops(kv_cache: torch.Tensor, indices: torch.Tensor, values: Optional[torch
     Differences, both deliberate: the gather output keeps the cache dtype (the reference
     allocated it in the default dtype, kv_ops_triton.py:112), and an index outside
     ``[0, S)`` raises ``IndexError`` instead of reading or writing out of bounds.
+    Runs as :class:`KVOps`, as ``kv_ops_triton`` runs ``KVOpsTriton.apply``
+    (kv_ops_triton.py:150-156).
     """
+    return KVOps.apply(kv_cache, indices, values, operation)
+
+
+def _kv_ops(kv_cache: torch.Tensor, indices: torch.Tensor, values: Optional[torch.Tensor],
+            operation: str) -> torch.Tensor:
     if operation not in ("gather", "scatter"):
         raise ValueError(f"Unknown operation: {operation}")
     if operation == "scatter" and values is None:

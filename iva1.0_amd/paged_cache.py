@@ -75,6 +75,9 @@ class PagedKVPool:
         self._free_rows: List[int] = list(range(self.max_seqs - 1, -1, -1))
         self.block_tables = np.full((self.max_seqs, self.max_blocks), -1, dtype=np.int32)
         self.context_lens = np.zeros(self.max_seqs, dtype=np.int32)
+        # bumped by every change of a block-table entry (allocation, release, fork, free,
+        # compaction, restore): device copies of the tables are stale once it moves
+        self.generation = 0
         self.k_pools: List[torch.Tensor] = []
         self.v_pools: List[torch.Tensor] = []
         # FP8 pools: one fp32 scaling factor per (slot, kv head) and layer
@@ -155,6 +158,7 @@ class PagedKVPool:
 
     def _sync_row(self, seq_id) -> None:
         s, row = self._seqs[seq_id], self._rows[seq_id]
+        self.generation += 1
         self.block_tables[row, :] = -1
         self.block_tables[row, :len(s.pages)] = s.pages
         self.context_lens[row] = s.length
@@ -230,6 +234,7 @@ class PagedKVPool:
             self._drop_page(p)
         row = self._rows.pop(seq_id)
         del self._seqs[seq_id]
+        self.generation += 1
         self.block_tables[row, :] = -1
         self.context_lens[row] = 0
         self._free_rows.append(row)
@@ -351,6 +356,7 @@ class PagedKVPool:
         self._free_rows = list(state["free_rows"])
         self._seqs = {k: _Seq(pages=list(p), length=int(n), reserved=len(p) * self.block_size)
                       for k, (p, n) in state["seqs"].items()}
+        self.generation += 1
         self.block_tables[:] = -1
         self.context_lens[:] = 0
         for k in self._seqs:
@@ -410,7 +416,7 @@ class PagedKVCache:
         self._cursor = 0
         self._view: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor, int, int]] = None
         self._bt_dev: Optional[torch.Tensor] = None
-        self._bt_pages = -1
+        self._bt_gen = -1      # pool generation the device block table was copied at
         self._static: Optional[dict] = None
         self._positions: Optional[torch.Tensor] = None
         if seq_len > 0:
@@ -500,7 +506,7 @@ class PagedKVCache:
         kv_append(rows_k, rows_v, self.pool.k_pools[layer], self.pool.v_pools[layer],
                   torch.from_numpy(slots).to(self.device), **self.pool.scales(layer))
         self.seq_len = max(self.seq_len, end)
-        self._bt_pages = -1
+        self._bt_gen = -1
 
     def free(self) -> None:
         """Returns every page of this cache's sequences to the pool."""
@@ -510,11 +516,13 @@ class PagedKVCache:
 
     # ------------------------------------------------------- layer cursor
     def _tables(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Device block table (copied again only when the pool's tables changed since the
+        last copy) and context lengths of this cache's sequences."""
         bt, ctx = self.pool.tables(self.seq_ids)
-        pages = int((bt >= 0).sum())
-        if self._bt_dev is None or self._bt_pages != pages or self._bt_dev.shape != bt.shape:
+        gen = self.pool.generation
+        if self._bt_dev is None or self._bt_gen != gen or self._bt_dev.shape != bt.shape:
             self._bt_dev = torch.from_numpy(bt).to(self.device)
-            self._bt_pages = pages
+            self._bt_gen = gen
         return self._bt_dev, torch.from_numpy(ctx).to(self.device)
 
     # ------------------------------------------------------ static decode
@@ -565,7 +573,7 @@ class PagedKVCache:
             if grow > 0:
                 self.pool.allocate(s, grow)
         self._static = None
-        self._bt_pages = -1
+        self._bt_gen = -1
 
     def _static_step(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, int, int]:
         st = self._static

@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol(iva):
     lib = iva._abi.lib()
     for name in declared_symbols():
         assert hasattr(lib, name), f"{name} not exported by libivakv.so"
-    assert lib.ivakv_abi_version() == iva._abi.ABI_VERSION == 1
+    assert lib.ivakv_abi_version() == iva._abi.ABI_VERSION == 2
 
 
 def call(iva, name, *args):
@@ -149,7 +149,7 @@ def test_fp8_entry_argument_checks(iva):
 
     def prefill8(**over):
         args = dict(q=FAKE, k=FAKE, v=FAKE, ks=FAKE, vs=FAKE, bt=FAKE, ctx=FAKE, qs=FAKE,
-                    out=FAKE, batch=2, hq=8, hkv=2, d=128, bs=16, max_blocks=8,
+                    n_tok=8, out=FAKE, batch=2, hq=8, hkv=2, d=128, bs=16, max_blocks=8,
                     num_pages=16, max_q=4, scale=0.088, window=0, n_sink=0, dtype=a.F16,
                     stream=None)
         args.update(over)
@@ -161,7 +161,9 @@ def test_fp8_entry_argument_checks(iva):
     assert prefill8(vs=FAKE + 4) == a.E_ARG       # factors must be 16-byte aligned
     assert prefill8(d=96) == a.E_SHAPE
     assert prefill8(hq=9) == a.E_SHAPE
+    assert prefill8(n_tok=-1) == a.E_ARG
     assert prefill8(max_q=0) == a.OK              # nothing to do
+    assert prefill8(n_tok=0) == a.OK
 
     def fused8(**over):
         args = dict(q=FAKE, kn=FAKE, vn=FAKE, k=FAKE, v=FAKE, ks=FAKE, vs=FAKE, bt=FAKE,
@@ -176,3 +178,35 @@ def test_fp8_entry_argument_checks(iva):
     assert fused8(kn=None) == a.E_ARG
     assert fused8() == a.E_WORKSPACE              # the stream walk needs a workspace
     assert fused8(bs=8) == a.E_SHAPE
+
+
+def test_prefill_and_copy_pages_argument_checks(iva):
+    """ivakv_prefill_attn takes the row count of q / out (query_start is bounded by it in
+    the kernel); ivakv_copy_pages takes the pool's page count (moves outside it are
+    skipped in the kernel)."""
+    a = iva._abi
+
+    def prefill(**over):
+        args = dict(q=FAKE, k=FAKE, v=FAKE, bt=FAKE, ctx=FAKE, qs=FAKE, n_tok=8, out=FAKE,
+                    batch=2, hq=8, hkv=2, d=128, bs=16, max_blocks=8, num_pages=16, max_q=4,
+                    scale=0.088, window=0, n_sink=0, dtype=a.F16, stream=None)
+        args.update(over)
+        return call(iva, "ivakv_prefill_attn", *args.values())
+
+    assert prefill(n_tok=-1) == a.E_ARG
+    assert "n_tok" in a.last_error()
+    assert prefill(d=96) == a.E_SHAPE
+    assert prefill(n_tok=0) == a.OK
+    assert prefill(batch=0) == a.OK
+
+    def copy(**over):
+        args = dict(k=FAKE, v=FAKE, ks=None, vs=None, src=FAKE, dst=FAKE, n=4, pages=16,
+                    hkv=8, d=128, bs=16, eb=2, stream=None)
+        args.update(over)
+        return call(iva, "ivakv_copy_pages", *args.values())
+
+    assert copy(pages=-1) == a.E_ARG
+    assert "pages=-1" in a.last_error()
+    assert copy(eb=3) == a.E_ARG
+    assert copy(ks=FAKE) == a.E_ARG               # both factor tensors or neither
+    assert copy(n=0) == a.OK

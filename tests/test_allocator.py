@@ -197,3 +197,35 @@ def test_compaction_moves_pack_live_pages(iva):
     p.allocate("new", 1)
     assert p.pages("new") == [n_used]             # allocation continues from the tail
     assert p.compact() == 0
+
+
+def test_generation_moves_with_every_table_change(iva):
+    """Every block-table change bumps the pool generation (device copies of the tables
+    are keyed on it); a length-only change inside allocated pages does not."""
+    p, _ = pool(iva, pages=32, max_seqs=8)
+    g = [p.generation]
+
+    def bumped():
+        g.append(p.generation)
+        return g[-1] > g[-2]
+
+    p.add_sequence("a")
+    assert bumped()
+    p.allocate("a", 20)                          # new pages
+    assert bumped()
+    p.allocate("a", 3)                           # fits in the pages it has
+    assert not bumped()
+    p.add_sequence("b")
+    p.allocate("b", 40)
+    p.fork("a", "c")
+    assert bumped()
+    p.free("b")                                  # frees the low pages: a gap below "c"
+    assert bumped()
+    assert p.compact() > 0                       # renumbers "a" / "c" with no length change
+    assert bumped()
+    p.add_sequence("d")
+    p.allocate("d", 16 * 6)
+    assert p.release_outside_window("d", window=20, n_sink=0) > 0
+    assert bumped()
+    p.load_state_dict(p.state_dict())
+    assert bumped()

@@ -166,6 +166,34 @@ def test_prefill_argument_errors(iva, dev):
         iva.paged_prefill_attention(args[0].float(), *args[1:], c["query_start"].to(dev))
     out = iva.paged_prefill_attention(*args, c["query_start"].to(dev), max_query_len=0)
     assert out.shape == c["q"].shape  # nothing computed, no error
+    # query_start must rise from 0 to n_tok (checked when max_query_len is read from it)
+    for qs in ([1, 20], [0, 19], [0, 21]):
+        with pytest.raises(ValueError, match="query_start"):
+            iva.paged_prefill_attention(*args, torch.tensor(qs, dtype=torch.int32, device=dev))
+
+
+def test_prefill_skips_sequences_outside_q(iva, dev):
+    """With max_query_len given there is no host read of query_start: the kernel skips
+    a sequence whose rows [query_start[b], query_start[b+1]) do not lie inside q (its
+    output rows stay as they were) and computes the others."""
+    c = make(iva, [40, 30, 25], [8, 6, 5], 4, 2, 64, torch.float16, seed=3)
+    lay = c["layout"]
+    n_tok = c["q"].shape[0]          # 19 rows: 0..7, 8..13, 14..18
+    want = run(iva, dev, c)
+    qs = torch.tensor([0, 8, 14, 21], dtype=torch.int32, device=dev)   # last ends past q
+    out = torch.full_like(want, 7.0)
+    iva.paged_prefill_attention(c["q"].to(dev), c["k_pool"].to(dev), c["v_pool"].to(dev),
+                                lay.block_tables.to(dev), lay.context_lens.to(dev), qs,
+                                max_query_len=8, out=out)
+    assert torch.equal(out[:14], want[:14])
+    assert bool((out[14:] == 7.0).all())
+    qs = torch.tensor([-3, 8, 14, n_tok], dtype=torch.int32, device=dev)  # first before q
+    out = torch.full_like(want, 7.0)
+    iva.paged_prefill_attention(c["q"].to(dev), c["k_pool"].to(dev), c["v_pool"].to(dev),
+                                lay.block_tables.to(dev), lay.context_lens.to(dev), qs,
+                                max_query_len=11, out=out)
+    assert bool((out[:8] == 7.0).all())
+    assert torch.equal(out[8:], want[8:])
 
 
 @pytest.mark.parametrize("scale", [-0.2, 0.0, 0.35])

@@ -133,6 +133,28 @@ def test_copy_pages_and_pool_compaction(iva, dev, fp8):
         assert torch.equal(w[keep], r[keep])
 
 
+def test_copy_pages_rejects_and_skips_ids_outside_the_pool(iva, dev):
+    """ops.copy_pages raises IndexError for an id outside [0, num_pages); at the C ABI
+    (no host check) the kernel skips such a move and performs the others."""
+    ks, vs = iva.pool_shapes(8, 2, 64, 16, torch.float16)
+    k = torch.randn(ks, device=dev).half()
+    v = torch.randn(vs, device=dev).half()
+    k0, v0 = k.clone(), v.clone()
+    for src, dst in (([1, 8], [2, 3]), ([1, 2], [-1, 3])):
+        with pytest.raises(IndexError, match="outside the pool"):
+            iva.copy_pages(k, v, torch.tensor(src, dtype=torch.int32, device=dev),
+                           torch.tensor(dst, dtype=torch.int32, device=dev))
+    assert torch.equal(k, k0) and torch.equal(v, v0)
+    src = torch.tensor([1, 9, 5, 2], dtype=torch.int32, device=dev)
+    dst = torch.tensor([0, 3, -2, 6], dtype=torch.int32, device=dev)
+    iva._abi.call("ivakv_copy_pages", k.data_ptr(), v.data_ptr(), None, None, src.data_ptr(),
+                  dst.data_ptr(), 4, 8, 2, 64, 16, 2, torch.cuda.current_stream().cuda_stream)
+    want_k, want_v = k0.clone(), v0.clone()
+    want_k[[0, 6]] = k0[[1, 2]]
+    want_v[[0, 6]] = v0[[1, 2]]
+    assert torch.equal(k, want_k) and torch.equal(v, want_v)
+
+
 def test_kv_compact_vs_torch(iva, dev):
     kv = torch.randn(3, 4, 40, 64, device=dev).half()
     mask = torch.zeros(40, dtype=torch.bool)
