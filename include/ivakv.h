@@ -188,6 +188,28 @@ int ivakv_decode_append_attn(const void* q, const void* k_new, const void* v_new
                              hipStream_t stream);
 
 /*
+ * ivakv_decode_append_attn without a workspace argument: the same plan, kernels and
+ * results as ivakv_decode_append_attn, with the decode workspace taken from a
+ * file-scope device array of the library (64 MiB per device, held from the first call
+ * on a device until the process ends).  It allocates nothing: no hipMalloc, hipFree or
+ * allocating library call.  A geometry whose workspace exceeds 64 MiB (see
+ * ivakv_decode_workspace_size; e.g. more than ~12k (sequence, kv head) units at GQA 4,
+ * D 128) returns IVAKV_E_WORKSPACE before any launch.  Every call on one device shares
+ * that device's array: calls that overlap on one device (different streams, or
+ * threads) race and must be serialised by the caller.  Nothing in the array needs to
+ * start at zero.
+ * No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).
+ */
+int ivakv_decode_append_attn_noalloc(const void* q, const void* k_new, const void* v_new,
+                                     void* k_pool, void* v_pool, const int32_t* block_tables,
+                                     const int32_t* context_lens, void* out, int batch,
+                                     int num_q_heads, int num_kv_heads, int head_dim,
+                                     int block_size, int max_blocks, int num_pages, float scale,
+                                     int window, int n_sink, int dtype, hipStream_t stream);
+
+/*
  * FP8 KV pages (OCP e4m3fn codes, one byte per element) with one fp32 scaling factor
  * per (slot, kv head):
  *   k_pool  [num_pages][Hkv][D/16][BS][16] bytes (16-byte chunks of 16 dims)

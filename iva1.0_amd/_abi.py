@@ -120,6 +120,14 @@ SIGNATURES = {
         c_void_p, c_void_p, c_int, c_int,      # src_pages, dst_pages, n_moves, num_pages
         c_int, c_int, c_int, c_int, c_void_p,  # Hkv, D, block_size, elem_bytes, stream
     ]),
+    "ivakv_decode_append_attn_noalloc": (c_int, [
+        c_void_p, c_void_p, c_void_p,          # q, k_new, v_new
+        c_void_p, c_void_p,                    # k_pool, v_pool
+        c_void_p, c_void_p, c_void_p,          # block_tables, context_lens, out
+        c_int, c_int, c_int, c_int,            # batch, num_q_heads, num_kv_heads, head_dim
+        c_int, c_int, c_int, c_float,          # block_size, max_blocks, num_pages, scale
+        c_int, c_int, c_int, c_void_p,         # window, n_sink, dtype, stream
+    ]),
     "ivakv_prefill_attn_fp8": (c_int, [
         c_void_p, c_void_p, c_void_p,          # q, k_pool, v_pool
         c_void_p, c_void_p,                    # k_scale, v_scale
