@@ -68,5 +68,41 @@ def build(verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+def kernel_resource_usage(srcs=None) -> dict:
+    """Per-kernel register and scratch figures of every gfx950 kernel instantiation, from
+    the compiler's ``-Rpass-analysis=kernel-resource-usage`` remarks (device-only
+    compiles of each source, in parallel, into a temporary directory).  Returns
+    ``{mangled kernel name: {"VGPRs", "AGPRs", "ScratchSize", "Occupancy"}}``."""
+    import re
+    import tempfile
+    srcs = sources() if srcs is None else srcs
+    keys = ("VGPRs", "AGPRs", "ScratchSize", "Occupancy")
+    out: dict = {}
+    with tempfile.TemporaryDirectory() as tmp:
+        procs = []
+        for i, src in enumerate(srcs):
+            cmd = [hipcc_path(), f"--offload-arch={OFFLOAD_ARCH}", "-O3", "-std=c++17", "-c",
+                   "--cuda-device-only", "-Rpass-analysis=kernel-resource-usage",
+                   f"-I{INCLUDE}", f"-I{CSRC}", *DEVICE_FLAGS, "-o", str(Path(tmp) / f"{i}.o"),
+                   str(src)]
+            procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE,
+                                                stderr=subprocess.PIPE, text=True)))
+        for src, proc in procs:
+            _, err = proc.communicate()
+            if proc.returncode != 0:
+                raise RuntimeError(f"hipcc failed on {src.name}:\n{err[-2000:]}")
+            cur = None
+            for line in err.splitlines():
+                m = re.search(r"Function Name: (\S+)", line)
+                if m:
+                    cur = m.group(1)
+                    out[cur] = {}
+                    continue
+                m = re.search(r"remark:\s+(\w+)(?: \[[^\]]*\])?: (\d+)", line)
+                if m and cur and m.group(1) in keys:
+                    out[cur][m.group(1)] = int(m.group(2))
+    return out
+
+
 if __name__ == "__main__":
     print(build(verbose=True))

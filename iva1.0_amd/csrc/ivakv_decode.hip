@@ -38,13 +38,12 @@ namespace {
 constexpr int kWaves = 4;     // wavefronts per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kDefaultPartitionPages = 32;
-#ifndef IVAKV_PAGE_BUFS
-#define IVAKV_PAGE_BUFS 2
-#endif
-constexpr int kPageBufs = IVAKV_PAGE_BUFS;  // register page buffers per wave (ring)
-// Workgroups per CU the partitioned walk is built for (two 4-wave groups: 2 waves
-// per SIMD, up to 256 registers each).
-constexpr int kPartialWGsPerCU = 2;
+constexpr int kPageBufs = 2;  // register page buffers per wave (ring)
+// Workgroups per CU the partitioned walk is built for: two 4-wave groups (2 waves
+// per SIMD, up to 256 registers each), or one at head_dim 256, whose two-tile ring
+// alone takes 128 (16-bit) or 256 (fp32) registers per lane: one wave per SIMD gets
+// 512, so nothing spills to scratch.
+constexpr int partial_wgs_per_cu(int D) { return D == 256 ? 1 : 2; }
 // Stream walk workgroup: kStreamWaves independent waves, one per SIMD; how many
 // workgroups share a CU is a property of the tile operations (Ops::kWGsPerCU).
 // Then the wave budget the workspace is sized for, the fewest tiles worth giving
@@ -58,12 +57,8 @@ constexpr int kMaxStreamBatch = 8192;
 // tile).  One 4-wave workgroup per CU keeps 2 x 8 KiB slots per wave in flight at
 // D 128 on 16-bit pages, enough to hold HBM busy; 4 KiB slots (D 64 at 16 bits,
 // D 128 on FP8 pages) need two workgroups per CU for as many bytes in flight.
-#ifndef IVAKV_WG2_SLOT_BYTES
-#define IVAKV_WG2_SLOT_BYTES 4096
-#endif
-constexpr int walk_wgs_per_cu(int64_t slot_bytes) {
-  return slot_bytes <= IVAKV_WG2_SLOT_BYTES ? 2 : 1;
-}
+constexpr int64_t kWG2SlotBytes = 4096;
+constexpr int walk_wgs_per_cu(int64_t slot_bytes) { return slot_bytes <= kWG2SlotBytes ? 2 : 1; }
 
 struct DecodeArgs {
   const void* q;
@@ -366,13 +361,13 @@ struct TileOps8 {
 // loop body has no branches and the compiler's vmcnt waits only cover the
 // buffer about to be consumed.
 //
-// Built for two workgroups per CU (like the stream walk): with a higher
+// Built for two workgroups per CU (one at head_dim 256): with a higher
 // occupancy target the scheduler sinks each load next to its use and the ring
 // stops overlapping loads with compute.
 // Block table and context lengths come in as __restrict__ parameters, which
 // keeps their reads on the scalar cache (see decode_stream_kernel).
 template <int DT, int D>
-__global__ __launch_bounds__(kThreads, kPartialWGsPerCU) void decode_partial_kernel(
+__global__ __launch_bounds__(kThreads, partial_wgs_per_cu(D)) void decode_partial_kernel(
     DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ ctx) {
   using Ops = TileOps<DT, D>;
   using E = typename Ops::E;

@@ -63,7 +63,9 @@ struct PrefillShape {
   static constexpr int kESize = DT == IVAKV_F32 ? 4 : 2;
   static constexpr int kWaves = (DT == IVAKV_F32 || D == 256) ? 4 : 8;
   static constexpr int kThreads = 64 * kWaves;
-  static constexpr int NR = 2;
+  // Row blocks per wave; one for fp32 at head_dim 256, whose q rows and accumulators
+  // for two blocks would not fit 512 registers.
+  static constexpr int NR = (DT == IVAKV_F32 && D == 256) ? 1 : 2;
   static constexpr int kStages = kWaves == 8 ? 2 : 1;  // pairs in flight in registers
   static constexpr int kRowsWave = 16 * NR;
   static constexpr int kRowsWG = kRowsWave * kWaves;

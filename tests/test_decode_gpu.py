@@ -233,6 +233,37 @@ def test_c2_full_size(iva, dev):
     assert err64 <= 2e-3, f"C2 max abs err vs fp64 oracle {err64}"
 
 
+def test_c2_fused_step_full_size(iva, dev):
+    """The op bench.py times for C2, on the bench's own first pool set (c2_lengths(0),
+    pools of decode_batch seed 100, new rows from a device generator seeded 500):
+    paged_decode_append_attention leaves the pools bit-identical to kv_append of the new
+    rows at position L-1, and its output over all 32 sequences is within the fp16
+    tolerance of the fp64 oracle evaluated on the appended pools; so is the unfused
+    append + attention."""
+    lengths = iva.workloads.c2_lengths(seed=0)
+    sc = 1 / math.sqrt(128)
+    d = iva.workloads.decode_batch(lengths, 32, 8, 128, torch.float16, seed=100, device=dev,
+                                   scale=sc)
+    lay = d["layout"]
+    bt, ctx = lay.block_tables.to(dev), lay.context_lens.to(dev)
+    gen = torch.Generator(device=dev).manual_seed(500)
+    k_new = (torch.randn(32, 8, 128, generator=gen, device=dev) * sc).half()
+    v_new = (torch.randn(32, 8, 128, generator=gen, device=dev) * sc).half()
+    kp_f, vp_f = d["k_pool"].clone(), d["v_pool"].clone()
+    out = iva.paged_decode_append_attention(d["q"], k_new, v_new, kp_f, vp_f, bt, ctx)
+    slots = torch.stack([lay.slots(b, torch.tensor([n - 1])) for b, n in enumerate(lengths)])
+    kp_a, vp_a = d["k_pool"].clone(), d["v_pool"].clone()
+    iva.kv_append(k_new, v_new, kp_a, vp_a, slots.reshape(-1).to(dev))
+    assert torch.equal(kp_f.view(torch.int16), kp_a.view(torch.int16))
+    assert torch.equal(vp_f.view(torch.int16), vp_a.view(torch.int16))
+    ref = orc.decode_attention(to_np(d["q"]), to_np(kp_a), to_np(vp_a),
+                               lay.block_tables.numpy(), lay.context_lens.numpy())
+    err = assert_close(out, ref, torch.float16, what="C2 fused step")
+    unfused = iva.paged_decode_attention(d["q"], kp_a, vp_a, bt, ctx)
+    assert_close(unfused, ref, torch.float16, what="C2 append + attention")
+    print(f"C2 fused step: max abs err vs fp64 oracle {err:.2e} over all 32 sequences")
+
+
 def test_c4_long_context(iva, dev):
     """C4: B 4 at 32k..128k tokens, window 4096 + 4 sinks, bf16, K/V ~ N(0,1)."""
     d = iva.workloads.c4_long_context(seed=0, device=dev)

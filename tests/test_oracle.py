@@ -537,6 +537,87 @@ def test_rope_matches_the_reference_module():
             assert np.allclose(got, ref[b], rtol=0, atol=2e-6 * max(1.0, np.abs(x).max()))
 
 
+def _rope_check_d2_rotates_by_p(fn):
+    """D 2, any theta: the one pair has frequency theta^0 = 1, so position p rotates it by
+    p radians counter-clockwise: (1, 0) -> (cos p, sin p), (0, 1) -> (-sin p, cos p)."""
+    p = np.array([1, 2, 7, 100], dtype=np.int64)
+    e0 = fn(np.tile([[1.0, 0.0]], (4, 1)), p, 10000.0)
+    e1 = fn(np.tile([[0.0, 1.0]], (4, 1)), p, 10000.0)
+    a = p.astype(np.float64)
+    return (np.allclose(e0, np.stack([np.cos(a), np.sin(a)], 1), atol=1e-6)
+            and np.allclose(e1, np.stack([-np.sin(a), np.cos(a)], 1), atol=1e-6))
+
+
+def _rope_check_pair_frequencies(fn):
+    """D 4 / 8 at theta 10000: pair j turns at theta^(-2j/D), so at D 4 pair 1 turns by
+    0.01 p, and at D 8 pairs 1, 2, 3 by 0.1 p, 0.01 p, 0.001 p; a unit vector on the even
+    dim of pair j lands on (cos a_j, sin a_j) and leaves the other pairs at zero."""
+    ok = True
+    for d, rates in ((4, [1.0, 0.01]), (8, [1.0, 0.1, 0.01, 0.001])):
+        for j, rate in enumerate(rates):
+            x = np.zeros((3, d))
+            x[:, 2 * j] = 1.0
+            p = np.array([0, 100, 1000], dtype=np.int64)
+            y = fn(x, p, 10000.0)
+            a = p * rate
+            want = np.zeros((3, d))
+            want[:, 2 * j], want[:, 2 * j + 1] = np.cos(a), np.sin(a)
+            ok = ok and np.allclose(y, want, atol=1e-4)
+    return ok
+
+
+def _rope_check_composition(fn):
+    """R(p) then R(q) is R(p + q) (a rotation group), and R(p) is orthogonal: checked on
+    random rows at D 16 where the float32 angles are exact (p * f_i with small p)."""
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((5, 16))
+    p, q = np.array([1, 2, 3, 4, 5]), np.array([3, 1, 4, 1, 5])
+    two = fn(fn(x, p, 10.0), q, 10.0)
+    one = fn(x, p + q, 10.0)
+    return np.allclose(two, one, atol=1e-5) and np.allclose(
+        np.linalg.norm(fn(x, p, 10.0), axis=1), np.linalg.norm(x, axis=1))
+
+
+ROPE_PINS = [_rope_check_d2_rotates_by_p, _rope_check_pair_frequencies, _rope_check_composition]
+
+
+@pytest.mark.parametrize("check", ROPE_PINS, ids=lambda f: f.__name__)
+def test_rope_oracle_pins(check):
+    assert check(orc.rope)
+
+
+def _rope_mutant(kind):
+    """Plausible mistakes in a RoPE restatement, each of which a pin must catch."""
+    def fn(x, positions, theta=10000.0):
+        x = np.asarray(x, dtype=np.float64)
+        d = x.shape[-1]
+        j = np.arange(d // 2)
+        expo = (j / d) if kind == "exponent_i_over_d" else (2 * j / d)
+        f = (1.0 / theta ** expo).astype(np.float32)
+        ang = np.asarray(positions, np.float64)[:, None] * f[None, :]
+        c, s = np.cos(ang), np.sin(ang)
+        if kind == "rotate_half":   # pairs (i, i + D/2) instead of (2i, 2i + 1)
+            x0, x1 = x[..., :d // 2], x[..., d // 2:]
+        else:
+            x0, x1 = x[..., 0::2], x[..., 1::2]
+        sg = -1.0 if kind == "sign_flip" else 1.0
+        y0, y1 = x0 * c - sg * x1 * s, sg * x0 * s + x1 * c
+        y = np.empty_like(x)
+        if kind == "rotate_half":
+            y[..., :d // 2], y[..., d // 2:] = y0, y1
+        else:
+            y[..., 0::2], y[..., 1::2] = y0, y1
+        return y
+    return fn
+
+
+@pytest.mark.parametrize("kind", ["sign_flip", "exponent_i_over_d", "rotate_half"])
+def test_rope_planted_mistakes_are_caught(kind):
+    fn = _rope_mutant(kind)
+    assert not all(check(fn) for check in ROPE_PINS), f"planted RoPE mistake {kind} passed"
+    assert all(check(_rope_mutant("none")) for check in ROPE_PINS)   # the harness itself
+
+
 def test_rope_invariants():
     rng = np.random.default_rng(22)
     x = rng.standard_normal((10, 4, 32))
