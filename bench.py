@@ -39,6 +39,7 @@ from __future__ import annotations
 
 import argparse
 import csv
+import itertools
 import json
 import math
 import os
@@ -53,8 +54,8 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 METRIC = "paged decode-attn + KV append GB/s and % HBM peak; decode tokens/s at 1 GPU"
 def traffic_path(context: str):
-    """Committed HBM-traffic summary of the walk for a --context choice."""
-    name = "c2" if context == "c2" else f"ctx{int(context)}"
+    """Committed HBM-traffic summary of the walk for a --context choice (or "c4")."""
+    name = context if context in ("c2", "c4") else f"ctx{int(context)}"
     return ROOT / "profiles" / f"decode_attn_{name}_traffic.json"
 WALK_KERNEL = "decode_stream_kernel"
 COPY_BYTES = 256 << 20
@@ -98,12 +99,14 @@ def parse_args():
     p.add_argument("--no-target-4k", dest="target_4k", action="store_false",
                    help="skip the second measurement at the target shape (B 32, every "
                         "sequence at context 4096) that the default line carries")
-    p.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "prefill", "c2fp8", "ops"),
+    p.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "prefill", "c2fp8", "ops",
+                                          "ceiling"),
                    default="c2",
                    help="c2 (default): the contract line; c3 dense-decoder tokens/s, c4 "
                         "long-context window+sinks decode, c5 ragged churn, prefill: 512-token "
                         "chunks over paged context, c2fp8: C2 over FP8 pages, ops: the append / "
-                        "gather / kv_ops / page-move kernels (informational lines)")
+                        "gather / kv_ops / page-move kernels, ceiling: measured streaming "
+                        "and random-tile read bandwidth (informational lines)")
     return p.parse_args()
 
 
@@ -175,7 +178,8 @@ def _mean_kib(directory: str, counter: str, match) -> float:
 def summarize_pmc(fetch_dir: str, write_dir: str, context: str = "c2") -> None:
     """Scales the walk's FETCH_SIZE / WRITE_SIZE (KiB per dispatch) by what the same
     counters read for the plain copy of COPY_BYTES, and writes the traffic summary."""
-    is_walk = lambda k: WALK_KERNEL in k and "TileOps<1, 128>" in k
+    ops = "TileOps<2, 128>" if context == "c4" else "TileOps<1, 128>"   # C4 is bf16
+    is_walk = lambda k: WALK_KERNEL in k and ops in k
     is_copy = lambda k: "copy" in k.lower() and "ivakv" not in k
 
     def copy_kib(directory, counter):
@@ -200,8 +204,9 @@ def summarize_pmc(fetch_dir: str, write_dir: str, context: str = "c2") -> None:
     read_b = fetch_walk * 1024 * f_scale
     write_b = write_walk * 1024 * w_scale
     summary = {
-        "kernel": "decode_stream_kernel<f16,128> (%s)" % (
-            "C2" if context == "c2" else f"B 32 at context {int(context)}"),
+        "kernel": ("decode_stream_kernel<bf16,128> (C4)" if context == "c4" else
+                   "decode_stream_kernel<f16,128> (%s)" % (
+                       "C2" if context == "c2" else f"B 32 at context {int(context)}")),
         "fetch_kib_per_dispatch": round(fetch_walk, 1),
         "write_kib_per_dispatch": round(write_walk, 1),
         "copy_calibration_bytes": COPY_BYTES,
@@ -217,6 +222,85 @@ def summarize_pmc(fetch_dir: str, write_dir: str, context: str = "c2") -> None:
     out.parent.mkdir(exist_ok=True)
     out.write_text(json.dumps(summary, indent=1) + "\n")
     print(json.dumps(summary))
+
+
+def _ceiling_lib():
+    """The read-ceiling kernels (iva1.0_amd/bench_kernels/ivakv_ceiling.hip), built by
+    build() into libivakv_ceiling.so."""
+    import ctypes
+    path = ROOT / "iva1.0_amd" / "libivakv_ceiling.so"
+    if not path.exists():
+        raise SystemExit(f"{path} is missing: run __graft_entry__.build() first")
+    lib = ctypes.CDLL(str(path))
+    c_int, c_int64, c_void_p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+    lib.ceiling_stream.argtypes = [c_void_p, c_int64, c_void_p, c_int, c_void_p]
+    lib.ceiling_tiles.argtypes = [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_int, c_void_p]
+    return lib
+
+
+def measure_ceiling(torch, dev, sets=4, set_bytes=288 << 20, tile_bytes=4096,
+                    tiles_per_launch=70144, reps=40):
+    """Read-bandwidth ceilings of this GPU, on 4 rotated buffers of 288 MiB (as the C2
+    bench rotates its pools): a streaming read of each buffer (best of 2, 4, 8 workgroups
+    per CU), and reads of tiles_per_launch random 4 KiB tiles of each buffer (the C2
+    walk's 70,144 K and V tiles), one tile in flight per wave, 2, 4 or 8 4-wave
+    workgroups per CU (32, 64 or 128 KiB in flight per CU; the walk keeps 64 KiB).
+    GB/s =
+    bytes read / average launch time over back-to-back launches (HIP events); the best
+    arrangement is reported."""
+    lib = _ceiling_lib()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream(dev)
+    st = stream.cuda_stream
+    gen = torch.Generator().manual_seed(3)
+    bufs = [torch.empty(set_bytes, dtype=torch.uint8, device=dev).fill_(i + 1) for i in range(sets)]
+    n_tiles = set_bytes // tile_bytes
+    idxs = [torch.randperm(n_tiles, generator=gen)[:tiles_per_launch].to(torch.int32).to(dev)
+            for _ in range(sets)]
+    sink = torch.empty(cus * 8 * 4 * 16, dtype=torch.uint8, device=dev)   # one word per wave
+
+    def timed(launch):
+        for i in range(sets):
+            launch(i)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for r in range(reps):
+            launch(r % sets)
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        return e0.elapsed_time(e1) * 1e-3 / reps
+
+    def check(rc):
+        if rc != 0:
+            raise SystemExit(f"ceiling kernel launch failed ({rc})")
+
+    stream_gbs = {}
+    for per_cu in (2, 4, 8):
+        t = timed(lambda i: check(lib.ceiling_stream(bufs[i].data_ptr(), set_bytes,
+                                                     sink.data_ptr(), cus * per_cu, st)))
+        stream_gbs[per_cu] = set_bytes / t / 1e9
+    tile_gbs = {}
+    for per_cu in (2, 4, 8):
+        t = timed(lambda i: check(lib.ceiling_tiles(bufs[i].data_ptr(), idxs[i].data_ptr(),
+                                                    tiles_per_launch, tile_bytes,
+                                                    sink.data_ptr(), cus * per_cu, st)))
+        tile_gbs[per_cu] = tiles_per_launch * tile_bytes / t / 1e9
+    del bufs, idxs
+    return {"stream_read_gbs": round(max(stream_gbs.values()), 1),
+            "stream_read_gbs_by_wg_per_cu": {k: round(v, 1) for k, v in stream_gbs.items()},
+            "tile_read_gbs": round(max(tile_gbs.values()), 1),
+            "tile_read_gbs_by_wg_per_cu": {k: round(v, 1) for k, v in tile_gbs.items()},
+            "sample": f"{sets} rotated buffers of {set_bytes >> 20} MiB; tiles: "
+                      f"{tiles_per_launch} random {tile_bytes}-byte tiles per launch, one in "
+                      f"flight per wave, 2 / 4 / 8 workgroups of 4 waves per CU ({cus} CUs)"}
+
+
+def bench_ceiling(args, iva, torch, dev):
+    """Measured read ceilings of the GPU (see measure_ceiling)."""
+    c = measure_ceiling(torch, dev)
+    return {"metric": "HBM read ceiling GB/s (streaming and random 4 KiB tiles)",
+            "workload": "ceiling", "value": c["tile_read_gbs"], "unit": "GB/s",
+            "peak": HBM_PEAK_GBS, **c}
 
 
 def _timer(torch, dev):
@@ -383,7 +467,9 @@ def bench_c2fp8(args, iva, torch, dev):
 
 def bench_c4(args, iva, torch, dev):
     """C4: long-context decode, bf16, B 4 at 32k/64k/96k/128k, GQA 32/8, D 128, window
-    4096 + 4 sinks (union); GB/s on attended bytes."""
+    4096 + 4 sinks (union); GB/s on attended bytes.  Attention (walk + merge) and the walk
+    alone, each as a HIP graph of back-to-back launches over rotated pools (1.34 GB
+    each), plus the same eagerly."""
     wl = iva.workloads
     measure = _timer(torch, dev)
     sets = []
@@ -393,89 +479,177 @@ def bench_c4(args, iva, torch, dev):
         sets.append((d["q"], d["k_pool"], d["v_pool"], lay.block_tables.to(dev),
                      lay.context_lens.to(dev), torch.empty_like(d["q"])))
     w, ns = wl.C4_WINDOW, wl.C4_SINKS
-    run = lambda s, fn: fn(s[0], s[1], s[2], s[3], s[4], window=w, n_sink=ns, out=s[5])
-    for s in sets:
-        run(s, iva.paged_decode_attention)
-    reps = 50
-    t_attn = measure(lambda: [run(sets[i % len(sets)], iva.paged_decode_attention)
-                              for i in range(reps)]) / reps
-    t_walk = measure(lambda: [run(sets[i % len(sets)], iva.paged_decode_attention_partial)
-                              for i in range(reps)]) / reps
-    attended = [min(n, w) + min(ns, max(n - w, 0)) for n in wl.C4_LENGTHS]
-    byts = sum(2 * a * 8 * 128 * 2 for a in attended) + 2 * 4 * 32 * 128 * 2
-    return {"metric": "C4 long-context windowed decode attention GB/s (attended bytes)",
-            "workload": "c4", "value": round(byts / t_attn / 1e9, 1), "unit": "GB/s",
-            "dtype": "bf16", "config": {"lengths": wl.C4_LENGTHS, "window": w, "sinks": ns,
-                                        "heads": "32/8", "head_dim": 128, "launch": "eager"},
-            "attention_us": round(t_attn * 1e6, 2), "walk_us": round(t_walk * 1e6, 2),
-            "walk_gbps": round(byts / t_walk / 1e9, 1), "attended_bytes": byts}
-
-
-def bench_c5(args, iva, torch, dev):
-    """C5: ragged continuous-batching churn, fp16: 256 live sequences, LogNormal(ln 1024,
-    sigma 1) lengths capped at 16k, 512-token prefill chunks, one decode token per
-    sequence per step, completed sequences replaced (LIFO page reuse).  Reports the
-    decode attention GB/s per step on the fragmented tables."""
-    from importlib import import_module
-    pc = import_module("iva_amd.paged_cache")
-    wl = iva.workloads
-    pool = pc.PagedKVPool(48000, 8, 128, 16, 1, torch.float16, dev, max_seqs=512,
-                          max_blocks_per_seq=1024)
-    churn = wl.ChurnBatch(pool, n_seqs=256, seed=0, scale=128 ** -0.5)
-    q = (torch.randn(256, 32, 128, device=dev) * 128 ** -0.5).half()
-    out = torch.empty_like(q)
-    for _ in range(5):
-        churn.step()
-    # Each step's tables go into static buffers (full table width, -1 past the pages
-    # in use) so one captured HIP graph of the attention call serves every step, as
-    # in a graph-captured serving loop; the eager call is timed beside it.
-    bt_s = torch.full((256, pool.max_blocks), -1, dtype=torch.int32, device=dev)
-    ctx_s = torch.zeros(256, dtype=torch.int32, device=dev)
-    ws = torch.empty(iva.decode_workspace_bytes(256, 32, 8, 128, 16, pool.max_blocks),
+    batch, max_blocks = sets[0][0].shape[0], sets[0][3].shape[1]
+    ws = torch.empty(iva.decode_workspace_bytes(batch, 32, 8, 128, 16, max_blocks, w, ns),
                      dtype=torch.uint8, device=dev)
-    attn = lambda bt, ctx: iva.paged_decode_attention(q, pool.k_pools[0], pool.v_pools[0], bt, ctx,
-                                                      out=out, workspace=ws)
+    run = lambda s, fn: fn(s[0], s[1], s[2], s[3], s[4], window=w, n_sink=ns, out=s[5],
+                           workspace=ws)
+    attn = lambda s: run(s, iva.paged_decode_attention)
+    walk = lambda s: run(s, iva.paged_decode_attention_partial)
+    reps = 48
     stream = torch.cuda.Stream(device=dev)
     stream.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(stream):
-        attn(bt_s, ctx_s)
+        for s in sets:
+            attn(s)
+            walk(s)
         torch.cuda.synchronize(dev)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            attn(bt_s, ctx_s)
-    times, eager, byts, done = [], [], [], 0
-    for _ in range(args.c5_steps):
-        done += churn.step()
-        bt, ctx = churn.tables()
-        lens = churn.lengths()
-        bt_s.fill_(-1)
-        bt_s[:, :bt.shape[1]].copy_(bt)
-        ctx_s.copy_(ctx)
-        torch.cuda.synchronize(dev)
-        with torch.cuda.stream(stream):
+
+        def graph_us(fn):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for r in range(reps):
+                    fn(sets[r % len(sets)])
+            g.replay()
+            torch.cuda.synchronize(dev)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
-            graph.replay()
+            for _ in range(4):
+                g.replay()
             e1.record(stream)
             torch.cuda.synchronize(dev)
-            times.append(e0.elapsed_time(e1) * 1e-3)
-            e0.record(stream)
-            attn(bt, ctx)
-            e1.record(stream)
-            torch.cuda.synchronize(dev)
-            eager.append(e0.elapsed_time(e1) * 1e-3)
-        byts.append(sum(2 * n * 8 * 128 * 2 for n in lens) + 2 * 256 * 32 * 128 * 2)
-    t = statistics.median(times)
-    gbs = statistics.median([b / x / 1e9 for b, x in zip(byts, times)])
-    return {"metric": "C5 ragged churn decode attention GB/s per step", "workload": "c5",
-            "value": round(gbs, 1), "unit": "GB/s", "dtype": "f16",
-            "config": {"live_seqs": 256, "lengths": "LogNormal(ln 1024, 1.0) cap 16384",
+            return e0.elapsed_time(e1) * 1e3 / (4 * reps)
+        t_attn, t_walk = graph_us(attn), graph_us(walk)
+        e_attn = measure(lambda: [attn(sets[i % len(sets)]) for i in range(reps)]) / reps * 1e6
+        e_walk = measure(lambda: [walk(sets[i % len(sets)]) for i in range(reps)]) / reps * 1e6
+    if args.copy_calibration:
+        src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(7)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
+    attended = [min(n, w) + min(ns, max(n - w, 0)) for n in wl.C4_LENGTHS]
+    byts = sum(2 * a * 8 * 128 * 2 for a in attended) + 2 * 4 * 32 * 128 * 2
+    return {"metric": "C4 long-context windowed decode attention GB/s (attended bytes)",
+            "workload": "c4", "value": round(byts / (t_attn * 1e-6) / 1e9, 1), "unit": "GB/s",
+            "dtype": "bf16", "config": {"lengths": wl.C4_LENGTHS, "window": w, "sinks": ns,
+                                        "heads": "32/8", "head_dim": 128,
+                                        "launch": "hip graph of back-to-back launches",
+                                        "pools_rotated": args.pools},
+            "attention_us": round(t_attn, 2), "walk_us": round(t_walk, 2),
+            "walk_gbps": round(byts / (t_walk * 1e-6) / 1e9, 1),
+            "walk_frac": round(byts / (t_walk * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "eager_attention_us": round(e_attn, 2), "eager_walk_us": round(e_walk, 2),
+            "attended_bytes": byts, "traffic": read_traffic("c4")}
+
+
+def bench_c5(args, iva, torch, dev):
+    """C5: ragged continuous-batching churn, fp16, GQA 32/8, D 128: 256 live sequences of
+    total length LogNormal(ln 1024, sigma 1) capped at 16k, the last U{1..256} tokens
+    decoded one per step after 512-token prefill chunks, completed sequences replaced
+    (LIFO page reuse), every sequence starting at a random point of its lifetime
+    (workloads.ChurnBatch).  A step appends every prefill chunk (ivakv_append), runs the
+    chunks' causal attention over their pages (ivakv_prefill_attn) and the decode step of
+    every decoding sequence (append + attention, ivakv_decode_append_attn).  Each of the
+    three is timed on the GPU as back-to-back replays of its captured HIP graph, with
+    the step's inputs already on the device; the step time is their sum."""
+    from importlib import import_module
+    pc = import_module("iva_amd.paged_cache")
+    wl = iva.workloads
+    hq, hkv, d, sc = 32, 8, 128, 128 ** -0.5
+    pool = pc.PagedKVPool(64000, hkv, d, 16, 1, torch.float16, dev, max_seqs=512,
+                          max_blocks_per_seq=1024)
+    churn = wl.ChurnBatch(pool, n_seqs=256, seed=0, scale=sc)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    rnd = lambda *shape: (torch.randn(*shape, generator=gen, device=dev) * sc).half()
+    ws = torch.empty(iva.decode_workspace_bytes(256, hq, hkv, d, 16, pool.max_blocks),
+                     dtype=torch.uint8, device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    reps = 5
+    rows = {k: [] for k in ("append_us", "prefill_us", "decode_us", "step_us", "chunk_tok",
+                            "decode_seqs", "decode_bytes", "append_bytes", "prefill_flop",
+                            "completed", "mean_context")}
+    for step in range(5 + args.c5_steps):
+        plan = churn.plan_step()
+        pre_ids = [sid for sid, _ in plan["prefill"]]
+        n_chunk = len(plan["prefill_slots"])
+        dec_ids = plan["decode"]
+        kc, vc, qc = rnd(n_chunk, hkv, d), rnd(n_chunk, hkv, d), rnd(n_chunk, hq, d)
+        slots = torch.from_numpy(plan["prefill_slots"]).to(dev)
+        qs = torch.tensor(list(itertools.accumulate([n for _, n in plan["prefill"]],
+                                                    initial=0)), dtype=torch.int32, device=dev)
+        bt_p, ctx_p = churn.tables(pre_ids) if pre_ids else (None, None)
+        bt_d, ctx_d = churn.tables(dec_ids)
+        qd, kd, vd = rnd(len(dec_ids), hq, d), rnd(len(dec_ids), hkv, d), rnd(len(dec_ids), hkv, d)
+        out_d = torch.empty_like(qd)
+        max_chunk = max((n for _, n in plan["prefill"]), default=0)
+        out_p = torch.empty_like(qc)
+        ops = {"append": lambda: iva.kv_append(kc, vc, pool.k_pools[0], pool.v_pools[0], slots),
+               "prefill": lambda: iva.paged_prefill_attention(
+                   qc, pool.k_pools[0], pool.v_pools[0], bt_p, ctx_p, qs,
+                   max_query_len=max_chunk, out=out_p),
+               "decode": lambda: iva.paged_decode_append_attention(
+                   qd, kd, vd, pool.k_pools[0], pool.v_pools[0], bt_d, ctx_d, out=out_d,
+                   workspace=ws)}
+        if not n_chunk:
+            del ops["append"], ops["prefill"]
+        # Each op is captured as a HIP graph, replayed once (the step), then replayed
+        # back to back for its GPU time: the ops are idempotent (the same rows to the
+        # same slots; attention rewrites its output), so the replays leave the step's
+        # state as one run does.
+        t_op = {}
+        stream.wait_stream(torch.cuda.current_stream(dev))   # the step's inputs
+        with torch.cuda.stream(stream):
+            graphs = {}
+            for name, fn in ops.items():
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=stream):
+                    fn()
+                graphs[name] = g
+            for g in graphs.values():
+                g.replay()
+            for name, g in graphs.items():
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(reps):
+                    g.replay()
+                e1.record(stream)
+                torch.cuda.synchronize(dev)
+                t_op[name] = e0.elapsed_time(e1) * 1e3 / reps
+        del graphs
+        dec_lens = churn.lengths(dec_ids)
+        pre_lens = churn.lengths(pre_ids)
+        done = churn.finish_step()
+        if step < 5:
+            continue
+        rows["append_us"].append(t_op.get("append", 0.0))
+        rows["prefill_us"].append(t_op.get("prefill", 0.0))
+        rows["decode_us"].append(t_op["decode"])
+        rows["step_us"].append(sum(t_op.values()))
+        rows["chunk_tok"].append(n_chunk)
+        rows["decode_seqs"].append(len(dec_ids))
+        rows["decode_bytes"].append(sum(2 * n * hkv * d * 2 for n in dec_lens)
+                                    + 2 * len(dec_ids) * hq * d * 2)
+        rows["append_bytes"].append(4 * n_chunk * hkv * d * 2 + 4 * n_chunk)
+        rows["prefill_flop"].append(sum(4 * d * hq * sum(range(L - n + 1, L + 1))
+                                        for (_, n), L in zip(plan["prefill"], pre_lens)))
+        rows["completed"].append(done)
+        rows["mean_context"].append(statistics.mean(churn.lengths()))
+    med = lambda k: statistics.median(rows[k])
+    dec_gbs = statistics.median([b / (x * 1e-6) / 1e9 for b, x in zip(rows["decode_bytes"], rows["decode_us"])])
+    app_gbs = statistics.median([b / (x * 1e-6) / 1e9 for b, x in zip(rows["append_bytes"], rows["append_us"]) if x > 0])
+    pre_tf = statistics.median([f / (x * 1e-6) / 1e12 for f, x in zip(rows["prefill_flop"], rows["prefill_us"]) if x > 0])
+    return {"metric": "C5 ragged churn: decode step (append + attention) GB/s per step",
+            "workload": "c5", "value": round(dec_gbs, 1), "unit": "GB/s", "dtype": "f16",
+            "config": {"live_seqs": 256, "lengths": "total LogNormal(ln 1024, 1.0) capped 16384",
+                       "generated": "U{1..256} tokens per sequence, one per step",
                        "prefill_chunk": 512, "steps": args.c5_steps, "heads": "32/8",
-                       "launch": "hip graph of the attention call, tables copied in per step"},
-            "attention_us_median": round(t * 1e6, 2),
-            "eager_attention_us_median": round(statistics.median(eager) * 1e6, 2),
-            "completed_sequences": done,
-            "mean_context": round(statistics.mean(churn.lengths()), 1),
+                       "head_dim": 128,
+                       "launch": "each op a HIP graph replayed back to back, inputs on the device"},
+            "step_us_median": round(med("step_us"), 1),
+            "steps_per_s": round(1e6 / med("step_us"), 1),
+            "decode_us_median": round(med("decode_us"), 1),
+            "decode_seqs_median": med("decode_seqs"),
+            "append_us_median": round(med("append_us"), 1),
+            "append_gbps": round(app_gbs, 1),
+            "prefill_us_median": round(med("prefill_us"), 1),
+            "prefill_tflops": round(pre_tf, 1),
+            "prefill_chunk_tokens_median": med("chunk_tok"),
+            "completions_per_step_mean": round(statistics.mean(rows["completed"]), 2),
+            "steps_with_completions": sum(1 for c in rows["completed"] if c),
+            "mean_context": round(statistics.mean(rows["mean_context"]), 1),
+            "lognormal_mean": round(churn.lognormal_mean(), 1),
             "free_pages_left": pool.num_free_pages}
 
 
@@ -763,7 +937,7 @@ def main():
     wl = iva.workloads
     if args.workload != "c2":
         fn = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "prefill": bench_prefill,
-              "c2fp8": bench_c2fp8, "ops": bench_ops}[args.workload]
+              "c2fp8": bench_c2fp8, "ops": bench_ops, "ceiling": bench_ceiling}[args.workload]
         print(json.dumps(fn(args, iva, torch, dev)), flush=True)
         return
 
@@ -788,6 +962,7 @@ def main():
         t_ach = t_attn / (mt["walk_us"] * 1e-6) / 1e9
         target = {"context": 4096, "batch": batch, "kernel_us": round(mt["walk_us"], 3),
                   "achieved": round(t_ach, 1), "frac": round(t_ach / HBM_PEAK_GBS, 4),
+                  "frac_of_measured_tile_read_ceiling": None,
                   "algorithmic_bytes": t_attn, "attention_us": round(mt["attn_us"], 3),
                   "step_us": round(mt["step_ms"] * 1e3, 3),
                   "step_gbs": round((t_append + t_attn) / (mt["step_ms"] * 1e-3) / 1e9, 1),
@@ -798,6 +973,11 @@ def main():
         for _ in range(10):
             dst.copy_(src)
         torch.cuda.synchronize(dev)
+
+    ceiling = None
+    if not args.copy_calibration and not args.eager:
+        torch.cuda.empty_cache()
+        ceiling = measure_ceiling(torch, dev)
 
     append_b, attn_b = algorithmic_bytes(lengths, hq, hkv, d, esize)
     step_s = step_ms * 1e-3
@@ -819,6 +999,9 @@ def main():
 
     walk_name = (f"{WALK_KERNEL}<f16,128>" if not args.partition_pages
                  else "decode_partial_kernel<f16,128>")
+    if target is not None and ceiling is not None:
+        target["frac_of_measured_tile_read_ceiling"] = round(
+            target["achieved"] / ceiling["tile_read_gbs"], 4)
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -844,7 +1027,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "kernel": walk_name,
-                     "kernel_us": round(walk_us, 3), "algorithmic_bytes": attn_b},
+                     "kernel_us": round(walk_us, 3), "algorithmic_bytes": attn_b,
+                     "frac_of_measured_tile_read_ceiling":
+                         round(achieved / ceiling["tile_read_gbs"], 4) if ceiling else None},
+        "ceiling": ceiling,
         "cpu_baseline": cpu,
         "tokens_per_s": round(batch / step_s, 1),
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),

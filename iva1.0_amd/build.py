@@ -36,12 +36,23 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+CEILING_SRC = PKG_DIR / "bench_kernels" / "ivakv_ceiling.hip"
+CEILING_LIB = PKG_DIR / "libivakv_ceiling.so"
+
+
 def build(verbose: bool = False) -> Path:
-    """Compiles all HIP sources into ``libivakv.so``; returns its path."""
+    """Compiles all HIP sources into ``libivakv.so`` (and the read-ceiling kernels of
+    ``bench.py --workload ceiling`` into ``libivakv_ceiling.so``); returns the main path."""
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    tmp = LIB_PATH.with_name(LIB_NAME + f".tmp{os.getpid()}")
+    _compile(srcs, LIB_PATH, verbose)
+    _compile([CEILING_SRC], CEILING_LIB, verbose)
+    return LIB_PATH
+
+
+def _compile(srcs, lib_path: Path, verbose: bool) -> None:
+    tmp = lib_path.with_name(lib_path.name + f".tmp{os.getpid()}")
     cmd = [
         hipcc_path(),
         f"--offload-arch={OFFLOAD_ARCH}",
@@ -64,8 +75,7 @@ def build(verbose: bool = False) -> Path:
     if proc.returncode != 0:
         tmp.unlink(missing_ok=True)
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, lib_path)
 
 
 def kernel_resource_usage(srcs=None) -> dict:

@@ -13,9 +13,11 @@ so the oracle and the GPU path see identical bits; the bench draws on the GPU).
       block tables are a seeded page permutation.
   C4  long-context decode, bf16: 4 sequences of 32k/64k/96k/128k tokens, window
       4096 + 4 sinks, 32/8 heads, head_dim 128, K/V ~ N(0, 1).
-  C5  ragged churn, fp16: 256 sequences, lengths LogNormal(ln 1024, sigma=1.0)
-      capped at 16384 (sigma is not given by the config; 1.0 is stated here),
-      block tables fragmented by LIFO free-list reuse (see PagedKVPool).
+  C5  ragged churn, fp16: 256 live sequences, total lengths LogNormal(ln 1024,
+      sigma=1.0) capped at 16384 (sigma is not given by the config; 1.0 is stated
+      here), the last Uniform{1..256} tokens decoded one per step after 512-token
+      prefill chunks, completed sequences replaced; block tables fragmented by LIFO
+      free-list reuse (see PagedKVPool and ChurnBatch).
 """
 from __future__ import annotations
 
@@ -23,6 +25,7 @@ import math
 from dataclasses import dataclass
 from typing import List, Optional
 
+import numpy as np
 import torch
 
 from .ops import pool_shapes
@@ -159,80 +162,135 @@ def c5_lengths(seed: int, n_seqs: int = 256, median: int = 1024, sigma: float = 
 
 
 class ChurnBatch:
-    """Config C5 driver: continuous batching over a PagedKVPool (one layer, fp16,
-    GQA 32/8, head_dim 128 by default).
+    """Config C5 driver: continuous batching over a PagedKVPool (one layer).
 
-    ``n_seqs`` sequences are live at any time, each with a target length drawn from
-    LogNormal(ln median, sigma) capped at ``cap``.  A new sequence is prefilled in
-    ``chunk``-token appends; every step appends one decode token to each live
-    sequence; a sequence that reaches its target completes, its pages go back to
-    the LIFO free list and a new sequence takes its block-table row, reusing those
-    pages, so block tables become fragmented.  K/V rows are drawn from a seeded
-    device generator; the host keeps the lengths.
+    Every live sequence has a total length T ~ LogNormal(ln median, sigma) capped at
+    ``cap``.  Its last G ~ Uniform{1, ..., gen_max} tokens (at most T - 1) are generated
+    one per step; the first P = T - G are its prompt, appended ``chunk`` tokens per step
+    (chunked prefill).  A sequence whose length reaches T completes: its pages go back
+    to the pool's LIFO free list and a new sequence (length 0, in prefill) takes its
+    block-table row and, through the free list, its pages, so tables fragment.  At
+    construction every sequence is placed at a uniformly random step of its lifetime
+    and the rows it would hold by then are written: the batch starts in steady state,
+    and prefill chunks, decode tokens and completions occur on (almost) every step.
+
+    :meth:`plan_step` does the host bookkeeping of one step (allocates its slots) and
+    returns what the step appends; :meth:`finish_step` retires completed sequences.
+    K/V rows come from a seeded device generator.
     """
 
     def __init__(self, pool, n_seqs: int = 256, median: int = 1024, sigma: float = 1.0,
-                 cap: int = 16384, chunk: int = 512, seed: int = 0, scale: float = 1.0):
+                 cap: int = 16384, chunk: int = 512, gen_max: int = 256, seed: int = 0,
+                 scale: float = 1.0, fill: bool = True):
         self.pool = pool
-        self.n_seqs, self.median, self.sigma, self.cap, self.chunk = n_seqs, median, sigma, cap, chunk
-        self.scale = scale
+        self.n_seqs, self.median, self.sigma, self.cap = n_seqs, median, sigma, cap
+        self.chunk, self.gen_max, self.scale = chunk, gen_max, scale
         self.gen = torch.Generator().manual_seed(seed)
-        self.dev_gen = torch.Generator(device=pool.device).manual_seed(seed + 1)
-        self.ids = []
-        self.targets = {}
+        self.dev_gen = (torch.Generator(device=pool.device).manual_seed(seed + 1)
+                        if fill else None)
+        self.ids: List = []
+        self.target: dict = {}
+        self.prompt: dict = {}
+        self.completed = 0
         self._next = 0
+        starts = []
         for _ in range(n_seqs):
-            self._start()
+            sid = self._start()
+            t, p = self.target[sid], self.prompt[sid]
+            n_pre = math.ceil(p / chunk)
+            life = n_pre + (t - p)
+            s_ = int(torch.randint(0, life, (1,), generator=self.gen))
+            n0 = min(s_ * chunk, p) if s_ < n_pre else p + (s_ - n_pre)
+            starts.append((sid, n0))
+        # The rows each sequence holds by now, allocated a page at a time in rounds over
+        # the batch (in a shuffled order each round), as their growth would have
+        # interleaved: the tables are fragmented from the first step.
+        left = {sid: n0 for sid, n0 in starts}
+        got = {sid: [] for sid, _ in starts}
+        while left:
+            order = list(left)
+            perm = torch.randperm(len(order), generator=self.gen).tolist()
+            for j in perm:
+                sid = order[j]
+                n = min(self.pool.block_size, left[sid])
+                got[sid].append(self.pool.allocate(sid, n))
+                left[sid] -= n
+                if left[sid] == 0:
+                    del left[sid]
+        if fill:
+            self._write(np.concatenate([np.concatenate(v) for v in got.values() if v]))
 
-    def _draw_length(self) -> int:
+    def _draw(self):
         z = torch.randn(1, generator=self.gen, dtype=torch.float64).item()
-        return int(max(1, min(self.cap, round(math.exp(math.log(self.median) + self.sigma * z)))))
+        t = int(max(2, min(self.cap, round(math.exp(math.log(self.median) + self.sigma * z)))))
+        g = int(torch.randint(1, self.gen_max + 1, (1,), generator=self.gen))
+        return t, t - min(g, t - 1)
 
-    def _rows(self, n: int):
-        shape = (n, self.pool.num_kv_heads, self.pool.head_dim)
-        k = torch.randn(shape, generator=self.dev_gen, device=self.pool.device) * self.scale
-        v = torch.randn(shape, generator=self.dev_gen, device=self.pool.device) * self.scale
-        return k.to(self.pool.dtype), v.to(self.pool.dtype)
-
-    def _append(self, sid, n: int) -> None:
-        from .ops import kv_append
-        slots = torch.from_numpy(self.pool.allocate(sid, n)).to(self.pool.device)
-        k, v = self._rows(n)
-        kv_append(k, v, self.pool.k_pools[0], self.pool.v_pools[0], slots)
-
-    def _start(self) -> None:
+    def _start(self):
         sid = ("c5", self._next)
         self._next += 1
-        target = self._draw_length()
+        self.target[sid], self.prompt[sid] = self._draw()
         self.pool.add_sequence(sid)
         self.ids.append(sid)
-        self.targets[sid] = target
-        prompt = max(1, target // 2)
-        for off in range(0, prompt, self.chunk):       # prefill-chunk appends
-            self._append(sid, min(self.chunk, prompt - off))
+        return sid
 
-    def step(self) -> int:
-        """One decode step: one token appended to every live sequence (a single append
-        launch), completed sequences freed and replaced by new, chunk-prefilled ones.
-        Returns how many sequences completed."""
-        import numpy as np
+    def _rows(self, n: int, heads: int):
+        shape = (n, heads, self.pool.head_dim)
+        return (torch.randn(shape, generator=self.dev_gen, device=self.pool.device)
+                * self.scale).to(self.pool.dtype)
+
+    def _write(self, slots) -> None:
         from .ops import kv_append
-        slots = np.concatenate([self.pool.allocate(sid, 1) for sid in self.ids])
-        k, v = self._rows(len(self.ids))
-        kv_append(k, v, self.pool.k_pools[0], self.pool.v_pools[0],
-                  torch.from_numpy(slots).to(self.pool.device))
-        finished = [sid for sid in self.ids if self.pool.length(sid) >= self.targets[sid]]
-        for sid in finished:
+        for lo in range(0, len(slots), 1 << 16):
+            sl = torch.from_numpy(np.ascontiguousarray(slots[lo:lo + (1 << 16)])).to(self.pool.device)
+            hkv = self.pool.num_kv_heads
+            kv_append(self._rows(len(sl), hkv), self._rows(len(sl), hkv), self.pool.k_pools[0],
+                      self.pool.v_pools[0], sl)
+
+    def plan_step(self) -> dict:
+        """Allocates this step's slots: a chunk of up to ``chunk`` prompt tokens for every
+        sequence still in prefill, one token for every sequence in decode.  Returns host
+        lists: ``prefill`` [(sid, n)], ``prefill_slots`` (int32, the chunks' slots in
+        order), ``decode`` [sid] (their new token is the last position of the updated
+        lengths)."""
+        prefill, pre_slots, decode = [], [], []
+        for sid in self.ids:
+            n_now, p = self.pool.length(sid), self.prompt[sid]
+            if n_now < p:
+                n = min(self.chunk, p - n_now)
+                pre_slots.append(self.pool.allocate(sid, n))
+                prefill.append((sid, n))
+            else:
+                self.pool.allocate(sid, 1)
+                decode.append(sid)
+        slots = np.concatenate(pre_slots) if pre_slots else np.zeros(0, dtype=np.int32)
+        return {"prefill": prefill, "prefill_slots": slots.astype(np.int32), "decode": decode}
+
+    def finish_step(self) -> int:
+        """Retires the sequences that reached their length and starts new ones in their
+        rows; returns how many completed."""
+        done = [sid for sid in self.ids if self.pool.length(sid) >= self.target[sid]]
+        for sid in done:
             self.pool.free(sid)
             self.ids.remove(sid)
-            del self.targets[sid]
-        for _ in finished:
+            del self.target[sid], self.prompt[sid]
+        for _ in done:
             self._start()
-        return len(finished)
+        self.completed += len(done)
+        return len(done)
 
-    def tables(self):
-        """Device block tables and context lengths of the live sequences."""
-        return self.pool.device_tables(self.ids)
+    def lengths(self, ids=None) -> List[int]:
+        return [self.pool.length(s) for s in (self.ids if ids is None else ids)]
 
-    def lengths(self):
-        return [self.pool.length(s) for s in self.ids]
+    def tables(self, ids=None):
+        """Device block tables and context lengths of ``ids`` (default: all live)."""
+        return self.pool.device_tables(self.ids if ids is None else ids)
+
+    def lognormal_mean(self) -> float:
+        """Mean of the stated length distribution (LogNormal(ln median, sigma) capped at
+        cap), by quadrature of the capped distribution."""
+        mu, s = math.log(self.median), self.sigma
+        z = torch.linspace(-8, 8, 20001, dtype=torch.float64)
+        w = torch.exp(-0.5 * z * z)
+        x = torch.exp(mu + s * z).clamp(max=self.cap)
+        return float((w * x).sum() / w.sum())

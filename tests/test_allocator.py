@@ -229,3 +229,36 @@ def test_generation_moves_with_every_table_change(iva):
     assert bumped()
     p.load_state_dict(p.state_dict())
     assert bumped()
+
+
+def test_churn_driver_reaches_steady_state(iva):
+    """The C5 driver's host bookkeeping (no device storage): sequences start at random
+    points of their lifetimes, so from the first step on prefill chunks (<= 512 tokens,
+    never past the prompt), decode tokens and completions all occur; lengths never pass
+    their targets; completed sequences' pages return and are reused (fragmented tables)."""
+    from importlib import import_module
+    pc = import_module("iva_amd.paged_cache")
+    wl = import_module("iva_amd.workloads")
+    pool = pc.PagedKVPool(64000, 8, 128, 16, 1, allocate_storage=False, device="cpu",
+                          max_seqs=512, max_blocks_per_seq=1024)
+    churn = wl.ChurnBatch(pool, n_seqs=256, seed=0, fill=False)
+    steps, done, n_pre, n_dec = 40, [], [], []
+    for _ in range(steps):
+        plan = churn.plan_step()
+        assert all(0 < n <= 512 for _, n in plan["prefill"])
+        assert len(plan["prefill_slots"]) == sum(n for _, n in plan["prefill"])
+        assert len(plan["prefill"]) + len(plan["decode"]) == 256
+        for sid, _ in plan["prefill"]:
+            assert pool.length(sid) <= churn.prompt[sid]
+        for sid in churn.ids:
+            assert pool.length(sid) <= churn.target[sid]
+        n_pre.append(len(plan["prefill"]))
+        n_dec.append(len(plan["decode"]))
+        done.append(churn.finish_step())
+    assert min(n_pre) > 0 and min(n_dec) > 0
+    assert sum(done) >= steps               # about two completions per step
+    assert sum(1 for d in done if d > 0) >= steps * 0.7
+    assert 1600 < churn.lognormal_mean() < 1700   # E[LogNormal(ln 1024, 1)] = 1688, capped
+    for ids in (churn.ids[:64], churn.ids[-64:]):   # the oldest and the newest sequences
+        bt, _ = pool.tables(ids)
+        assert (np.diff(bt[:, :4], axis=1) != 1).mean() > 0.3
