@@ -330,16 +330,22 @@ def test_context_beyond_block_table(iva, dev):
 
 
 def test_workspace_reuse_across_calls(iva, dev):
-    """One workspace serves alternating batches of different shapes; results stay exact."""
+    """One workspace, filled with garbage (it needs no initialisation), serves alternating
+    batches of different shapes through both walks (stream walk and 8-page partitions);
+    results stay exact."""
     a = iva.workloads.decode_batch([3000, 700, 16, 2500], 32, 8, 128, torch.float16, seed=21,
                                    scale=128 ** -0.5)
     b = iva.workloads.decode_batch([900, 4000], 32, 8, 128, torch.float16, seed=22,
                                    scale=128 ** -0.5)
-    ws = torch.full((1 << 22,), 0x7F, dtype=torch.uint8, device=dev)  # needs no initialisation
+    need = max(iva.decode_workspace_bytes(len(d["lengths"]), 32, 8, 128, 16,
+                                          d["layout"].block_tables.shape[1], partition_pages=pp)
+               for d in (a, b) for pp in (0, 8))
+    ws = torch.full((need,), 0x7F, dtype=torch.uint8, device=dev)
     for _ in range(3):
-        for d in (a, b):
-            out = run_gpu(iva, dev, d, workspace=ws, partition_pages=8)
-            assert_close(out, oracle_out(d), torch.float16, rel_ulp=False, what="workspace reuse")
+        for d, pp in ((a, 8), (b, 0), (a, 0), (b, 8)):
+            out = run_gpu(iva, dev, d, workspace=ws, partition_pages=pp)
+            assert_close(out, oracle_out(d), torch.float16, rel_ulp=False,
+                         what=f"workspace reuse, partition_pages {pp}")
 
 
 @pytest.mark.parametrize("lengths", [
