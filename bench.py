@@ -348,8 +348,20 @@ def bench_c3(args, iva, torch, dev):
             dev, torch.bfloat16).eval()
         ref.load_state_dict(model.state_dict())
         tokens_torch = ref.generate(prompts, max_length=256, do_sample=False, eos_token_id=None)
-    same = (tokens_paged == tokens_torch)[:, 512:]
-    first_diff = [int((~row).nonzero()[0]) if (~row).any() else 256 for row in same.cpu()]
+        same = (tokens_paged == tokens_torch)[:, 512:]
+        first_diff = [int((~row).nonzero()[0]) if (~row).any() else 256 for row in same.cpu()]
+        # The torch backend's top-2 logit margin where each sequence first diverges,
+        # teacher-forced along its own stream (one causal forward): a divergence is a
+        # near-tie when that margin is within twice the logits' bf16 agreement bound.
+        logits = ref(tokens_torch[:, :-1])["logits"]
+        margins = []
+        for b, s in enumerate(first_diff):
+            if s < 256:
+                top = logits[b, 511 + s].float().topk(2).values
+                margins.append(round(float(top[0] - top[1]), 4))
+            else:
+                margins.append(None)
+        del logits
     weight_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
     step_s = (t256 - t128) / 128
     return {
@@ -367,6 +379,9 @@ def bench_c3(args, iva, torch, dev):
         "weights_gbps_per_step": round(weight_bytes / step_s / 1e9, 1),
         "greedy_tokens_identical_to_torch_backend": int(same.all(dim=1).sum()),
         "first_divergence_per_seq": first_diff,
+        "torch_top2_margin_at_first_divergence": margins,
+        # twice the teacher-forced logit bound of tests/test_c3_model_gpu.py (0.09375)
+        "near_tie_margin": 0.1875,
     }
 
 
