@@ -74,8 +74,9 @@ __global__ __launch_bounds__(256) void rope_kernel(E* x, int64_t ts, int64_t hs,
   rotate_pair(row[2 * i], row[2 * i + 1], c, s);
 }
 
-// Paged append with K rotated: one thread per (token, group of up to four kv heads,
-// 16-byte chunk), the chunk's pairs rotated before the store.
+// Paged append with K rotated: one thread per (token, group of up to eight kv heads,
+// 16-byte chunk), the chunk's pairs rotated before the store.  Sources and pools that
+// allow it (16-byte aligned rows) move whole 16-byte chunks (VEC).
 struct AppendRopeArgs {
   const void* k_new;
   const void* v_new;
@@ -91,9 +92,9 @@ struct AppendRopeArgs {
 
 // Lanes rotate up to kRopeHeads kv heads of one (token, chunk): cos / sin depend on the
 // position and the pair only, so they are computed once per lane, not once per head.
-constexpr int kRopeHeads = 4;
+constexpr int kRopeHeads = 8;
 
-template <typename E>
+template <typename E, bool VEC>
 __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
   constexpr int X = 16 / sizeof(E);
   const int nch = a.D / X;
@@ -121,14 +122,29 @@ __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
   const E* __restrict__ vb = static_cast<const E*>(a.v_new) + t * a.vts + (int64_t)c * X;
   E* __restrict__ kp = static_cast<E*>(a.k_pool);
   E* __restrict__ vp = static_cast<E*>(a.v_pool);
+  union Row {
+    Chunk16 c;
+    E e[X];
+  };
   E k[kRopeHeads][X], v[kRopeHeads][X];
 #pragma unroll
   for (int u = 0; u < kRopeHeads; ++u) {
     if (u < nh) {
+      if constexpr (VEC) {  // 16-byte source chunks
+        Row rk, rv;
+        rk.c = *reinterpret_cast<const Chunk16*>(kb + (h0 + u) * a.khs);
+        rv.c = *reinterpret_cast<const Chunk16*>(vb + (h0 + u) * a.vhs);
 #pragma unroll
-      for (int j = 0; j < X; ++j) {
-        k[u][j] = kb[(h0 + u) * a.khs + j];
-        v[u][j] = vb[(h0 + u) * a.vhs + j];
+        for (int j = 0; j < X; ++j) {
+          k[u][j] = rk.e[j];
+          v[u][j] = rv.e[j];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < X; ++j) {
+          k[u][j] = kb[(h0 + u) * a.khs + j];
+          v[u][j] = vb[(h0 + u) * a.vhs + j];
+        }
       }
     }
   }
@@ -144,11 +160,17 @@ __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
       const int64_t head_base = page * a.Hkv + h0 + u;
       E* kd = kp + ((head_base * nch + c) * a.bs + off) * X;
       E* vd = vp + head_base * a.D * a.bs + (int64_t)c * X * a.bs + off;
+      if constexpr (VEC) {
+        Row rk;
 #pragma unroll
-      for (int j = 0; j < X; ++j) {
-        kd[j] = k[u][j];
-        vd[(int64_t)j * a.bs] = v[u][j];
+        for (int j = 0; j < X; ++j) rk.e[j] = k[u][j];
+        *reinterpret_cast<Chunk16*>(kd) = rk.c;
+      } else {
+#pragma unroll
+        for (int j = 0; j < X; ++j) kd[j] = k[u][j];
       }
+#pragma unroll
+      for (int j = 0; j < X; ++j) vd[(int64_t)j * a.bs] = v[u][j];
     }
   }
 }
@@ -239,10 +261,24 @@ extern "C" int ivakv_append_rope(const void* k_new, const void* v_new, int64_t k
   const int64_t total = (int64_t)cdiv(n_tok, 16) * 16 * cdiv(num_kv_heads, kRopeHeads) * (head_dim / X);
   const int64_t blocks = (total + 255) / 256;
   if (blocks > kMaxGridR) return fail(IVAKV_E_SHAPE, "%s: too many rows", name);
+  // 16-byte K / V chunk accesses when every source row and the pools allow them
+  const bool vec = aligned16(k_new) && aligned16(v_new) && aligned16(k_pool) && aligned16(v_pool) &&
+                   (k_tok_stride % X == 0) && (k_head_stride % X == 0) &&
+                   (v_tok_stride % X == 0) && (v_head_stride % X == 0);
+  const unsigned g = (unsigned)blocks;
   switch (dtype) {
-    case IVAKV_F16: append_rope_kernel<_Float16><<<(unsigned)blocks, 256, 0, stream>>>(a); break;
-    case IVAKV_BF16: append_rope_kernel<__bf16><<<(unsigned)blocks, 256, 0, stream>>>(a); break;
-    default: append_rope_kernel<float><<<(unsigned)blocks, 256, 0, stream>>>(a); break;
+    case IVAKV_F16:
+      if (vec) append_rope_kernel<_Float16, true><<<g, 256, 0, stream>>>(a);
+      else append_rope_kernel<_Float16, false><<<g, 256, 0, stream>>>(a);
+      break;
+    case IVAKV_BF16:
+      if (vec) append_rope_kernel<__bf16, true><<<g, 256, 0, stream>>>(a);
+      else append_rope_kernel<__bf16, false><<<g, 256, 0, stream>>>(a);
+      break;
+    default:
+      if (vec) append_rope_kernel<float, true><<<g, 256, 0, stream>>>(a);
+      else append_rope_kernel<float, false><<<g, 256, 0, stream>>>(a);
+      break;
   }
   return launch_status(name);
 }

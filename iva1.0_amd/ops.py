@@ -103,6 +103,13 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+def _capturing(dev: torch.device) -> bool:
+    """True while the device's current stream is being captured into a HIP graph, when
+    no host read of device data is allowed (the kernels' own bounds checks then stand)."""
+    with torch.cuda.device(dev):
+        return torch.cuda.is_current_stream_capturing()
+
+
 def _i32(t: torch.Tensor, name: str) -> torch.Tensor:
     if t.dtype != torch.int32:
         raise TypeError(f"{name} must be int32, got {t.dtype}")
@@ -500,6 +507,9 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
     if query_start.numel() != batch + 1:
         raise ValueError(f"query_start must have B+1 = {batch + 1} entries")
     if max_query_len is None:
+        if _capturing(dev):
+            raise ValueError("max_query_len is required under HIP-graph capture (the host "
+                             "cannot read query_start then)")
         qs = query_start.tolist()
         if qs[0] != 0 or qs[-1] != q.shape[0] or any(b < a for a, b in zip(qs, qs[1:])):
             raise ValueError(f"query_start must rise from 0 to n_tok = {q.shape[0]}; got "
@@ -551,15 +561,15 @@ def copy_pages(k_pool: torch.Tensor, v_pool: torch.Tensor, src_pages: torch.Tens
                v_scale: Optional[torch.Tensor] = None) -> None:
     """Moves pages ``src_pages[i] -> dst_pages[i]`` (int32, disjoint sets) of a pool pair,
     with the FP8 scaling factors when the pools are FP8.  Every id must lie in
-    ``[0, num_pages)`` (checked here, with one device read; the kernel also skips a move
-    outside the pool)."""
+    ``[0, num_pages)``: checked here with one device read (``IndexError``), except under
+    HIP-graph capture, where the kernel's own check skips a move outside the pool."""
     dev = _require_gpu(k_pool, v_pool, src_pages, dst_pages)
     num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
     src = _i32(src_pages, "src_pages").reshape(-1)
     dst = _i32(dst_pages, "dst_pages").reshape(-1)
     if src.numel() != dst.numel():
         raise ValueError("src_pages and dst_pages differ in length")
-    if src.numel():
+    if src.numel() and not _capturing(dev):
         ids = torch.cat([src, dst])
         lo, hi = (int(v) for v in torch.stack([ids.min(), ids.max()]).tolist())
         if lo < 0 or hi >= num_pages:
@@ -640,7 +650,9 @@ def _kv_ops(kv_cache: torch.Tensor, indices: torch.Tensor, values: Optional[torc
     batch, n_heads, seq_len, head_dim = kv_cache.shape
     idx = indices.reshape(-1).to(torch.int64).contiguous()
     n_idx = idx.numel()
-    if n_idx and bool(((idx < 0) | (idx >= seq_len)).any()):
+    # Under HIP-graph capture the host cannot read the indices; the kernel then gathers
+    # zeros for, and does not scatter, an out-of-range index.
+    if n_idx and not _capturing(dev) and bool(((idx < 0) | (idx >= seq_len)).any()):
         raise IndexError(f"kv_ops index out of range for sequence length {seq_len}")
     code = dtype_code(kv_cache.dtype)
     if operation == "gather":

@@ -55,3 +55,29 @@ def test_out_of_range_index_raises(iva, dev):
         iva.kv_ops(kv, torch.tensor([8], device=dev), operation="gather")
     with pytest.raises(IndexError):
         iva.kv_ops(kv, torch.tensor([-1], device=dev), torch.zeros(1, 1, 1, 16, device=dev), "scatter")
+
+
+def test_kv_ops_in_a_hip_graph(iva, dev):
+    """kv_ops captured into a HIP graph (no host read of the indices then): every replay,
+    with new cache contents written eagerly between replays, equals the eager op; an
+    out-of-range index gathers zeros and is not scattered."""
+    g = torch.Generator().manual_seed(7)
+    kv = torch.randn(2, 3, 24, 64, generator=g).half().to(dev)
+    idx = torch.tensor([5, 23, 0, 40, 11], device=dev)   # 40 is outside S = 24
+    vals = torch.randn(2, 3, 5, 64, generator=g).half().to(dev)
+    ok = torch.tensor([True, True, True, False, True], device=dev)
+    iva.kv_ops(kv, idx[ok], operation="gather")          # warm-up outside the capture
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gathered = iva.kv_ops(kv, idx, operation="gather")
+        scattered = iva.kv_ops(kv, idx, vals, operation="scatter")
+    for rep in range(3):
+        kv.copy_(torch.randn(2, 3, 24, 64, generator=g).half().to(dev))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = torch.zeros_like(gathered)
+        want[:, :, ok] = iva.kv_ops(kv, idx[ok], operation="gather")
+        assert torch.equal(gathered.view(torch.int16), want.view(torch.int16)), f"replay {rep}"
+        want_s = iva.kv_ops(kv, idx[ok], vals[:, :, ok], operation="scatter")
+        assert torch.equal(scattered.view(torch.int16), want_s.view(torch.int16)), f"replay {rep}"

@@ -51,11 +51,13 @@ def test_rope_in_place_vs_oracle(iva, dev, dtype, d):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=str)
-@pytest.mark.parametrize("hkv,d", [(8, 64), (3, 128), (5, 64), (1, 128), (6, 256)])
-def test_append_rope_vs_oracle(iva, dev, dtype, hkv, d):
-    """Lanes rotate groups of up to four kv heads: head counts that are not a multiple
-    of four leave a partial last group.  A row with slot -1 and one past the pool are
-    skipped (pools keep the fill value)."""
+@pytest.mark.parametrize("hkv,d", [(8, 64), (3, 128), (5, 64), (1, 128), (6, 256), (12, 64)])
+@pytest.mark.parametrize("shift", [0, 1], ids=["aligned", "shifted"])
+def test_append_rope_vs_oracle(iva, dev, dtype, hkv, d, shift):
+    """Lanes rotate groups of up to eight kv heads: head counts that are not a multiple
+    of eight leave a partial last group.  A row with slot -1 and one past the pool are
+    skipped (pools keep the fill value).  Source rows shifted by one element are not
+    16-byte aligned and take the element-wise path; aligned rows move 16-byte chunks."""
     lengths = [7, 33, 20]
     lay = iva.workloads.permuted_layout(lengths, 12, torch.Generator().manual_seed(3))
     n = sum(lengths)
@@ -64,11 +66,19 @@ def test_append_rope_vs_oracle(iva, dev, dtype, hkv, d):
     v_new = torch.randn(n, hkv, d, generator=gen).to(dtype)
     slots = torch.cat([lay.slots(b, torch.arange(m)) for b, m in enumerate(lengths)])
     slots[5], slots[40] = -1, 12 * 16 + 3
+    k_src, v_src = k_new.to(dev), v_new.to(dev)
+    if shift:   # views starting one element into a wider buffer
+        kb = torch.zeros(n, hkv, d + 8, dtype=dtype, device=dev)
+        vb = torch.zeros(n, hkv, d + 8, dtype=dtype, device=dev)
+        k_src, v_src = kb[..., 1:d + 1], vb[..., 1:d + 1]
+        k_src.copy_(k_new.to(dev))
+        v_src.copy_(v_new.to(dev))
+        assert k_src.data_ptr() % 16 and v_src.data_ptr() % 16
     positions = torch.cat([torch.arange(m) + 1000 * b for b, m in enumerate(lengths)]).to(torch.int32)
     ks, vs = iva.pool_shapes(12, hkv, d, 16, dtype)
     kp = torch.full(ks, 3.0, dtype=dtype, device=dev)
     vp = torch.full(vs, 3.0, dtype=dtype, device=dev)
-    iva.kv_append(k_new.to(dev), v_new.to(dev), kp, vp, slots.to(dev),
+    iva.kv_append(k_src, v_src, kp, vp, slots.to(dev),
                   rope_positions=positions.to(dev), rope_theta=10000.0)
     # expected pools: the oracle append of the rotated K rows (rounded once), V as is
     k_rot = orc.rope(k_new.float().numpy(), positions.numpy(), 10000.0)
@@ -167,3 +177,30 @@ def test_kv_compact_vs_torch(iva, dev):
     bad[1, 5] = True
     with pytest.raises(ValueError, match="same mask"):
         iva.kv_compact(kv, bad.to(dev))
+
+
+def test_copy_pages_in_a_hip_graph(iva, dev):
+    """copy_pages captured into a HIP graph (no host read of the ids then): every replay,
+    from pools reset eagerly between replays, equals the eager moves; a move with an id
+    outside the pool is skipped by the kernel."""
+    ks, vs = iva.pool_shapes(16, 2, 64, 16, torch.float16)
+    k = torch.randn(ks, device=dev).half()
+    v = torch.randn(vs, device=dev).half()
+    src = torch.tensor([3, 7, 12, 1], dtype=torch.int32, device=dev)
+    dst = torch.tensor([0, 5, 20, 9], dtype=torch.int32, device=dev)   # 20 is outside
+    iva.copy_pages(k, v, src[[0, 1, 3]], dst[[0, 1, 3]])               # warm-up, eager
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        iva.copy_pages(k, v, src, dst)
+    for rep in range(3):
+        k0 = torch.randn(ks, device=dev).half()
+        v0 = torch.randn(vs, device=dev).half()
+        k.copy_(k0)
+        v.copy_(v0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want_k, want_v = k0.clone(), v0.clone()
+        want_k[[0, 5, 9]] = k0[[3, 7, 1]]
+        want_v[[0, 5, 9]] = v0[[3, 7, 1]]
+        assert torch.equal(k, want_k) and torch.equal(v, want_v), f"replay {rep}"
