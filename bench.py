@@ -34,6 +34,9 @@ Profiling helpers (no timing line):
                        and a WRITE_SIZE run (directory W) and writes
                        profiles/decode_attn_c2_traffic.json (with --context N:
                        profiles/decode_attn_ctxN_traffic.json).
+  --rdreq-dir R        with --summarize-pmc: a third run's TCC_EA0_RDREQ_{32B,64B,
+                       128B}_sum counts, which give the read bytes directly (no copy
+                       scale) as a cross-check of the scaled FETCH_SIZE.
 """
 from __future__ import annotations
 
@@ -47,6 +50,7 @@ import statistics
 import sys
 import time
 from pathlib import Path
+from typing import Optional
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
@@ -91,6 +95,9 @@ def parse_args():
                    help="launch a plain 256 MiB copy 10x after timing (counter calibration)")
     p.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="write the HBM traffic summary from two rocprofv3 --pmc runs")
+    p.add_argument("--rdreq-dir", default=None,
+                   help="with --summarize-pmc: a run of TCC_EA0_RDREQ_sum and its 32B / 64B / "
+                        "128B parts, for read bytes counted by request size")
     p.add_argument("--c5-steps", type=int, default=40, help="timed churn steps of --workload c5")
     p.add_argument("--context", default="c2",
                    help="c2 (default): context lengths U[512, 4096] seed 0 (the contract line); "
@@ -175,9 +182,13 @@ def _mean_kib(directory: str, counter: str, match) -> float:
     return sum(vals) / len(vals)
 
 
-def summarize_pmc(fetch_dir: str, write_dir: str, context: str = "c2") -> None:
+def summarize_pmc(fetch_dir: str, write_dir: str, context: str = "c2",
+                  rdreq_dir: Optional[str] = None) -> None:
     """Scales the walk's FETCH_SIZE / WRITE_SIZE (KiB per dispatch) by what the same
-    counters read for the plain copy of COPY_BYTES, and writes the traffic summary."""
+    counters read for the plain copy of COPY_BYTES, and writes the traffic summary.
+    With rdreq_dir, the read bytes are also counted from the L2's read requests to
+    memory by size (32 n32 + 64 n64 + 128 n128 per dispatch), for the walk and for the
+    copy: a second counter path that needs no scale."""
     ops = "TileOps<2, 128>" if context == "c4" else "TileOps<1, 128>"   # C4 is bf16
     is_walk = lambda k: WALK_KERNEL in k and ops in k
     is_copy = lambda k: "copy" in k.lower() and "ivakv" not in k
@@ -218,6 +229,31 @@ def summarize_pmc(fetch_dir: str, write_dir: str, context: str = "c2") -> None:
         "hbm_write_bytes_per_launch": int(write_b),
         "hbm_bytes_per_launch": int(read_b + write_b),
     }
+    if rdreq_dir:
+        def rdreq(match):
+            parts = {}
+            for size in ("", "_32B", "_64B", "_128B"):
+                name = f"TCC_EA0_RDREQ{size}_sum"
+                vals = [v for k, c, v in _counter_rows(rdreq_dir) if c == name and match(k)]
+                if not vals:
+                    raise SystemExit(f"no {name} rows in {rdreq_dir}")
+                parts[size or "all"] = vals
+            return parts
+        walk = {k: sum(v) / len(v) for k, v in rdreq(is_walk).items()}
+        # the copy: dispatches whose 128-byte requests cover at least a quarter of it
+        copy_all = rdreq(is_copy)
+        big = [i for i, v in enumerate(copy_all["_128B"]) if v * 128 > 0.25 * COPY_BYTES]
+        if not big:
+            raise SystemExit(f"no calibration copy rows in {rdreq_dir}")
+        copy = {k: sum(v[i] for i in big) / len(big) for k, v in copy_all.items()}
+        by_size = lambda d: 32 * d["_32B"] + 64 * d["_64B"] + 128 * d["_128B"]
+        summary.update({
+            "rdreq_walk": {k: round(v, 1) for k, v in walk.items()},
+            "rdreq_copy": {k: round(v, 1) for k, v in copy.items()},
+            "rdreq_read_bytes_per_launch": int(by_size(walk)),
+            "rdreq_copy_read_bytes": int(by_size(copy)),
+            "rdreq_over_scaled_fetch": round(by_size(walk) / read_b, 4),
+        })
     out = traffic_path(context)
     out.parent.mkdir(exist_ok=True)
     out.write_text(json.dumps(summary, indent=1) + "\n")
@@ -935,7 +971,7 @@ def bench_ops(args, iva, torch, dev):
 def main():
     args = parse_args()
     if args.summarize_pmc:
-        summarize_pmc(*args.summarize_pmc, context=args.context)
+        summarize_pmc(*args.summarize_pmc, context=args.context, rdreq_dir=args.rdreq_dir)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
