@@ -271,6 +271,7 @@ def _ceiling_lib():
     c_int, c_int64, c_void_p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
     lib.ceiling_stream.argtypes = [c_void_p, c_int64, c_void_p, c_int, c_void_p]
     lib.ceiling_tiles.argtypes = [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_int, c_void_p]
+    lib.ceiling_mfma.argtypes = [c_int, c_void_p, c_int, c_void_p]
     return lib
 
 
@@ -322,19 +323,47 @@ def measure_ceiling(torch, dev, sets=4, set_bytes=288 << 20, tile_bytes=4096,
                                                     sink.data_ptr(), cus * per_cu, st)))
         tile_gbs[per_cu] = tiles_per_launch * tile_bytes / t / 1e9
     del bufs, idxs
+    mfma_tf = measure_mfma(torch, dev)
     return {"stream_read_gbs": round(max(stream_gbs.values()), 1),
             "stream_read_gbs_by_wg_per_cu": {k: round(v, 1) for k, v in stream_gbs.items()},
             "tile_read_gbs": round(max(tile_gbs.values()), 1),
             "tile_read_gbs_by_wg_per_cu": {k: round(v, 1) for k, v in tile_gbs.items()},
+            "mfma_f16_tflops": round(max(mfma_tf.values()), 1),
+            "mfma_f16_tflops_by_waves_per_simd": {k: round(v, 1) for k, v in mfma_tf.items()},
             "sample": f"{sets} rotated buffers of {set_bytes >> 20} MiB; tiles: "
                       f"{tiles_per_launch} random {tile_bytes}-byte tiles per launch, one in "
                       f"flight per wave, 2 / 4 / 8 workgroups of 4 waves per CU ({cus} CUs)"}
 
 
+def measure_mfma(torch, dev, iters=4000, reps=10):
+    """Dense fp16 MFMA throughput of this GPU (TFLOP/s by waves per SIMD): 1 / 2 / 4
+    4-wave workgroups per CU, each wave 8 independent chains of `iters` 16x16x32 MFMAs
+    (the prefill's instruction) with no memory traffic; average over back-to-back
+    launches (HIP events)."""
+    lib = _ceiling_lib()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream(dev)
+    sink = torch.empty(cus * 16 * 16, dtype=torch.uint8, device=dev)   # one word per wave
+    out = {}
+    for per_cu in (1, 2, 4):
+        launch = lambda: lib.ceiling_mfma(iters, sink.data_ptr(), cus * per_cu, stream.cuda_stream)
+        if launch() != 0:
+            raise SystemExit("ceiling_mfma launch failed")
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            launch()
+        e1.record(stream)
+        torch.cuda.synchronize(dev)
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        out[per_cu] = cus * per_cu * 4 * iters * 8 * 16384 / t / 1e12
+    return out
+
+
 def bench_ceiling(args, iva, torch, dev):
-    """Measured read ceilings of the GPU (see measure_ceiling)."""
+    """Measured read and MFMA ceilings of the GPU (see measure_ceiling, measure_mfma)."""
     c = measure_ceiling(torch, dev)
-    return {"metric": "HBM read ceiling GB/s (streaming and random 4 KiB tiles)",
+    return {"metric": "HBM read ceiling GB/s (streaming and random 4 KiB tiles); dense fp16 MFMA TFLOP/s",
             "workload": "ceiling", "value": c["tile_read_gbs"], "unit": "GB/s",
             "peak": HBM_PEAK_GBS, **c}
 
@@ -749,6 +778,7 @@ def bench_prefill(args, iva, torch, dev):
     t8 = measure(lambda: [run8(sets8[i % len(sets8)]) for i in range(reps)]) / reps
     flops = sum(4 * d * hq * (L - n + i + 1) for L, n in zip(lengths, chunks) for i in range(n))
     tf = flops / t / 1e12
+    mfma_ceiling = max(measure_mfma(torch, dev).values())
     return {"metric": "paged chunked-prefill attention TFLOP/s", "workload": "prefill",
             "value": round(tf, 1), "unit": "TFLOP/s", "dtype": "f16",
             "config": {"sequences": 16, "chunk": 512, "context": 2048, "heads": "32/8",
@@ -756,6 +786,8 @@ def bench_prefill(args, iva, torch, dev):
             "kernel_us": round(t * 1e6, 2), "algorithmic_flops": flops,
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0,
                          "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4)},
+            "measured_mfma_f16_ceiling_tflops": round(mfma_ceiling, 1),
+            "frac_of_measured_mfma_ceiling": round(tf / mfma_ceiling, 4),
             "fp8_pages_kernel_us": round(t8 * 1e6, 2),
             "fp8_pages_tflops": round(flops / t8 / 1e12, 1)}
 

@@ -1,6 +1,6 @@
-// Read-bandwidth ceiling kernels for bench.py --workload ceiling (measurement only: not
-// part of libivakv's C ABI).  Both read HBM and write one 16-byte word per wave, so the
-// traffic is the bytes read.
+// Ceiling kernels for bench.py --workload ceiling (measurement only: not
+// part of libivakv's C ABI).  The two read kernels read HBM and write one 16-byte word
+// per wave, so the traffic is the bytes read; the MFMA kernel reads nothing.
 //
 //   ceiling_stream_read: the buffer read front to back, 16 bytes per lane per load, a
 //     grid-stride loop with four loads in flight per lane.
@@ -9,6 +9,8 @@
 //     head_dim 128, fp16) at the offsets idx[i] * tile_bytes, dealt in equal contiguous
 //     shares to a grid of 4-wave workgroups, one tile in flight per wave (the bytes in
 //     flight per CU are set by the workgroups per CU).
+//   ceiling_mfma_f16: dense fp16 16x16x32 MFMA throughput (the prefill's instruction)
+//     with no memory traffic in the loop.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -66,7 +68,43 @@ __global__ __launch_bounds__(256) void ceiling_tile_read(const u32x4* __restrict
   if (lane == 0) sink[wave] = acc;
 }
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Dense fp16 MFMA throughput: every wave runs `iters` rounds of kChains independent
+// 16x16x32 accumulations (no loads in the loop), so nothing but the matrix cores and
+// the clock bounds it.  Operands come from the lane index, so nothing folds away.
+constexpr int kChains = 8;
+__global__ __launch_bounds__(256, 2) void ceiling_mfma_f16(int iters, f32x4* sink) {
+  const int lane = threadIdx.x & 63;
+  f16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (_Float16)(0.001f * (lane + i));
+    b[i] = (_Float16)(0.002f * (lane - i));
+  }
+  f32x4 acc[kChains];
+#pragma unroll
+  for (int k = 0; k < kChains; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int k = 0; k < kChains; ++k) acc[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[k], 0, 0, 0);
+  }
+  f32x4 s = acc[0];
+#pragma unroll
+  for (int k = 1; k < kChains; ++k) s += acc[k];
+  if (lane == 0) sink[(blockIdx.x * blockDim.x + threadIdx.x) >> 6] = s;
+}
+
 }  // namespace
+
+// Runs grid workgroups of 4 waves, each wave iters x 8 MFMAs of 16x16x32 (16,384 FLOP
+// each); sink holds one 16-byte word per wave (grid * 4 words).  Returns the HIP error
+// code of the launch.
+extern "C" int ceiling_mfma(int iters, void* sink, int grid, hipStream_t stream) {
+  ceiling_mfma_f16<<<grid, 256, 0, stream>>>(iters, static_cast<f32x4*>(sink));
+  return (int)hipGetLastError();
+}
 
 // Reads n_bytes (a multiple of 16) of src; sink holds one 16-byte word per wave of the
 // grid (grid * 4 words).  Returns the HIP error code of the launch.
