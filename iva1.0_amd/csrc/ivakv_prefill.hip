@@ -11,7 +11,7 @@
 // rows spans as few positions as possible (tight causal ranges).  A workgroup
 // of W waves takes 32*W consecutive rows (two 16-row blocks per wave) and walks
 // the pages its rows can see two at a time (32 keys):
-// the pair's K and V tiles move HBM -> registers -> an LDS ring (five buffers
+// the pair's K and V tiles move HBM -> registers -> an LDS ring (eight buffers
 // for the pipelined loop, two otherwise) once per workgroup, and every wave
 // reads them from LDS in MFMA operand order (the pools' tile layout is kept in
 // LDS):
@@ -71,8 +71,9 @@ struct PrefillShape {
   static constexpr int kRowsWG = kRowsWave * kWaves;
   static constexpr int kPageElems = kBS * D;          // one K or V page tile
   static constexpr int kPairElems = 4 * kPageElems;   // K_A, K_B, V_A, V_B
-  // LDS pair buffers: five for the pipelined loop (two stage sets), else two.
-  static constexpr int kBufs = kStages == 2 ? 5 : 2;
+  // LDS pair buffers: eight for the pipelined loop (two stage sets; it needs five,
+  // and a power of two makes the ring index a mask), else two.
+  static constexpr int kBufs = kStages == 2 ? 8 : 2;
   static constexpr size_t kLdsBytes = kBufs * (size_t)kPairElems * kESize;
 };
 
@@ -534,13 +535,13 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
     fetch_ids(0, 0);
     fetch_ids(1, 1);
     if constexpr (S::kStages == 2) {
-      // Software pipeline over five LDS buffers (pair p in buffer p % 5) and two
+      // Software pipeline over eight LDS buffers (pair p in buffer p & 7) and two
       // stage sets (pair p in set p % 2), two steps and one barrier per
       // iteration.  Step i issues the QK MFMAs of pair i + 1, then runs pair i's
       // softmax (on the VALU while those MFMAs execute) and PV.  An iteration
       // (steps i, i + 1) reads pairs i .. i + 2, published by the barrier before
-      // it, and stores pairs i + 3 and i + 4 into the buffers of pairs i - 2 and
-      // i - 1, which that barrier retired; its own barrier publishes them.  Loads
+      // it, and stores pairs i + 3 and i + 4 into the buffers of pairs i - 5 and
+      // i - 4, which earlier barriers retired; its own barrier publishes them.  Loads
       // (pairs i + 5, i + 6) refill the stage sets just stored.  Loads past the
       // last pair repeat the last page (an L2 hit) into buffers nobody reads;
       // being unconditional keeps the stage in registers.
@@ -556,12 +557,12 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
       __syncthreads();
       if (pair_live(0)) qk_pair(0, s0);
       for (int i = 0; i < n_pairs; i += 2) {
-        store((i + 3) % 5, 1, i + 3);
+        store((i + 3) & 7, 1, i + 3);
         load(i + 5, 1, 1);
-        step((i + 1) % 5, s1, i % 5, i, s0);
-        store((i + 4) % 5, 0, i + 4);
+        step((i + 1) & 7, s1, i & 7, i, s0);
+        store((i + 4) & 7, 0, i + 4);
         load(i + 6, 0, 0);
-        step((i + 2) % 5, s0, (i + 1) % 5, i + 1, s1);
+        step((i + 2) & 7, s0, (i + 1) & 7, i + 1, s1);
         __syncthreads();
       }
     } else {
