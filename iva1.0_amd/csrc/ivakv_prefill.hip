@@ -95,12 +95,14 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   // XCD-aware order: the dispatcher deals workgroup ids round-robin to the 8
   // XCDs, so unit u = (sequence, kv head) gets ids == u % 8 (mod 8) and all its
   // row blocks run on one XCD, close in time: its pages come from HBM once per
-  // XCD and are L2 hits for the other row blocks.
+  // XCD and are L2 hits for the other row blocks.  A unit's row blocks go last
+  // first: later rows see more keys, so the longest blocks are dispatched first and
+  // the shortest fill the tail.
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const int unit = (slot / a.blocks_x) * 8 + xcd;
   if (unit >= a.batch * a.Hkv) return;
   const int b = unit / a.Hkv, h = unit % a.Hkv;
-  const int xb = slot % a.blocks_x;
+  const int xb = a.blocks_x - 1 - slot % a.blocks_x;
   const int tid = threadIdx.x;
   const int lane = tid & 63, ln = lane & 15, lq = lane >> 4;
   const int wave = uni(tid >> 6);
