@@ -2,7 +2,8 @@
 
 The reference package cannot be imported (src/core/rope_kv.py:199-203 is a SyntaxError,
 src/utils/logging.py:13 needs tensorboard), so the tests restate the three pieces of it
-that a user of the paged backend goes through, each with the patch INTEGRATION.md gives:
+that a user of the paged backend goes through, each with the two-line patch into src/core
+(the whitelist entry and the get_attention branch below):
 
   RefTransformerConfig   src/core/transformer.py:25-78: exactly the reference's fields,
                          and its __post_init__ with "hip_paged" added to the whitelist
@@ -84,7 +85,7 @@ def field_list():
 
 
 def patched_get_attention(config):
-    """attention.py:190-194 with the INTEGRATION.md branch; AttentionTriton's forward runs
+    """attention.py:190-194 with a first branch for "hip_paged"; AttentionTriton's forward runs
     an AttentionTorch with its weights (attention.py:151-187), so the torch module
     stands in for it."""
     from iva_amd.model import AttentionTorch
