@@ -271,7 +271,7 @@ def _ceiling_lib():
     c_int, c_int64, c_void_p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
     lib.ceiling_stream.argtypes = [c_void_p, c_int64, c_void_p, c_int, c_void_p]
     lib.ceiling_tiles.argtypes = [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_int, c_void_p]
-    lib.ceiling_mfma.argtypes = [c_int, c_void_p, c_int, c_void_p]
+    lib.ceiling_mfma.argtypes = [c_int, c_void_p, c_void_p, c_int, c_void_p]
     return lib
 
 
@@ -335,18 +335,21 @@ def measure_ceiling(torch, dev, sets=4, set_bytes=288 << 20, tile_bytes=4096,
                       f"flight per wave, 2 / 4 / 8 workgroups of 4 waves per CU ({cus} CUs)"}
 
 
-def measure_mfma(torch, dev, iters=4000, reps=10):
+def measure_mfma(torch, dev, iters=20000, reps=5):
     """Dense fp16 MFMA throughput of this GPU (TFLOP/s by waves per SIMD): 1 / 2 / 4
     4-wave workgroups per CU, each wave 8 independent chains of `iters` 16x16x32 MFMAs
-    (the prefill's instruction) with no memory traffic; average over back-to-back
-    launches (HIP events)."""
+    (the prefill's instruction) on random N(0, 0.5) fp16 operands read once, with no
+    memory traffic in the loop; average over back-to-back launches (HIP events)."""
     lib = _ceiling_lib()
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     stream = torch.cuda.current_stream(dev)
     sink = torch.empty(cus * 16 * 16, dtype=torch.uint8, device=dev)   # one word per wave
+    gen = torch.Generator(device=dev).manual_seed(11)
+    ops = (torch.randn(1024 * 4 * 64 * 8, generator=gen, device=dev) * 0.5).half()
     out = {}
     for per_cu in (1, 2, 4):
-        launch = lambda: lib.ceiling_mfma(iters, sink.data_ptr(), cus * per_cu, stream.cuda_stream)
+        launch = lambda: lib.ceiling_mfma(iters, ops.data_ptr(), sink.data_ptr(), cus * per_cu,
+                                          stream.cuda_stream)
         if launch() != 0:
             raise SystemExit("ceiling_mfma launch failed")
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

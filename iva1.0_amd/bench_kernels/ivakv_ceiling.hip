@@ -10,7 +10,7 @@
 //     shares to a grid of 4-wave workgroups, one tile in flight per wave (the bytes in
 //     flight per CU are set by the workgroups per CU).
 //   ceiling_mfma_f16: dense fp16 16x16x32 MFMA throughput (the prefill's instruction)
-//     with no memory traffic in the loop.
+//     on random operands, with no memory traffic in the loop.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -73,22 +73,23 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Dense fp16 MFMA throughput: every wave runs `iters` rounds of kChains independent
 // 16x16x32 accumulations (no loads in the loop), so nothing but the matrix cores and
-// the clock bounds it.  Operands come from the lane index, so nothing folds away.
+// the clock bounds it.  The four operand vectors of each wave are read once from
+// `ops` (random fp16 values, 1024 waves' worth): operands that toggle as many bits as
+// real data draw the power, and so set the clock, that real data does.
 constexpr int kChains = 8;
-__global__ __launch_bounds__(256, 2) void ceiling_mfma_f16(int iters, f32x4* sink) {
+__global__ __launch_bounds__(256, 2) void ceiling_mfma_f16(int iters, const f16x8* __restrict__ ops,
+                                                           f32x4* sink) {
   const int lane = threadIdx.x & 63;
-  f16x8 a, b;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    a[i] = (_Float16)(0.001f * (lane + i));
-    b[i] = (_Float16)(0.002f * (lane - i));
-  }
+  const int w = (blockIdx.x * 4 + (threadIdx.x >> 6)) & 1023;
+  const f16x8 a0 = ops[(w * 4 + 0) * 64 + lane], b0 = ops[(w * 4 + 1) * 64 + lane];
+  const f16x8 a1 = ops[(w * 4 + 2) * 64 + lane], b1 = ops[(w * 4 + 3) * 64 + lane];
   f32x4 acc[kChains];
 #pragma unroll
   for (int k = 0; k < kChains; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
-    for (int k = 0; k < kChains; ++k) acc[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[k], 0, 0, 0);
+    for (int k = 0; k < kChains; ++k)
+      acc[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16((k & 1) ? a1 : a0, (k & 2) ? b1 : b0, acc[k], 0, 0, 0);
   }
   f32x4 s = acc[0];
 #pragma unroll
@@ -99,10 +100,11 @@ __global__ __launch_bounds__(256, 2) void ceiling_mfma_f16(int iters, f32x4* sin
 }  // namespace
 
 // Runs grid workgroups of 4 waves, each wave iters x 8 MFMAs of 16x16x32 (16,384 FLOP
-// each); sink holds one 16-byte word per wave (grid * 4 words).  Returns the HIP error
-// code of the launch.
-extern "C" int ceiling_mfma(int iters, void* sink, int grid, hipStream_t stream) {
-  ceiling_mfma_f16<<<grid, 256, 0, stream>>>(iters, static_cast<f32x4*>(sink));
+// each) on operands read from ops (1024 * 4 * 64 vectors of 8 fp16, 4 MiB); sink holds
+// one 16-byte word per wave (grid * 4 words).  Returns the HIP error code of the launch.
+extern "C" int ceiling_mfma(int iters, const void* ops, void* sink, int grid, hipStream_t stream) {
+  ceiling_mfma_f16<<<grid, 256, 0, stream>>>(iters, static_cast<const f16x8*>(ops),
+                                             static_cast<f32x4*>(sink));
   return (int)hipGetLastError();
 }
 
