@@ -355,6 +355,50 @@ int ivakv_prefill_attn_fp8(const void* q, const void* k_pool, const void* v_pool
                            int window, int n_sink, int dtype, hipStream_t stream);
 
 /*
+ * Bytes of device workspace ivakv_prefill_attn_split(_fp8) needs for this geometry:
+ * the plan (item queues, per-row-block segments), and 512 fp32 partial slots of one
+ * row block each (the rows of one workgroup: 256 at head_dim <= 128 in fp16 / bf16)
+ * with a running max and row sum per row: about 65 MiB at head_dim 128.
+ */
+int ivakv_prefill_split_workspace_size(int batch, int num_q_heads, int num_kv_heads,
+                                       int head_dim, int max_query_len, int dtype,
+                                       size_t* bytes);
+
+/*
+ * ivakv_prefill_attn with each row block's walk split along the keys: the same
+ * arguments and results (within the attention tolerance: segments round P to the
+ * query dtype against their own running maxima), for batches whose longest chunks
+ * sit on long contexts.  ivakv_prefill_attn gives a row block one workgroup, so a
+ * 512-token chunk at 16k keys occupies 64 workgroups for the whole launch; here a plan
+ * kernel cuts every row block's walk into segments of about (total work / CUs),
+ * a persistent grid (one workgroup per CU) runs the (row block, segment) items,
+ * longest sequences first, from per-XCD queues, and a merge kernel folds each split
+ * block's segments by log-sum-exp.  Three launches, no host synchronisation (graph
+ * capture safe).  batch <= 4096, num_kv_heads <= 32767.  The workspace
+ * (ivakv_prefill_split_workspace_size) needs no initialisation; calls that share a
+ * workspace must not run concurrently.
+ * Replaces: the same reference code as ivakv_prefill_attn.
+ */
+int ivakv_prefill_attn_split(const void* q, const void* k_pool, const void* v_pool,
+                             const int32_t* block_tables, const int32_t* context_lens,
+                             const int32_t* query_start, int n_tok, void* out,
+                             void* workspace, size_t workspace_bytes, int batch,
+                             int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                             int max_blocks, int num_pages, int max_query_len, float scale,
+                             int window, int n_sink, int dtype, hipStream_t stream);
+
+/* ivakv_prefill_attn_split over FP8 pools, as ivakv_prefill_attn_fp8. */
+int ivakv_prefill_attn_split_fp8(const void* q, const void* k_pool, const void* v_pool,
+                                 const float* k_scale, const float* v_scale,
+                                 const int32_t* block_tables, const int32_t* context_lens,
+                                 const int32_t* query_start, int n_tok, void* out,
+                                 void* workspace, size_t workspace_bytes, int batch,
+                                 int num_q_heads, int num_kv_heads, int head_dim,
+                                 int block_size, int max_blocks, int num_pages,
+                                 int max_query_len, float scale, int window, int n_sink,
+                                 int dtype, hipStream_t stream);
+
+/*
  * Index gather on a contiguous-layout cache kv = [batch][n_heads][seq_len][D]
  * with element strides (s_b, s_h, s_s, s_d):
  *   out[b, h, j, :] = kv[b, h, indices[j], :]      out = [B][H][n_idx][D] dense

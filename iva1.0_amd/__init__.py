@@ -24,6 +24,7 @@ from .ops import (
     paged_decode_attention_merge,
     paged_decode_attention_partial,
     paged_prefill_attention,
+    prefill_split_workspace_bytes,
     pool_geometry,
     pool_shapes,
     rope_,
@@ -55,6 +56,7 @@ __all__ = [
     "paged_decode_attention_merge",
     "paged_decode_attention_partial",
     "paged_prefill_attention",
+    "prefill_split_workspace_bytes",
     "pool_geometry",
     "pool_shapes",
     "rope_",

@@ -147,6 +147,31 @@ SIGNATURES = {
         c_int, c_int, c_int,                   # window, n_sink, dtype
         c_void_p,                              # stream
     ]),
+    "ivakv_prefill_split_workspace_size": (c_int, [
+        c_int, c_int, c_int, c_int,            # batch, num_q_heads, num_kv_heads, head_dim
+        c_int, c_int, POINTER(c_size_t),       # max_query_len, dtype, bytes
+    ]),
+    "ivakv_prefill_attn_split": (c_int, [
+        c_void_p, c_void_p, c_void_p,          # q, k_pool, v_pool
+        c_void_p, c_void_p, c_void_p,          # block_tables, context_lens, query_start
+        c_int, c_void_p,                       # n_tok, out
+        c_void_p, c_size_t,                    # workspace, workspace_bytes
+        c_int, c_int, c_int, c_int,            # batch, num_q_heads, num_kv_heads, head_dim
+        c_int, c_int, c_int, c_int, c_float,   # block_size, max_blocks, num_pages, max_query_len, scale
+        c_int, c_int, c_int,                   # window, n_sink, dtype
+        c_void_p,                              # stream
+    ]),
+    "ivakv_prefill_attn_split_fp8": (c_int, [
+        c_void_p, c_void_p, c_void_p,          # q, k_pool, v_pool
+        c_void_p, c_void_p,                    # k_scale, v_scale
+        c_void_p, c_void_p, c_void_p,          # block_tables, context_lens, query_start
+        c_int, c_void_p,                       # n_tok, out
+        c_void_p, c_size_t,                    # workspace, workspace_bytes
+        c_int, c_int, c_int, c_int,            # batch, num_q_heads, num_kv_heads, head_dim
+        c_int, c_int, c_int, c_int, c_float,   # block_size, max_blocks, num_pages, max_query_len, scale
+        c_int, c_int, c_int,                   # window, n_sink, dtype
+        c_void_p,                              # stream
+    ]),
     "ivakv_index_gather": (c_int, [
         c_void_p, c_int64, c_int64, c_int64, c_int64,  # kv + strides
         c_void_p, c_int,                             # indices, n_idx

@@ -51,6 +51,10 @@ struct PrefillArgs {
   int blocks_x;  // row-block workgroups per (sequence, kv head)
   const float* k_scale;  // FP8 pools: [num_pages][Hkv][16] fp32 scaling factors
   const float* v_scale;
+  // Split walks: partial slots [slot][rows_wg][D] (acc) and [slot][rows_wg][2]
+  // (running max, row sum) of the split workspace.
+  float* part_acc;
+  float* part_ml;
 };
 
 // Shape of the kernel instance.  fp16 / bf16 up to head_dim 128: 8 waves of
@@ -77,11 +81,54 @@ struct PrefillShape {
   static constexpr size_t kLdsBytes = kBufs * (size_t)kPairElems * kESize;
 };
 
+// Geometry of row block xb (rows xb * rows_wg ..) of sequence b: its rows, positions
+// and the page walk that covers every key any of its rows can see.  ok is false
+// when the block has no row to compute (a sequence whose rows do not lie inside q,
+// an empty chunk, a block past the chunk's rows).
+struct RowBlock {
+  bool ok;
+  int q0, rows, L, first_pos, r_wg;
+  PageWalk w;
+  int n_eff, n_pairs;  // effective pages of the walk, and pairs of them (32 keys)
+};
+
+__device__ inline RowBlock row_block(const PrefillArgs& a, const int32_t* ctx, const int32_t* qstart,
+                                     int b, int xb, int rows_wg) {
+  RowBlock rb;
+  rb.ok = false;
+  // The sequence's rows [q0, q1) must lie inside q / out; a range that does not is
+  // skipped (its rows are not written).
+  const int64_t q0l = qstart[b], q1l = qstart[b + 1];
+  if (q0l < 0 || q1l <= q0l || q1l > a.n_tok) return rb;
+  const int n = (int)(q1l - q0l);
+  rb.q0 = (int)q0l;
+  rb.L = ctx[b];
+  rb.rows = n * a.G;
+  rb.r_wg = xb * rows_wg;
+  if (rb.r_wg >= rb.rows) return rb;
+  rb.first_pos = rb.L - n;  // position of query row 0 of the chunk
+  // Keys any row of the block can see: positions <= p_hi, from p_lo - window + 1 on,
+  // plus the sinks.  (All rows before position 0: nothing to walk.)
+  const int p_lo = max(rb.first_pos + rb.r_wg / a.G, 0);
+  const int p_hi = rb.first_pos + (min(rb.r_wg + rows_wg, rb.rows) - 1) / a.G;
+  rb.w = make_walk(p_hi >= 0 ? p_hi + 1 : 0, a.window > 0 ? a.window + (p_hi - p_lo) : 0,
+                   a.n_sink, kBS);
+  rb.n_eff = table_pages(rb.w, a.max_blocks, kBS);
+  rb.n_pairs = (rb.n_eff + 1) / 2;
+  rb.ok = true;
+  return rb;
+}
+
+// Row block xb of (sequence b, kv head h) over pairs [pair_lo, pair_hi) of its walk
+// (pair_lo even).  slot < 0: the block's whole walk, normalized rows into out; slot
+// >= 0: one segment of a split walk, its unnormalized rows (acc, running max, row sum)
+// into partial slot `slot` of the split workspace, for prefill_merge_kernel.  Every
+// thread of the workgroup calls it with the same arguments (the returns and barriers
+// inside are uniform).
 template <int DT, int D, bool kFp8>
-__global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kernel(PrefillArgs a,
-                                                             const int32_t* __restrict__ bt,
-                                                             const int32_t* __restrict__ ctx,
-                                                             const int32_t* __restrict__ qstart) {
+__device__ __attribute__((always_inline)) inline void prefill_rows(
+    const PrefillArgs& a, const int32_t* __restrict__ bt, const int32_t* __restrict__ ctx,
+    const int32_t* __restrict__ qstart, int b, int h, int xb, int pair_lo, int pair_hi, int slot) {
   using Tr = Traits<DT>;
   using E = typename Tr::E;
   using S = PrefillShape<DT, D>;
@@ -92,41 +139,21 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   constexpr int64_t kTile = (int64_t)D * kBS;
   extern __shared__ Chunk16 lds[];  // 2 x [K_A | K_B | V_A | V_B], global tile layout
 
-  // XCD-aware order: the dispatcher deals workgroup ids round-robin to the 8
-  // XCDs, so unit u = (sequence, kv head) gets ids == u % 8 (mod 8) and all its
-  // row blocks run on one XCD, close in time: its pages come from HBM once per
-  // XCD and are L2 hits for the other row blocks.  A unit's row blocks go last
-  // first: later rows see more keys, so the longest blocks are dispatched first and
-  // the shortest fill the tail.
-  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  const int unit = (slot / a.blocks_x) * 8 + xcd;
-  if (unit >= a.batch * a.Hkv) return;
-  const int b = unit / a.Hkv, h = unit % a.Hkv;
-  const int xb = a.blocks_x - 1 - slot % a.blocks_x;
   const int tid = threadIdx.x;
   const int lane = tid & 63, ln = lane & 15, lq = lane >> 4;
   const int wave = uni(tid >> 6);
   const int G = a.G, Hkv = a.Hkv, Hq = Hkv * G;
-  // The sequence's rows [q0, q1) must lie inside q / out; a range that does not is
-  // skipped (its rows are not written).
-  const int64_t q0l = qstart[b], q1l = qstart[b + 1];
-  if (q0l < 0 || q1l <= q0l || q1l > a.n_tok) return;  // uniform over the workgroup
-  const int q0 = (int)q0l;
-  const int n = (int)(q1l - q0l);
-  const int L = ctx[b];
-  const int rows = n * G;
-  const int r_wg = xb * S::kRowsWG;
-  if (n <= 0 || r_wg >= rows) return;  // uniform over the workgroup
-  const int first_pos = L - n;  // position of query row 0 of the chunk
-
-  // Keys any row of the workgroup can see: positions <= p_hi, from p_lo - window
-  // + 1 on, plus the sinks.  (All rows before position 0: nothing to walk.)
-  const int p_lo = max(first_pos + r_wg / G, 0);
-  const int p_hi = first_pos + (min(r_wg + S::kRowsWG, rows) - 1) / G;
-  const PageWalk w = make_walk(p_hi >= 0 ? p_hi + 1 : 0, a.window > 0 ? a.window + (p_hi - p_lo) : 0,
-                               a.n_sink, kBS);
-  const int n_eff = table_pages(w, a.max_blocks, kBS);
-  const int n_pairs = (n_eff + 1) / 2;
+  const RowBlock blk = row_block(a, ctx, qstart, b, xb, S::kRowsWG);
+  if (!blk.ok) return;  // uniform over the workgroup
+  const int q0 = blk.q0, L = blk.L, rows = blk.rows, r_wg = blk.r_wg, first_pos = blk.first_pos;
+  const PageWalk w = blk.w;
+  const int n_eff = blk.n_eff;
+  // This call's pairs: [p0, n_pairs) with n_pairs the segment's end.
+  const int n_pairs = min(blk.n_pairs, pair_hi);
+  const int p0 = pair_lo;
+  // Pages loads may touch: the segment's (loads past its last pair repeat its last
+  // page, an L2 hit).
+  const int v_end = min(n_eff, 2 * n_pairs);
 
   // This wave's rows: the last position any of them has (pairs entirely past it
   // are skipped) and, per lane, the position of row ln of each block.
@@ -190,7 +217,7 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   // inside the walk) in okmask, bits 2 (pair % 16) and + 1, which the pair's
   // step reads.  Pages past n_eff are the last one (masked later); invalid ids
   // read page 0.
-  auto lpage = [&](int v) IVAKV_INLINE -> int { return logical_page(w, v < n_eff ? v : n_eff - 1); };
+  auto lpage = [&](int v) IVAKV_INLINE -> int { return logical_page(w, v < v_end ? v : v_end - 1); };
   const int32_t* bt_row = bt + (int64_t)b * a.max_blocks;
   int ids_a[2], ids_b[2];
   uint32_t okmask = 0;
@@ -533,9 +560,9 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   // Ring: pair i is in LDS buffer i % 2 while pair i + 1 travels from HBM / L2
   // into the staging registers; one barrier per pair.  Page ids are fetched two
   // loads ahead, in the slot of the pair's parity.
-  if (n_pairs > 0) {
-    fetch_ids(0, 0);
-    fetch_ids(1, 1);
+  if (n_pairs > p0) {
+    fetch_ids(p0, 0);
+    fetch_ids(p0 + 1, 1);
     if constexpr (S::kStages == 2) {
       // Software pipeline over eight LDS buffers (pair p in buffer p & 7) and two
       // stage sets (pair p in set p % 2), two steps and one barrier per
@@ -548,17 +575,17 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
       // last pair repeat the last page (an L2 hit) into buffers nobody reads;
       // being unconditional keeps the stage in registers.
       PairS s0, s1;
-      load(0, 0, 0);
-      load(1, 1, 1);
-      store(0, 0, 0);
-      load(2, 0, 0);
-      store(1, 1, 1);
-      load(3, 1, 1);
-      store(2, 0, 2);
-      load(4, 0, 0);
+      load(p0, 0, 0);
+      load(p0 + 1, 1, 1);
+      store(p0 & 7, 0, p0);
+      load(p0 + 2, 0, 0);
+      store((p0 + 1) & 7, 1, p0 + 1);
+      load(p0 + 3, 1, 1);
+      store((p0 + 2) & 7, 0, p0 + 2);
+      load(p0 + 4, 0, 0);
       __syncthreads();
-      if (pair_live(0)) qk_pair(0, s0);
-      for (int i = 0; i < n_pairs; i += 2) {
+      if (pair_live(p0)) qk_pair(p0 & 7, s0);
+      for (int i = p0; i < n_pairs; i += 2) {
         store((i + 3) & 7, 1, i + 3);
         load(i + 5, 1, 1);
         step((i + 1) & 7, s1, i & 7, i, s0);
@@ -570,10 +597,10 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
     } else {
       // Two pairs per iteration so that the page-id slot (the pair's parity) is
       // known at compile time; a pair past the walk is skipped.
-      load(0, 0, 0);
-      store(0, 0, 0);
+      load(p0, 0, 0);
+      store(0, 0, p0);
       __syncthreads();
-      for (int i = 0; i < n_pairs; i += 2) {
+      for (int i = p0; i < n_pairs; i += 2) {
         load(i + 1, 0, 1);
         compute(0, i);
         store(1, 0, i + 1);
@@ -587,19 +614,328 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
   }
 
   // O = acc / l, rows of this lane's column; the row sum is split over the 4 k-groups.
+  // A segment of a split walk stores acc, the running max and the row sum instead
+  // (row r_w + 16 rb + ln - r_wg of the slot).
 #pragma unroll
   for (int rb = 0; rb < NR; ++rb) {
     float l = l_run[rb] + __shfl_xor(l_run[rb], 16);
     l = l + __shfl_xor(l, 32);
     const int r = r_w + 16 * rb + ln;
     if (r < rows) {
-      const float inv = l > 0.f ? 1.f / l : 0.f;
-      E* o = static_cast<E*>(a.out) + ((int64_t)(q0 + r / G) * Hq + h * G + r % G) * D + 4 * lq;
+      if (slot >= 0) {
+        const int64_t pr = (int64_t)slot * S::kRowsWG + (r - r_wg);
+        float* po = a.part_acc + pr * D + 4 * lq;
 #pragma unroll
-      for (int m = 0; m < NB; ++m)
+        for (int m = 0; m < NB; ++m) *reinterpret_cast<f32x4*>(po + 16 * m) = acc[rb][m];
+        if (lq == 0) *reinterpret_cast<f32x2*>(a.part_ml + 2 * pr) = f32x2{m_run[rb], l};
+      } else {
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        E* o = static_cast<E*>(a.out) + ((int64_t)(q0 + r / G) * Hq + h * G + r % G) * D + 4 * lq;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[16 * m + i] = Tr::from_float(acc[rb][m][i] * inv);
+        for (int m = 0; m < NB; ++m)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[16 * m + i] = Tr::from_float(acc[rb][m][i] * inv);
+      }
     }
+  }
+}
+
+// One workgroup per row block, in XCD-aware order: the dispatcher deals workgroup
+// ids round-robin to the 8 XCDs, so unit u = (sequence, kv head) gets ids == u % 8
+// (mod 8) and all its row blocks run on one XCD, close in time: its pages come from
+// HBM once per XCD and are L2 hits for the other row blocks.  A unit's row blocks go
+// last first: later rows see more keys, so the longest blocks are dispatched first
+// and the shortest fill the tail.
+template <int DT, int D, bool kFp8>
+__global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kernel(PrefillArgs a,
+                                                             const int32_t* __restrict__ bt,
+                                                             const int32_t* __restrict__ ctx,
+                                                             const int32_t* __restrict__ qstart) {
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int unit = (slot / a.blocks_x) * 8 + xcd;
+  if (unit >= a.batch * a.Hkv) return;
+  const int b = unit / a.Hkv, h = unit % a.Hkv;
+  const int xb = a.blocks_x - 1 - slot % a.blocks_x;
+  prefill_rows<DT, D, kFp8>(a, bt, ctx, qstart, b, h, xb, 0, 0x7fffffff, -1);
+}
+
+// ---------------------------------------------------------------------------
+// Split walks (ivakv_prefill_attn_split).  A row block walks every pair its rows can
+// see, so a chunk late in a long context is one workgroup's serial walk: a single
+// 512-token chunk at 16k keys fills 64 of 256 CUs.  The split path cuts each row
+// block's walk into segments of seg_pairs pairs, sized so that the batch's work
+// spreads over every CU (seg_pairs ~ total pairs / CUs), runs (row block, segment)
+// items on a persistent grid that takes them from per-XCD queues, and merges the
+// segments of each split row block by log-sum-exp.  Three launches:
+//   prefill_plan_kernel   one workgroup: segment size, the item queues (longest
+//                         sequences first), partial slots, the queues' counters
+//                         reset to zero (so the workspace needs no initialisation);
+//   prefill_split_kernel  one workgroup per CU, items until its XCD's queue is empty;
+//   prefill_merge_kernel  the split row blocks' partials into out.
+// ---------------------------------------------------------------------------
+
+// Partial slots (row-block segments) the split workspace holds; the plan doubles the
+// segment length until the split row blocks fit.
+constexpr int kSplitSlots = 512;
+// Shortest segment, in pairs of pages (32 keys each); even, as the pair loop needs.
+constexpr int kSplitMinPairs = 16;
+// The plan ranks the sequences by their longest row block in LDS, up to this batch
+// (the split path's largest batch).
+constexpr int kPlanMaxBatch = 4096;
+constexpr int kPlanSortBatch = 256;
+constexpr int kPlanThreads = 1024;
+
+// Split workspace.  ctl: [0] virtual units V, [1] split row blocks, [2] segment
+// length in pairs, [32 + 4x] the queue counter of XCD x.  A virtual unit (sequence b,
+// kv head h, segment s) is packed (b | h << 16, s); the queue of XCD x holds virtual
+// units x, x + 8, ... and a ticket j of it is row block blocks_x - 1 - j % blocks_x of
+// unit x + 8 (j / blocks_x).  rb[b * blocks_x + xb] = (first slot, segments) of a
+// split row block ((-1, 1) unsplit, (-1, 0) no rows); the slot of segment s of kv
+// head h is first + h * segments + s.
+struct SplitWs {
+  int32_t* ctl;
+  int2* vus;     // [batch * Hkv + kSplitSlots]
+  int2* rb;      // [batch * blocks_x]
+  int4* splits;  // [kSplitSlots / 2] (b | h << 16 unused: b, xb, first slot, segments)
+  float* acc;    // [kSplitSlots][rows_wg][D]
+  float* ml;     // [kSplitSlots][rows_wg][2]
+};
+
+// Byte layout of the split workspace (each part 256-byte aligned).
+struct SplitLayout {
+  size_t ctl, vus, rb, splits, acc, ml, total;
+};
+inline SplitLayout split_layout(int batch, int num_kv_heads, int blocks_x, int rows_wg, int head_dim) {
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  SplitLayout l;
+  l.ctl = 0;
+  l.vus = up(l.ctl + 64 * sizeof(int32_t));
+  l.rb = up(l.vus + ((size_t)batch * num_kv_heads + kSplitSlots) * sizeof(int2));
+  l.splits = up(l.rb + (size_t)batch * blocks_x * sizeof(int2));
+  l.acc = up(l.splits + (size_t)(kSplitSlots / 2) * sizeof(int4));
+  l.ml = up(l.acc + (size_t)kSplitSlots * rows_wg * head_dim * sizeof(float));
+  l.total = up(l.ml + (size_t)kSplitSlots * rows_wg * 2 * sizeof(float));
+  return l;
+}
+
+// Sum of v over the workgroup (kPlanThreads threads), returned to every thread.
+__device__ inline int64_t plan_sum(int64_t v, int64_t* s_red64) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const int lo = __shfl_xor((int)(uint32_t)v, off), hi = __shfl_xor((int)(v >> 32), off);
+    v += (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+  }
+  const int wv = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) s_red64[wv] = v;
+  __syncthreads();
+  int64_t t = 0;
+  for (int i = 0; i < kPlanThreads / 64; ++i) t += s_red64[i];
+  return t;
+}
+
+// Exclusive prefix of v over the workgroup in thread order; *total gets the sum.
+__device__ inline int plan_scan(int v, int* s_red, int* total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(incl, off);
+    if (lane >= off) incl += u;
+  }
+  __syncthreads();
+  if (lane == 63) s_red[wv] = incl;
+  __syncthreads();
+  int before = 0, t = 0;
+  for (int i = 0; i < kPlanThreads / 64; ++i) {
+    before += i < wv ? s_red[i] : 0;
+    t += s_red[i];
+  }
+  *total = t;
+  return before + incl - v;
+}
+
+// Segments of a row block of n pairs (one when it is not split).
+__device__ inline int n_segments(int n_pairs, int seg) { return n_pairs > seg ? (n_pairs + seg - 1) / seg : 1; }
+
+__global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs a,
+                                                                    const int32_t* __restrict__ ctx,
+                                                                    const int32_t* __restrict__ qstart,
+                                                                    SplitWs ws, int rows_wg, int n_cu) {
+  __shared__ int s_red[kPlanThreads / 64];
+  __shared__ int64_t s_red64[kPlanThreads / 64];
+  __shared__ int s_key[kPlanMaxBatch];   // longest row block (pairs) per sequence, -1: none
+  __shared__ int s_order[kPlanMaxBatch];  // sequences by rank
+  __shared__ int s_pref[kPlanMaxBatch + 1];
+  const int tid = threadIdx.x;
+  const int B = a.batch, Hkv = a.Hkv, BX = a.blocks_x;
+  const int E = B * BX;
+  for (int b = tid; b < B; b += kPlanThreads) s_key[b] = -1;
+  __syncthreads();
+  // 1. Pairs of every row block (kept in rb[].x until the slots replace them), the
+  //    batch's total and each sequence's longest block.
+  int64_t part = 0;
+  for (int e = tid; e < E; e += kPlanThreads) {
+    const RowBlock blk = row_block(a, ctx, qstart, e / BX, e % BX, rows_wg);
+    const int np = blk.ok ? blk.n_pairs : -1;
+    ws.rb[e].x = np;
+    if (blk.ok) {
+      part += np;
+      atomicMax(&s_key[e / BX], np);
+    }
+  }
+  const int64_t total = plan_sum(part, s_red64) * Hkv;
+  // 2. Segment length: the work of one CU, at least kSplitMinPairs, even; doubled
+  //    until the split row blocks' segments fit the slots.
+  int seg = (int)min<int64_t>((total + n_cu - 1) / n_cu, 1 << 28);
+  seg = max(kSplitMinPairs, (seg + 1) & ~1);
+  for (;;) {
+    int64_t need = 0;
+    for (int e = tid; e < E; e += kPlanThreads) {
+      const int np = ws.rb[e].x;
+      if (np > seg) need += n_segments(np, seg);
+    }
+    if (plan_sum(need, s_red64) * Hkv <= kSplitSlots) break;
+    seg *= 2;
+  }
+  // 3. Sequences by their longest row block, longest first (ties by index): the
+  //    queues then hold the longest items first.  (A larger batch keeps its order:
+  //    the ranking is quadratic.)
+  for (int b = tid; b < B; b += kPlanThreads) {
+    int r = b;
+    if (B <= kPlanSortBatch) {
+      const int kb = s_key[b];
+      r = 0;
+      for (int o = 0; o < B; ++o) {
+        const int ko = s_key[o];
+        r += (ko > kb || (ko == kb && o < b)) ? 1 : 0;
+      }
+    }
+    s_order[r] = b;
+  }
+  __syncthreads();
+  // 4. Virtual units in rank order: every kv head of every segment of the sequence
+  //    (none for a sequence without rows).  Unit g goes to the queue of XCD g % 8.
+  int V = 0;
+  for (int r0 = 0; r0 < B; r0 += kPlanThreads) {
+    const int r = r0 + tid;
+    int cnt = 0;
+    if (r < B) {
+      const int kb = s_key[s_order[r]];
+      cnt = kb < 0 ? 0 : Hkv * (kb > seg ? (kb + seg - 1) / seg : 1);
+    }
+    int chunk;
+    const int ex = plan_scan(cnt, s_red, &chunk);
+    if (r < B) s_pref[r] = V + ex;
+    V += chunk;
+  }
+  if (tid == 0) s_pref[B] = V;
+  __syncthreads();
+  for (int g = tid; g < V; g += kPlanThreads) {
+    int lo = 0, hi = B;  // last r with s_pref[r] <= g
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_pref[mid] <= g) lo = mid;
+      else hi = mid;
+    }
+    const int b = s_order[lo], local = g - s_pref[lo];
+    ws.vus[g] = int2{b | ((local % Hkv) << 16), local / Hkv};
+  }
+  // 5. Slots of the split row blocks, in (sequence, row block) order, and their list.
+  int slot0 = 0, n_split = 0;
+  for (int e0 = 0; e0 < E; e0 += kPlanThreads) {
+    const int e = e0 + tid;
+    const int np = e < E ? ws.rb[e].x : -1;
+    const int ns = np > seg ? n_segments(np, seg) : 0;
+    int t_slots, t_split;
+    const int ex_slots = plan_scan(Hkv * ns, s_red, &t_slots);
+    const int ex_split = plan_scan(ns > 0 ? 1 : 0, s_red, &t_split);
+    if (e < E) {
+      ws.rb[e] = ns > 0 ? int2{slot0 + ex_slots, ns} : int2{-1, np < 0 ? 0 : 1};
+      if (ns > 0) ws.splits[n_split + ex_split] = int4{e / BX, e % BX, slot0 + ex_slots, ns};
+    }
+    slot0 += t_slots;
+    n_split += t_split;
+  }
+  if (tid == 0) {
+    ws.ctl[0] = V;
+    ws.ctl[1] = n_split;
+    ws.ctl[2] = seg;
+  }
+  if (tid < 8) ws.ctl[32 + 4 * tid] = 0;
+}
+
+// Persistent grid of the split path: workgroup w serves the queue of XCD w % 8 (the
+// dispatcher deals workgroup ids round-robin to the XCDs, so a unit's row blocks and
+// segments share one L2), taking tickets from the queue's counter until it is empty.
+template <int DT, int D, bool kFp8>
+__global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_split_kernel(
+    PrefillArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ ctx,
+    const int32_t* __restrict__ qstart, SplitWs ws) {
+  __shared__ int s_ticket[2];
+  const int x = blockIdx.x & 7;
+  // (V is at most the unit list's capacity; the clamp keeps every list read inside it.)
+  const int V = min(ws.ctl[0], a.batch * a.Hkv + kSplitSlots), seg = max(ws.ctl[2], 2);
+  const int tickets = (V > x ? (V - x + 7) / 8 : 0) * a.blocks_x;
+  int* counter = ws.ctl + 32 + 4 * x;
+  for (int it = 0;; ++it) {
+    // Two ticket cells used in turn: a thread may still read the last ticket while
+    // thread 0 writes the next one.
+    if (threadIdx.x == 0)
+      s_ticket[it & 1] = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int j = s_ticket[it & 1];
+    if (j >= tickets) break;  // uniform
+    const int2 vu = ws.vus[x + 8 * (j / a.blocks_x)];
+    const int xb = a.blocks_x - 1 - j % a.blocks_x;
+    const int b = vu.x & 0xffff, h = vu.x >> 16, s = vu.y;
+    const int2 rb = ws.rb[b * a.blocks_x + xb];
+    if (s >= rb.y) continue;  // the block has no rows, or fewer segments
+    if (rb.y > 1)
+      prefill_rows<DT, D, kFp8>(a, bt, ctx, qstart, b, h, xb, s * seg, (s + 1) * seg, rb.x + h * rb.y + s);
+    else
+      prefill_rows<DT, D, kFp8>(a, bt, ctx, qstart, b, h, xb, 0, 0x7fffffff, -1);
+  }
+}
+
+// Log-sum-exp merge of a split row block's segments: workgroup (split row block * Hkv
+// + kv head, row quarter), one f32x4 of a row per thread and step.
+template <int DT, int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a, const int32_t* __restrict__ ctx,
+                                                            const int32_t* __restrict__ qstart,
+                                                            SplitWs ws, int rows_wg) {
+  using Tr = Traits<DT>;
+  using E = typename Tr::E;
+  const int idx = blockIdx.x;
+  if (idx >= ws.ctl[1] * a.Hkv) return;
+  const int4 sp = ws.splits[idx / a.Hkv];
+  const int h = idx % a.Hkv, b = sp.x, xb = sp.y, n_seg = sp.w;
+  const int first = sp.z + h * n_seg;
+  const RowBlock blk = row_block(a, ctx, qstart, b, xb, rows_wg);
+  if (!blk.ok) return;
+  const int G = a.G, Hq = a.Hkv * G;
+  const int rq = rows_wg / 4;  // rows of this workgroup
+  constexpr int DV = D / 4;
+  for (int t = threadIdx.x; t < rq * DV; t += blockDim.x) {
+    const int rl = blockIdx.y * rq + t / DV, d4 = 4 * (t % DV);
+    const int r = blk.r_wg + rl;
+    if (r >= blk.rows) continue;
+    float M = kNegInf;
+    for (int s = 0; s < n_seg; ++s)
+      M = fmaxf(M, ws.ml[((int64_t)(first + s) * rows_wg + rl) * 2]);
+    const float m_use = M == kNegInf ? 0.f : M;
+    float L = 0.f;
+    f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < n_seg; ++s) {
+      const int64_t pr = (int64_t)(first + s) * rows_wg + rl;
+      const float wgt = exp2_fast(ws.ml[pr * 2] - m_use);
+      L += ws.ml[pr * 2 + 1] * wgt;
+      O += *reinterpret_cast<const f32x4*>(ws.acc + pr * D + d4) * wgt;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    E* o = static_cast<E*>(a.out) + ((int64_t)(blk.q0 + r / G) * Hq + h * G + r % G) * D + d4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = Tr::from_float(O[i] * inv);
   }
 }
 
@@ -624,6 +960,41 @@ void launch_prefill(int head_dim, dim3 grid, hipStream_t stream, const PrefillAr
   }
 }
 
+// The split path's three launches (see prefill_plan_kernel); n_wg workgroups, a
+// multiple of 8, for the persistent kernel.
+template <int DT, int D, bool kFp8>
+void launch_split_d(int n_wg, hipStream_t stream, const PrefillArgs& a, const int32_t* bt,
+                    const int32_t* ctx, const int32_t* qs, const SplitWs& ws) {
+  using S = PrefillShape<DT, D>;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&prefill_split_kernel<DT, D, kFp8>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLdsBytes);
+  (void)attr;
+  prefill_plan_kernel<<<1, kPlanThreads, 0, stream>>>(a, ctx, qs, ws, S::kRowsWG, n_wg);
+  prefill_split_kernel<DT, D, kFp8><<<n_wg, S::kThreads, S::kLdsBytes, stream>>>(a, bt, ctx, qs, ws);
+  prefill_merge_kernel<DT, D><<<dim3(kSplitSlots / 2, 4), 256, 0, stream>>>(a, ctx, qs, ws, S::kRowsWG);
+}
+
+template <int DT, bool kFp8 = false>
+void launch_split(int head_dim, int n_wg, hipStream_t stream, const PrefillArgs& a,
+                  const int32_t* bt, const int32_t* ctx, const int32_t* qs, const SplitWs& ws) {
+  switch (head_dim) {
+    case 64: launch_split_d<DT, 64, kFp8>(n_wg, stream, a, bt, ctx, qs, ws); break;
+    case 128: launch_split_d<DT, 128, kFp8>(n_wg, stream, a, bt, ctx, qs, ws); break;
+    default: launch_split_d<DT, 256, kFp8>(n_wg, stream, a, bt, ctx, qs, ws); break;
+  }
+}
+
+// Workgroups of the split path's persistent grid: one per CU of the current device,
+// rounded down to a multiple of the 8 XCD queues.
+int split_workgroups() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  return cus >= 16 ? cus & ~7 : 8;
+}
+
 template <int DT>
 int rows_per_workgroup_t(int head_dim) {
   switch (head_dim) {
@@ -646,7 +1017,8 @@ int prefill_entry(const char* name, const void* q, const void* k_pool, const voi
                   const int32_t* context_lens, const int32_t* query_start, int n_tok, void* out,
                   int batch, int num_q_heads, int num_kv_heads, int head_dim, int block_size,
                   int max_blocks, int num_pages, int max_query_len, float scale, int window,
-                  int n_sink, int dtype, hipStream_t stream, bool fp8) {
+                  int n_sink, int dtype, hipStream_t stream, bool fp8, bool split = false,
+                  void* workspace = nullptr, size_t workspace_bytes = 0) {
   if (dtype_size(dtype) == 0) return fail(IVAKV_E_DTYPE, "%s: unknown dtype code %d", name, dtype);
   if (fp8 && dtype != IVAKV_F16 && dtype != IVAKV_BF16)
     return fail(IVAKV_E_DTYPE, "%s: FP8 pools take fp16 or bf16 queries (dtype %d)", name, dtype);
@@ -696,6 +1068,41 @@ int prefill_entry(const char* name, const void* q, const void* k_pool, const voi
   a.blocks_x = (int)blocks_x;
   a.k_scale = k_scale;
   a.v_scale = v_scale;
+  a.part_acc = nullptr;
+  a.part_ml = nullptr;
+  if (split) {
+    if (batch > kPlanMaxBatch || num_kv_heads > 32767)
+      return fail(IVAKV_E_SHAPE, "%s: the split path takes batch <= %d and num_kv_heads <= 32767 "
+                  "(got %d, %d); use ivakv_prefill_attn", name, kPlanMaxBatch, batch, num_kv_heads);
+    if (((int64_t)batch * num_kv_heads + kSplitSlots) * blocks_x > 0x7fffffff)
+      return fail(IVAKV_E_SHAPE, "%s: launch too large", name);
+    const SplitLayout lay = split_layout(batch, num_kv_heads, (int)blocks_x, rows_wg, head_dim);
+    if (!workspace || workspace_bytes < lay.total || !aligned16(workspace))
+      return fail(IVAKV_E_WORKSPACE, "%s: workspace of %zu bytes (16-byte aligned) required, got %zu",
+                  name, lay.total, workspace ? workspace_bytes : (size_t)0);
+    char* w = static_cast<char*>(workspace);
+    SplitWs ws;
+    ws.ctl = reinterpret_cast<int32_t*>(w + lay.ctl);
+    ws.vus = reinterpret_cast<int2*>(w + lay.vus);
+    ws.rb = reinterpret_cast<int2*>(w + lay.rb);
+    ws.splits = reinterpret_cast<int4*>(w + lay.splits);
+    ws.acc = reinterpret_cast<float*>(w + lay.acc);
+    ws.ml = reinterpret_cast<float*>(w + lay.ml);
+    a.part_acc = ws.acc;
+    a.part_ml = ws.ml;
+    const int n_wg = split_workgroups();
+    if (fp8) {
+      if (dtype == IVAKV_F16) launch_split<IVAKV_F16, true>(head_dim, n_wg, stream, a, block_tables, context_lens, query_start, ws);
+      else launch_split<IVAKV_BF16, true>(head_dim, n_wg, stream, a, block_tables, context_lens, query_start, ws);
+      return launch_status(name);
+    }
+    switch (dtype) {
+      case IVAKV_F16: launch_split<IVAKV_F16>(head_dim, n_wg, stream, a, block_tables, context_lens, query_start, ws); break;
+      case IVAKV_BF16: launch_split<IVAKV_BF16>(head_dim, n_wg, stream, a, block_tables, context_lens, query_start, ws); break;
+      default: launch_split<IVAKV_F32>(head_dim, n_wg, stream, a, block_tables, context_lens, query_start, ws); break;
+    }
+    return launch_status(name);
+  }
   // 1-D grid in XCD-aware order (see prefill_kernel): 8 interleaved unit streams.
   const int64_t units_per_xcd = ((int64_t)batch * num_kv_heads + 7) / 8;
   const int64_t n_wg = units_per_xcd * blocks_x * 8;
@@ -743,4 +1150,55 @@ extern "C" int ivakv_prefill_attn_fp8(const void* q, const void* k_pool, const v
                        block_tables, context_lens, query_start, n_tok, out, batch, num_q_heads,
                        num_kv_heads, head_dim, block_size, max_blocks, num_pages, max_query_len,
                        scale, window, n_sink, dtype, stream, true);
+}
+
+extern "C" int ivakv_prefill_split_workspace_size(int batch, int num_q_heads, int num_kv_heads,
+                                                  int head_dim, int max_query_len, int dtype,
+                                                  size_t* bytes) {
+  if (!bytes) return fail(IVAKV_E_ARG, "ivakv_prefill_split_workspace_size: null bytes");
+  *bytes = 0;
+  if (dtype_size(dtype) == 0)
+    return fail(IVAKV_E_DTYPE, "ivakv_prefill_split_workspace_size: unknown dtype code %d", dtype);
+  if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_query_len < 0 ||
+      num_q_heads % num_kv_heads != 0 || (head_dim != 64 && head_dim != 128 && head_dim != 256))
+    return fail(IVAKV_E_ARG, "ivakv_prefill_split_workspace_size: bad geometry B=%d Hq=%d Hkv=%d "
+                "D=%d max_query_len=%d", batch, num_q_heads, num_kv_heads, head_dim, max_query_len);
+  const int rows_wg = rows_per_workgroup(dtype, head_dim);
+  const int64_t blocks_x = ((int64_t)max_query_len * (num_q_heads / num_kv_heads) + rows_wg - 1) / rows_wg;
+  if (blocks_x > 0x7fffffff)
+    return fail(IVAKV_E_SHAPE, "ivakv_prefill_split_workspace_size: max_query_len too large");
+  *bytes = split_layout(batch, num_kv_heads, (int)blocks_x, rows_wg, head_dim).total;
+  return IVAKV_OK;
+}
+
+extern "C" int ivakv_prefill_attn_split(const void* q, const void* k_pool, const void* v_pool,
+                                        const int32_t* block_tables, const int32_t* context_lens,
+                                        const int32_t* query_start, int n_tok, void* out,
+                                        void* workspace, size_t workspace_bytes, int batch,
+                                        int num_q_heads, int num_kv_heads, int head_dim,
+                                        int block_size, int max_blocks, int num_pages,
+                                        int max_query_len, float scale, int window, int n_sink,
+                                        int dtype, hipStream_t stream) {
+  return prefill_entry("ivakv_prefill_attn_split", q, k_pool, v_pool, nullptr, nullptr,
+                       block_tables, context_lens, query_start, n_tok, out, batch, num_q_heads,
+                       num_kv_heads, head_dim, block_size, max_blocks, num_pages, max_query_len,
+                       scale, window, n_sink, dtype, stream, false, true, workspace,
+                       workspace_bytes);
+}
+
+extern "C" int ivakv_prefill_attn_split_fp8(const void* q, const void* k_pool, const void* v_pool,
+                                            const float* k_scale, const float* v_scale,
+                                            const int32_t* block_tables,
+                                            const int32_t* context_lens,
+                                            const int32_t* query_start, int n_tok, void* out,
+                                            void* workspace, size_t workspace_bytes, int batch,
+                                            int num_q_heads, int num_kv_heads, int head_dim,
+                                            int block_size, int max_blocks, int num_pages,
+                                            int max_query_len, float scale, int window,
+                                            int n_sink, int dtype, hipStream_t stream) {
+  return prefill_entry("ivakv_prefill_attn_split_fp8", q, k_pool, v_pool, k_scale, v_scale,
+                       block_tables, context_lens, query_start, n_tok, out, batch, num_q_heads,
+                       num_kv_heads, head_dim, block_size, max_blocks, num_pages, max_query_len,
+                       scale, window, n_sink, dtype, stream, true, true, workspace,
+                       workspace_bytes);
 }

@@ -223,6 +223,24 @@ def decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head
     return int(out.value)
 
 
+# Split prefill (ivakv_prefill_attn_split) by default when a walk may exceed this many
+# keys, up to the split path's largest batch.
+SPLIT_MIN_KEYS = 4096
+SPLIT_MAX_BATCH = 4096
+
+
+def prefill_split_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int,
+                                  head_dim: int, max_query_len: int,
+                                  dtype: torch.dtype) -> int:
+    """Workspace bytes of :func:`paged_prefill_attention` with ``split=True`` (its plan
+    and 512 fp32 row-block partials).  The workspace needs no initialisation."""
+    import ctypes
+    out = ctypes.c_size_t(0)
+    _abi.call("ivakv_prefill_split_workspace_size", batch, num_q_heads, num_kv_heads, head_dim,
+              max_query_len, dtype_code(dtype), ctypes.byref(out))
+    return int(out.value)
+
+
 def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream(dev))
     ws = _WORKSPACES.get(key)
@@ -466,7 +484,9 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
                             max_query_len: Optional[int] = None,
                             out: Optional[torch.Tensor] = None,
                             k_scale: Optional[torch.Tensor] = None,
-                            v_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+                            v_scale: Optional[torch.Tensor] = None,
+                            split: Optional[bool] = None,
+                            workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Causal multi-query attention of chunks of new tokens over paged K/V.
 
     ``q`` is ``[n_tok, Hq, D]``; the rows of sequence b are
@@ -481,6 +501,12 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
     FP8 pools (``torch.float8_e4m3fn`` with ``k_scale`` / ``v_scale``) take fp16 or bf16
     queries; keys and values are dequantized (code / sf, rounded to the query dtype)
     on their way into LDS.
+    ``split`` cuts every row block's walk along the keys into segments sized to the
+    batch's work per CU (``ivakv_prefill_attn_split``: plan, persistent grid, merge),
+    so a chunk late in a long context no longer runs as a few long serial walks.  The
+    default (None) splits when a walk may exceed 4096 keys (from the block table's width,
+    or the window); ``workspace`` (:func:`prefill_split_workspace_bytes`) is then
+    allocated and kept per device and stream when omitted.
 
     Replaces ``AttentionTorch.forward`` with a cache and ``seq_len > 1``
     (src/core/attention.py:61-102), with the causal, window and sink masks
@@ -524,6 +550,35 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
         out = torch.empty_like(q)
     elif tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous tensor shaped and typed like q")
+    max_blocks = block_tables.shape[1]
+    if split is None:
+        keys = max_blocks * bs
+        if window > 0:
+            keys = min(keys, window + int(max_query_len) + n_sink)
+        split = keys > SPLIT_MIN_KEYS and batch <= SPLIT_MAX_BATCH
+    if split:
+        nbytes = prefill_split_workspace_bytes(batch, hq, hkv, head_dim, int(max_query_len),
+                                               q.dtype)
+        if workspace is None:
+            workspace = _workspace(dev, nbytes)
+        elif workspace.numel() * workspace.element_size() < nbytes:
+            raise ValueError(f"workspace has {workspace.numel() * workspace.element_size()} "
+                             f"bytes, {nbytes} needed")
+        ws = (workspace.data_ptr(), workspace.numel() * workspace.element_size())
+        if fp8:
+            _abi.call("ivakv_prefill_attn_split_fp8", q.data_ptr(), k_pool.data_ptr(),
+                      v_pool.data_ptr(), scales[0].data_ptr(), scales[1].data_ptr(),
+                      block_tables.data_ptr(), context_lens.data_ptr(), query_start.data_ptr(),
+                      q.shape[0], out.data_ptr(), *ws, batch, hq, hkv, head_dim, bs, max_blocks,
+                      num_pages, int(max_query_len), float(scale), window, n_sink,
+                      dtype_code(q.dtype), _stream(dev))
+        else:
+            _abi.call("ivakv_prefill_attn_split", q.data_ptr(), k_pool.data_ptr(),
+                      v_pool.data_ptr(), block_tables.data_ptr(), context_lens.data_ptr(),
+                      query_start.data_ptr(), q.shape[0], out.data_ptr(), *ws, batch, hq, hkv,
+                      head_dim, bs, max_blocks, num_pages, int(max_query_len), float(scale),
+                      window, n_sink, dtype_code(q.dtype), _stream(dev))
+        return out
     if fp8:
         _abi.call("ivakv_prefill_attn_fp8", q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
                   scales[0].data_ptr(), scales[1].data_ptr(), block_tables.data_ptr(),
