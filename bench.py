@@ -739,23 +739,43 @@ def bench_c5(args, iva, torch, dev):
 def bench_prefill(args, iva, torch, dev):
     """Chunked prefill at C5's chunk size: 16 sequences each appending a 512-token chunk
     on top of 1536 cached positions (context 2048), GQA 32/8, D 128, fp16.  TFLOP/s on
-    algorithmic causal FLOPs: 4 * D * Hq * (visible keys) summed over query rows."""
+    algorithmic causal FLOPs: 4 * D * Hq * (visible keys) summed over query rows.  The
+    value is the op's default path (split, by its work bound); the single-launch kernel,
+    FP8 pages and two long-context batches (one 512-token chunk at 16k keys; chunks at
+    4k / 8k / 16k / 32k) are reported beside it, each split and single-launch."""
     wl = iva.workloads
     measure = _timer(torch, dev)
-    lengths, chunks, hq, hkv, d = [2048] * 16, [512] * 16, 32, 8, 128
-    sets = []
-    for i in range(args.pools):
-        c = wl.prefill_batch(lengths, chunks, hq, hkv, d, torch.float16, seed=20 + i,
-                             device=dev, scale=d ** -0.5)
-        lay = c["layout"]
-        sets.append((c["q"], c["k_pool"], c["v_pool"], lay.block_tables.to(dev),
-                     lay.context_lens.to(dev), c["query_start"].to(dev), torch.empty_like(c["q"])))
-    run = lambda s: iva.paged_prefill_attention(s[0], s[1], s[2], s[3], s[4], s[5],
-                                                max_query_len=512, out=s[6])
-    for s in sets:
-        run(s)
+    hq, hkv, d = 32, 8, 128
     reps = 40
-    t = measure(lambda: [run(sets[i % len(sets)]) for i in range(reps)]) / reps
+
+    def batch_sets(lengths, chunks, n_sets, seed):
+        out = []
+        for i in range(n_sets):
+            c = wl.prefill_batch(lengths, chunks, hq, hkv, d, torch.float16, seed=seed + i,
+                                 device=dev, scale=d ** -0.5)
+            lay = c["layout"]
+            out.append((c["q"], c["k_pool"], c["v_pool"], lay.block_tables.to(dev),
+                        lay.context_lens.to(dev), c["query_start"].to(dev),
+                        torch.empty_like(c["q"])))
+        return out
+
+    def time_sets(sets, max_q, split, n=reps, **kw):
+        # an untimed pass (clocks, caches), then the better of two timed passes
+        run = lambda s: iva.paged_prefill_attention(s[0], s[1], s[2], s[3], s[4], s[5],
+                                                    max_query_len=max_q, out=s[6], split=split,
+                                                    **kw)
+        batch = lambda: [run(sets[i % len(sets)]) for i in range(n)]
+        batch()
+        return min(measure(batch), measure(batch)) / n
+
+    def tflops(lengths, chunks):
+        return sum(4 * d * hq * (L - n + i + 1) for L, n in zip(lengths, chunks) for i in range(n))
+
+    lengths, chunks = [2048] * 16, [512] * 16
+    sets = batch_sets(lengths, chunks, args.pools, 20)
+    t = time_sets(sets, 512, None)
+    t_single = time_sets(sets, 512, False)
+    t_split = time_sets(sets, 512, True)
     # the same batch over FP8 pages (the fp16 rows quantized by the FP8 append)
     sets8 = []
     for s in sets:
@@ -776,23 +796,37 @@ def bench_prefill(args, iva, torch, dev):
     run8 = lambda s: iva.paged_prefill_attention(s[0], s[1], s[2], s[3], s[4], s[5],
                                                  max_query_len=512, out=s[6], k_scale=s[7],
                                                  v_scale=s[8])
-    for s in sets8:
-        run8(s)
-    t8 = measure(lambda: [run8(sets8[i % len(sets8)]) for i in range(reps)]) / reps
-    flops = sum(4 * d * hq * (L - n + i + 1) for L, n in zip(lengths, chunks) for i in range(n))
+    batch8 = lambda: [run8(sets8[i % len(sets8)]) for i in range(reps)]
+    batch8()
+    t8 = min(measure(batch8), measure(batch8)) / reps
+    del sets8
+    flops = tflops(lengths, chunks)
     tf = flops / t / 1e12
+    long_ctx = {}
+    for name, (ll, cc) in {"one_chunk_at_16k": ([16384], [512]),
+                           "chunks_at_4k_8k_16k_32k": ([4096, 8192, 16384, 32768], [512] * 4)}.items():
+        lsets = batch_sets(ll, cc, 2, 60)
+        f = tflops(ll, cc)
+        ts, t1 = time_sets(lsets, 512, True, 10), time_sets(lsets, 512, False, 10)
+        long_ctx[name] = {"split_us": round(ts * 1e6, 1), "split_tflops": round(f / ts / 1e12, 1),
+                          "single_launch_us": round(t1 * 1e6, 1),
+                          "single_launch_tflops": round(f / t1 / 1e12, 1)}
+        del lsets
     mfma_ceiling = max(measure_mfma(torch, dev).values())
     return {"metric": "paged chunked-prefill attention TFLOP/s", "workload": "prefill",
             "value": round(tf, 1), "unit": "TFLOP/s", "dtype": "f16",
             "config": {"sequences": 16, "chunk": 512, "context": 2048, "heads": "32/8",
-                       "head_dim": 128, "launch": "eager"},
+                       "head_dim": 128, "launch": "eager", "path": "default (split)"},
             "kernel_us": round(t * 1e6, 2), "algorithmic_flops": flops,
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0,
                          "unit": "TFLOP/s", "frac": round(tf / 2500.0, 4)},
             "measured_mfma_f16_ceiling_tflops": round(mfma_ceiling, 1),
             "frac_of_measured_mfma_ceiling": round(tf / mfma_ceiling, 4),
+            "single_launch_kernel_us": round(t_single * 1e6, 2),
+            "split_kernel_us": round(t_split * 1e6, 2),
             "fp8_pages_kernel_us": round(t8 * 1e6, 2),
-            "fp8_pages_tflops": round(flops / t8 / 1e12, 1)}
+            "fp8_pages_tflops": round(flops / t8 / 1e12, 1),
+            "long_context": long_ctx}
 
 
 def measure_decode(args, iva, torch, dev, lengths):

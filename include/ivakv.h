@@ -374,7 +374,7 @@ int ivakv_prefill_split_workspace_size(int batch, int num_q_heads, int num_kv_he
  * a persistent grid (one workgroup per CU) runs the (row block, segment) items,
  * longest sequences first, from per-XCD queues, and a merge kernel folds each split
  * block's segments by log-sum-exp.  Three launches, no host synchronisation (graph
- * capture safe).  batch <= 4096, num_kv_heads <= 32767.  The workspace
+ * capture safe).  batch <= 2048, num_kv_heads <= 32767.  The workspace
  * (ivakv_prefill_split_workspace_size) needs no initialisation; calls that share a
  * workspace must not run concurrently.
  * Replaces: the same reference code as ivakv_prefill_attn.

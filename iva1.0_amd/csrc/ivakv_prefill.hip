@@ -680,10 +680,12 @@ constexpr int kSplitSlots = 512;
 // Shortest segment, in pairs of pages (32 keys each); even, as the pair loop needs.
 constexpr int kSplitMinPairs = 16;
 // The plan ranks the sequences by their longest row block in LDS, up to this batch
-// (the split path's largest batch).
-constexpr int kPlanMaxBatch = 4096;
+// (the split path's largest batch), and keeps the row blocks' pair counts in LDS up to
+// kPlanCache row blocks (more: in the workspace).
+constexpr int kPlanMaxBatch = 2048;
 constexpr int kPlanSortBatch = 256;
-constexpr int kPlanThreads = 1024;
+constexpr int kPlanCache = 8192;
+constexpr int kPlanThreads = 256;
 
 // Split workspace.  ctl: [0] virtual units V, [1] split row blocks, [2] segment
 // length in pairs, [32 + 4x] the queue counter of XCD x.  A virtual unit (sequence b,
@@ -767,18 +769,22 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs 
   __shared__ int s_key[kPlanMaxBatch];   // longest row block (pairs) per sequence, -1: none
   __shared__ int s_order[kPlanMaxBatch];  // sequences by rank
   __shared__ int s_pref[kPlanMaxBatch + 1];
+  __shared__ int s_np[kPlanCache];        // pairs of row block e (-1: no rows)
   const int tid = threadIdx.x;
   const int B = a.batch, Hkv = a.Hkv, BX = a.blocks_x;
   const int E = B * BX;
+  const bool cached = E <= kPlanCache;
+  // Row block e's pair count, written and read by the thread of e in every pass.
+  auto np_of = [&](int e) -> int { return cached ? s_np[e] : ws.rb[e].x; };
   for (int b = tid; b < B; b += kPlanThreads) s_key[b] = -1;
   __syncthreads();
-  // 1. Pairs of every row block (kept in rb[].x until the slots replace them), the
-  //    batch's total and each sequence's longest block.
+  // 1. Pairs of every row block, the batch's total and each sequence's longest block.
   int64_t part = 0;
   for (int e = tid; e < E; e += kPlanThreads) {
     const RowBlock blk = row_block(a, ctx, qstart, e / BX, e % BX, rows_wg);
     const int np = blk.ok ? blk.n_pairs : -1;
-    ws.rb[e].x = np;
+    if (cached) s_np[e] = np;
+    else ws.rb[e].x = np;
     if (blk.ok) {
       part += np;
       atomicMax(&s_key[e / BX], np);
@@ -792,7 +798,7 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs 
   for (;;) {
     int64_t need = 0;
     for (int e = tid; e < E; e += kPlanThreads) {
-      const int np = ws.rb[e].x;
+      const int np = np_of(e);
       if (np > seg) need += n_segments(np, seg);
     }
     if (plan_sum(need, s_red64) * Hkv <= kSplitSlots) break;
@@ -845,7 +851,7 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs 
   int slot0 = 0, n_split = 0;
   for (int e0 = 0; e0 < E; e0 += kPlanThreads) {
     const int e = e0 + tid;
-    const int np = e < E ? ws.rb[e].x : -1;
+    const int np = e < E ? np_of(e) : -1;
     const int ns = np > seg ? n_segments(np, seg) : 0;
     int t_slots, t_split;
     const int ex_slots = plan_scan(Hkv * ns, s_red, &t_slots);

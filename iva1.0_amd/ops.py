@@ -223,10 +223,15 @@ def decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head
     return int(out.value)
 
 
-# Split prefill (ivakv_prefill_attn_split) by default when a walk may exceed this many
-# keys, up to the split path's largest batch.
+# Split prefill (ivakv_prefill_attn_split) by default, up to the split path's largest
+# batch, when a walk may exceed SPLIT_MIN_KEYS keys (a chunk late in a long context:
+# 2-3.4x on one 512-token chunk at 8k-64k) or when the launch's work bound, query rows x
+# query heads x keys, reaches SPLIT_MIN_WORK (enough work that the persistent grid's
+# balance pays for the plan and merge launches: 16 x 512 rows at 2048 keys, 7 % faster
+# in fp16; shorter prefills are 2-11 us slower split).
 SPLIT_MIN_KEYS = 4096
-SPLIT_MAX_BATCH = 4096
+SPLIT_MIN_WORK = 1 << 28
+SPLIT_MAX_BATCH = 2048
 
 
 def prefill_split_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int,
@@ -505,8 +510,9 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
     batch's work per CU (``ivakv_prefill_attn_split``: plan, persistent grid, merge),
     so a chunk late in a long context no longer runs as a few long serial walks.  The
     default (None) splits when a walk may exceed 4096 keys (from the block table's width,
-    or the window); ``workspace`` (:func:`prefill_split_workspace_bytes`) is then
-    allocated and kept per device and stream when omitted.
+    or the window) or when rows x query heads x keys reaches 2^28; ``workspace``
+    (:func:`prefill_split_workspace_bytes`) is then allocated and kept per device and
+    stream when omitted.
 
     Replaces ``AttentionTorch.forward`` with a cache and ``seq_len > 1``
     (src/core/attention.py:61-102), with the causal, window and sink masks
@@ -555,7 +561,8 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
         keys = max_blocks * bs
         if window > 0:
             keys = min(keys, window + int(max_query_len) + n_sink)
-        split = keys > SPLIT_MIN_KEYS and batch <= SPLIT_MAX_BATCH
+        split = batch <= SPLIT_MAX_BATCH and (
+            keys > SPLIT_MIN_KEYS or q.shape[0] * hq * keys >= SPLIT_MIN_WORK)
     if split:
         nbytes = prefill_split_workspace_bytes(batch, hq, hkv, head_dim, int(max_query_len),
                                                q.dtype)
