@@ -122,7 +122,7 @@ __device__ inline RowBlock row_block(const PrefillArgs& a, const int32_t* ctx, c
 // Row block xb of (sequence b, kv head h) over pairs [pair_lo, pair_hi) of its walk
 // (pair_lo even).  slot < 0: the block's whole walk, normalized rows into out; slot
 // >= 0: one segment of a split walk, its unnormalized rows (acc, running max, row sum)
-// into partial slot `slot` of the split workspace, for prefill_merge_kernel.  Every
+// into partial slot `slot` of the split workspace, for merge_rows.  Every
 // thread of the workgroup calls it with the same arguments (the returns and barriers
 // inside are uniform).
 template <int DT, int D, bool kFp8>
@@ -666,12 +666,14 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_kerne
 // block's walk into segments of seg_pairs pairs, sized so that the batch's work
 // spreads over every CU (seg_pairs ~ total pairs / CUs), runs (row block, segment)
 // items on a persistent grid that takes them from per-XCD queues, and merges the
-// segments of each split row block by log-sum-exp.  Three launches:
+// segments of each split row block by log-sum-exp.  Two launches:
 //   prefill_plan_kernel   one workgroup: segment size, the item queues (longest
-//                         sequences first), partial slots, the queues' counters
-//                         reset to zero (so the workspace needs no initialisation);
+//                         sequences first), partial slots, and the queues' and the
+//                         split blocks' counters reset to zero (so the workspace needs
+//                         no initialisation);
 //   prefill_split_kernel  one workgroup per CU, items until its XCD's queue is empty;
-//   prefill_merge_kernel  the split row blocks' partials into out.
+//                         the workgroup that completes a split block's last segment
+//                         merges the block's partials into out.
 // ---------------------------------------------------------------------------
 
 // Partial slots (row-block segments) the split workspace holds; the plan doubles the
@@ -688,24 +690,25 @@ constexpr int kPlanCache = 8192;
 constexpr int kPlanThreads = 256;
 
 // Split workspace.  ctl: [0] virtual units V, [1] split row blocks, [2] segment
-// length in pairs, [32 + 4x] the queue counter of XCD x.  A virtual unit (sequence b,
+// length in pairs, [3] partial slots used, [32 + 4x] the queue counter of XCD x.  A virtual unit (sequence b,
 // kv head h, segment s) is packed (b | h << 16, s); the queue of XCD x holds virtual
 // units x, x + 8, ... and a ticket j of it is row block blocks_x - 1 - j % blocks_x of
 // unit x + 8 (j / blocks_x).  rb[b * blocks_x + xb] = (first slot, segments) of a
 // split row block ((-1, 1) unsplit, (-1, 0) no rows); the slot of segment s of kv
-// head h is first + h * segments + s.
+// head h is first + h * segments + s; arrive[first] counts that block's finished
+// segments.
 struct SplitWs {
   int32_t* ctl;
-  int2* vus;     // [batch * Hkv + kSplitSlots]
-  int2* rb;      // [batch * blocks_x]
-  int4* splits;  // [kSplitSlots / 2] (b | h << 16 unused: b, xb, first slot, segments)
-  float* acc;    // [kSplitSlots][rows_wg][D]
-  float* ml;     // [kSplitSlots][rows_wg][2]
+  int2* vus;       // [batch * Hkv + kSplitSlots]
+  int2* rb;        // [batch * blocks_x]
+  int32_t* arrive; // [kSplitSlots]
+  float* acc;      // [kSplitSlots][rows_wg][D]
+  float* ml;       // [kSplitSlots][rows_wg][2]
 };
 
 // Byte layout of the split workspace (each part 256-byte aligned).
 struct SplitLayout {
-  size_t ctl, vus, rb, splits, acc, ml, total;
+  size_t ctl, vus, rb, arrive, acc, ml, total;
 };
 inline SplitLayout split_layout(int batch, int num_kv_heads, int blocks_x, int rows_wg, int head_dim) {
   auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
@@ -713,8 +716,8 @@ inline SplitLayout split_layout(int batch, int num_kv_heads, int blocks_x, int r
   l.ctl = 0;
   l.vus = up(l.ctl + 64 * sizeof(int32_t));
   l.rb = up(l.vus + ((size_t)batch * num_kv_heads + kSplitSlots) * sizeof(int2));
-  l.splits = up(l.rb + (size_t)batch * blocks_x * sizeof(int2));
-  l.acc = up(l.splits + (size_t)(kSplitSlots / 2) * sizeof(int4));
+  l.arrive = up(l.rb + (size_t)batch * blocks_x * sizeof(int2));
+  l.acc = up(l.arrive + (size_t)kSplitSlots * sizeof(int32_t));
   l.ml = up(l.acc + (size_t)kSplitSlots * rows_wg * head_dim * sizeof(float));
   l.total = up(l.ml + (size_t)kSplitSlots * rows_wg * 2 * sizeof(float));
   return l;
@@ -847,28 +850,100 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillArgs 
     const int b = s_order[lo], local = g - s_pref[lo];
     ws.vus[g] = int2{b | ((local % Hkv) << 16), local / Hkv};
   }
-  // 5. Slots of the split row blocks, in (sequence, row block) order, and their list.
+  // 5. Slots of the split row blocks, in (sequence, row block) order.
   int slot0 = 0, n_split = 0;
   for (int e0 = 0; e0 < E; e0 += kPlanThreads) {
     const int e = e0 + tid;
     const int np = e < E ? np_of(e) : -1;
     const int ns = np > seg ? n_segments(np, seg) : 0;
-    int t_slots, t_split;
+    int t_slots;
     const int ex_slots = plan_scan(Hkv * ns, s_red, &t_slots);
-    const int ex_split = plan_scan(ns > 0 ? 1 : 0, s_red, &t_split);
-    if (e < E) {
-      ws.rb[e] = ns > 0 ? int2{slot0 + ex_slots, ns} : int2{-1, np < 0 ? 0 : 1};
-      if (ns > 0) ws.splits[n_split + ex_split] = int4{e / BX, e % BX, slot0 + ex_slots, ns};
-    }
+    if (e < E) ws.rb[e] = ns > 0 ? int2{slot0 + ex_slots, ns} : int2{-1, np < 0 ? 0 : 1};
+    n_split += ns > 0 ? 1 : 0;
     slot0 += t_slots;
-    n_split += t_split;
   }
+  n_split = (int)plan_sum(n_split, s_red64);
   if (tid == 0) {
     ws.ctl[0] = V;
     ws.ctl[1] = n_split;
     ws.ctl[2] = seg;
+    ws.ctl[3] = slot0;
   }
   if (tid < 8) ws.ctl[32 + 4 * tid] = 0;
+  for (int i = tid; i < kSplitSlots; i += kPlanThreads) ws.arrive[i] = 0;
+}
+
+// Log-sum-exp merge of the n_seg segments (partial slots first ..) of row block blk of
+// kv head h into out, by the whole workgroup.  A thread takes EG f32x4 elements (rows
+// x 4 dims) at once and folds their segments U at a time, so EG * U partial loads are
+// in flight per step rather than one element's.
+template <int DT, int D>
+__device__ inline void merge_rows(const PrefillArgs& a, const SplitWs& ws, const RowBlock& blk,
+                                  int h, int first, int n_seg, int rows_wg) {
+  using Tr = Traits<DT>;
+  using E = typename Tr::E;
+  constexpr int DV = D / 4;
+  constexpr int EG = D == 256 ? 2 : 4;
+  constexpr int U = 4;
+  const int G = a.G, Hq = a.Hkv * G;
+  const int n_el = rows_wg * DV, nt = blockDim.x;
+  for (int t0 = threadIdx.x; t0 < n_el; t0 += EG * nt) {
+    float M[EG], L[EG];
+    f32x4 O[EG];
+#pragma unroll
+    for (int k = 0; k < EG; ++k) {
+      M[k] = kNegInf;
+      L[k] = 0.f;
+      O[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int s0 = 0; s0 < n_seg; s0 += U) {
+      float mv[EG][U], lv[EG][U];
+      f32x4 ov[EG][U];
+#pragma unroll
+      for (int k = 0; k < EG; ++k) {
+        const int t = min(t0 + k * nt, n_el - 1);
+        const int rl = t / DV, d4 = 4 * (t % DV);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t pr = (int64_t)(first + min(s0 + u, n_seg - 1)) * rows_wg + rl;
+          mv[k][u] = ws.ml[pr * 2];
+          lv[k][u] = ws.ml[pr * 2 + 1];
+          ov[k][u] = *reinterpret_cast<const f32x4*>(ws.acc + pr * D + d4);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < EG; ++k) {
+        float mc = M[k];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          mv[k][u] = s0 + u < n_seg ? mv[k][u] : kNegInf;
+          mc = fmaxf(mc, mv[k][u]);
+        }
+        const float m_use = mc == kNegInf ? 0.f : mc;
+        const float f = exp2_fast(M[k] - m_use);
+        L[k] *= f;
+        O[k] *= f;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float w = exp2_fast(mv[k][u] - m_use);
+          L[k] += lv[k][u] * w;
+          O[k] += ov[k][u] * w;
+        }
+        M[k] = mc;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < EG; ++k) {
+      const int t = t0 + k * nt;
+      const int rl = t / DV, d4 = 4 * (t % DV);
+      const int r = blk.r_wg + rl;
+      if (t >= n_el || r >= blk.rows) continue;
+      const float inv = L[k] > 0.f ? 1.f / L[k] : 0.f;
+      E* o = static_cast<E*>(a.out) + ((int64_t)(blk.q0 + r / G) * Hq + h * G + r % G) * D + d4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = Tr::from_float(O[k][i] * inv);
+    }
+  }
 }
 
 // Persistent grid of the split path: workgroup w serves the queue of XCD w % 8 (the
@@ -878,7 +953,9 @@ template <int DT, int D, bool kFp8>
 __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_split_kernel(
     PrefillArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ ctx,
     const int32_t* __restrict__ qstart, SplitWs ws) {
+  using S = PrefillShape<DT, D>;
   __shared__ int s_ticket[2];
+  __shared__ int s_last;
   const int x = blockIdx.x & 7;
   // (V is at most the unit list's capacity; the clamp keeps every list read inside it.)
   const int V = min(ws.ctl[0], a.batch * a.Hkv + kSplitSlots), seg = max(ws.ctl[2], 2);
@@ -897,51 +974,35 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_split
     const int b = vu.x & 0xffff, h = vu.x >> 16, s = vu.y;
     const int2 rb = ws.rb[b * a.blocks_x + xb];
     if (s >= rb.y) continue;  // the block has no rows, or fewer segments
-    if (rb.y > 1)
-      prefill_rows<DT, D, kFp8>(a, bt, ctx, qstart, b, h, xb, s * seg, (s + 1) * seg, rb.x + h * rb.y + s);
-    else
+    if (rb.y == 1) {
       prefill_rows<DT, D, kFp8>(a, bt, ctx, qstart, b, h, xb, 0, 0x7fffffff, -1);
-  }
-}
-
-// Log-sum-exp merge of a split row block's segments: workgroup (split row block * Hkv
-// + kv head, row quarter), one f32x4 of a row per thread and step.
-template <int DT, int D>
-__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a, const int32_t* __restrict__ ctx,
-                                                            const int32_t* __restrict__ qstart,
-                                                            SplitWs ws, int rows_wg) {
-  using Tr = Traits<DT>;
-  using E = typename Tr::E;
-  const int idx = blockIdx.x;
-  if (idx >= ws.ctl[1] * a.Hkv) return;
-  const int4 sp = ws.splits[idx / a.Hkv];
-  const int h = idx % a.Hkv, b = sp.x, xb = sp.y, n_seg = sp.w;
-  const int first = sp.z + h * n_seg;
-  const RowBlock blk = row_block(a, ctx, qstart, b, xb, rows_wg);
-  if (!blk.ok) return;
-  const int G = a.G, Hq = a.Hkv * G;
-  const int rq = rows_wg / 4;  // rows of this workgroup
-  constexpr int DV = D / 4;
-  for (int t = threadIdx.x; t < rq * DV; t += blockDim.x) {
-    const int rl = blockIdx.y * rq + t / DV, d4 = 4 * (t % DV);
-    const int r = blk.r_wg + rl;
-    if (r >= blk.rows) continue;
-    float M = kNegInf;
-    for (int s = 0; s < n_seg; ++s)
-      M = fmaxf(M, ws.ml[((int64_t)(first + s) * rows_wg + rl) * 2]);
-    const float m_use = M == kNegInf ? 0.f : M;
-    float L = 0.f;
-    f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < n_seg; ++s) {
-      const int64_t pr = (int64_t)(first + s) * rows_wg + rl;
-      const float wgt = exp2_fast(ws.ml[pr * 2] - m_use);
-      L += ws.ml[pr * 2 + 1] * wgt;
-      O += *reinterpret_cast<const f32x4*>(ws.acc + pr * D + d4) * wgt;
+      continue;
     }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    E* o = static_cast<E*>(a.out) + ((int64_t)(blk.q0 + r / G) * Hq + h * G + r % G) * D + d4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = Tr::from_float(O[i] * inv);
+    prefill_rows<DT, D, kFp8>(a, bt, ctx, qstart, b, h, xb, s * seg, (s + 1) * seg,
+                              rb.x + h * rb.y + s);
+    // Count the segment in: the barrier waits for every wave's partial stores (in this
+    // XCD's L2), one agent-scope release writes them back where the other XCDs read,
+    // then the arrival is counted.  The workgroup that counts the last segment
+    // acquires (drops its L2's stale lines) and merges the block.  (The item is read
+    // again from its ticket, which stays in LDS until the next one: nothing of it
+    // stays live across the walk.)
+    __syncthreads();
+    const int2 vu2 = ws.vus[x + 8 * (s_ticket[it & 1] / a.blocks_x)];
+    const int xb2 = a.blocks_x - 1 - s_ticket[it & 1] % a.blocks_x;
+    const int b2 = vu2.x & 0xffff, h2 = vu2.x >> 16;
+    const int2 rb2 = ws.rb[b2 * a.blocks_x + xb2];
+    const int first = rb2.x + h2 * rb2.y;
+    if (threadIdx.x == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      s_last = __hip_atomic_fetch_add(ws.arrive + first, 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == rb2.y - 1;
+    }
+    __syncthreads();
+    if (s_last) {  // uniform
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      const RowBlock blk = row_block(a, ctx, qstart, b2, xb2, S::kRowsWG);
+      merge_rows<DT, D>(a, ws, blk, h2, first, rb2.y, S::kRowsWG);
+    }
   }
 }
 
@@ -966,7 +1027,7 @@ void launch_prefill(int head_dim, dim3 grid, hipStream_t stream, const PrefillAr
   }
 }
 
-// The split path's three launches (see prefill_plan_kernel); n_wg workgroups, a
+// The split path's two launches (see prefill_plan_kernel); n_wg workgroups, a
 // multiple of 8, for the persistent kernel.
 template <int DT, int D, bool kFp8>
 void launch_split_d(int n_wg, hipStream_t stream, const PrefillArgs& a, const int32_t* bt,
@@ -978,7 +1039,6 @@ void launch_split_d(int n_wg, hipStream_t stream, const PrefillArgs& a, const in
   (void)attr;
   prefill_plan_kernel<<<1, kPlanThreads, 0, stream>>>(a, ctx, qs, ws, S::kRowsWG, n_wg);
   prefill_split_kernel<DT, D, kFp8><<<n_wg, S::kThreads, S::kLdsBytes, stream>>>(a, bt, ctx, qs, ws);
-  prefill_merge_kernel<DT, D><<<dim3(kSplitSlots / 2, 4), 256, 0, stream>>>(a, ctx, qs, ws, S::kRowsWG);
 }
 
 template <int DT, bool kFp8 = false>
@@ -1091,7 +1151,7 @@ int prefill_entry(const char* name, const void* q, const void* k_pool, const voi
     ws.ctl = reinterpret_cast<int32_t*>(w + lay.ctl);
     ws.vus = reinterpret_cast<int2*>(w + lay.vus);
     ws.rb = reinterpret_cast<int2*>(w + lay.rb);
-    ws.splits = reinterpret_cast<int4*>(w + lay.splits);
+    ws.arrive = reinterpret_cast<int32_t*>(w + lay.arrive);
     ws.acc = reinterpret_cast<float*>(w + lay.acc);
     ws.ml = reinterpret_cast<float*>(w + lay.ml);
     a.part_acc = ws.acc;

@@ -173,6 +173,12 @@ def test_split_plan_invariants_and_garbage_workspace(iva, dev):
         assert int(ctl[32 + 4 * x]) == units * blocks_x + n_wg // 8, x
     assert seg >= 16 and seg % 2 == 0
     assert n_split >= 1  # the 4000-key chunk splits
+    # every segment of a split block counted in once: the arrival counters (the part
+    # after the control block, the unit list and the row-block table) sum to the slots
+    up = lambda v: (v + 255) & ~255
+    arrive = up(up(up(256) + (len(lengths) * hkv + SLOTS) * 8) + len(lengths) * blocks_x * 8)
+    counts = ws[arrive:arrive + 4 * SLOTS].view(torch.int32).cpu()
+    assert int(counts.sum()) == int(ctl[3]) > 0
     assert_close(out1, oracle(c), torch.float16, "garbage workspace")
     out2 = run(iva, dev, c, split=True, workspace=ws, max_query_len=max_q)
     assert torch.equal(out1, out2)
