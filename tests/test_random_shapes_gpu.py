@@ -5,7 +5,7 @@ lengths (empty sequences and page boundaries included), a sliding window and sin
 then checks the stream walk, the partitioned walk, the fused append + attend op (pools
 bit-identical to ivakv_append of the same rows; it takes the stream walk or, for
 batches with a unit per CU and short tables, one partition per sequence) and chunked
-prefill.  Tolerance as in the other GPU tests: 2e-3 (fp16 / bf16) or 1e-5 (fp32) plus
+prefill, single-launch and split.  Tolerance as in the other GPU tests: 2e-3 (fp16 / bf16) or 1e-5 (fp32) plus
 one half-ulp of the output dtype times the exact value.
 """
 from __future__ import annotations
@@ -89,7 +89,7 @@ def test_decode_paths_random(iva, dev, seed):
     assert_close(out, ref_f, dtype, "fused " + what)
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(12))
 def test_prefill_random(iva, dev, seed):
     batch, hkv, g, d, dtype, lengths, window, n_sink = draw(1000 + seed)
     batch = min(batch, 12)
@@ -100,10 +100,14 @@ def test_prefill_random(iva, dev, seed):
     c = iva.workloads.prefill_batch(lengths, chunks, hkv * g, hkv, d, dtype, seed=400 + seed,
                                     scale=d ** -0.5)
     lay = c["layout"]
-    out = iva.paged_prefill_attention(c["q"].to(dev), c["k_pool"].to(dev), c["v_pool"].to(dev),
-                                      lay.block_tables.to(dev), lay.context_lens.to(dev),
-                                      c["query_start"].to(dev), window=window, n_sink=n_sink)
     ref = orc.prefill_attention(to_np(c["q"]), to_np(c["k_pool"]), to_np(c["v_pool"]),
                                 lay.block_tables.numpy(), lay.context_lens.numpy(),
                                 c["query_start"].numpy(), window=window, n_sink=n_sink)
-    assert_close(out, ref, dtype, "prefill " + what)
+    # the single-launch kernel and the split path (segments of >= 16 pairs: contexts
+    # past 512 keys split)
+    for split in (False, True):
+        out = iva.paged_prefill_attention(c["q"].to(dev), c["k_pool"].to(dev),
+                                          c["v_pool"].to(dev), lay.block_tables.to(dev),
+                                          lay.context_lens.to(dev), c["query_start"].to(dev),
+                                          window=window, n_sink=n_sink, split=split)
+        assert_close(out, ref, dtype, f"prefill split={split} " + what)
