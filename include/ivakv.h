@@ -370,13 +370,13 @@ int ivakv_prefill_split_workspace_size(int batch, int num_q_heads, int num_kv_he
  * query dtype against their own running maxima), for batches whose longest chunks
  * sit on long contexts.  ivakv_prefill_attn gives a row block one workgroup, so a
  * 512-token chunk at 16k keys occupies 64 workgroups for the whole launch; here a plan
- * kernel cuts every row block's walk into segments of about (total work / CUs),
- * a persistent grid (one workgroup per CU) runs the (row block, segment) items,
- * longest sequences first, from per-XCD queues, and a merge kernel folds each split
- * block's segments by log-sum-exp.  Three launches, no host synchronisation (graph
- * capture safe).  batch <= 2048, num_kv_heads <= 32767.  The workspace
- * (ivakv_prefill_split_workspace_size) needs no initialisation; calls that share a
- * workspace must not run concurrently.
+ * kernel cuts every row block's walk into segments of about (total work / CUs), and a
+ * persistent grid (one workgroup per CU) runs the (row block, segment) items, longest
+ * sequences first, from per-XCD queues; the workgroup that finishes a split block's
+ * last segment folds its segments by log-sum-exp.  Two launches, no host
+ * synchronisation (graph capture safe).  batch <= 2048, num_kv_heads <= 32767.  The
+ * workspace (ivakv_prefill_split_workspace_size) needs no initialisation; calls that
+ * share a workspace must not run concurrently.
  * Replaces: the same reference code as ivakv_prefill_attn.
  */
 int ivakv_prefill_attn_split(const void* q, const void* k_pool, const void* v_pool,
