@@ -14,7 +14,7 @@ FP8 pools (torch.float8_e4m3fn) carry one fp32 scaling factor per (slot, kv head
 from __future__ import annotations
 
 import math
-from typing import Dict, Optional, Tuple
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
@@ -246,10 +246,19 @@ def prefill_split_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: in
     return int(out.value)
 
 
+# Workspaces replaced by larger ones stay allocated: a HIP graph captured with one keeps
+# its address, and freeing it would let the caching allocator hand that memory out
+# while the graph still writes there.
+_RETIRED_WORKSPACES: List[torch.Tensor] = []
+
+
 def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """The op-owned workspace of (device, current stream), grown to at least nbytes."""
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream(dev))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _RETIRED_WORKSPACES.append(ws)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
         _WORKSPACES[key] = ws
     return ws

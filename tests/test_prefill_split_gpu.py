@@ -221,3 +221,34 @@ def test_split_argument_errors(iva, dev):
                       args[2].data_ptr(), args[3].data_ptr(), args[4].data_ptr(),
                       args[5].data_ptr(), 40, args[0].data_ptr(), None, 0, 1, 4, 2, 64, 16,
                       args[3].shape[1], args[1].shape[0], 40, 0.125, 0, 0, 1, None)
+
+
+def test_captured_decode_survives_workspace_growth(iva, dev):
+    """A decode step captured in a HIP graph with the op-owned workspace keeps working
+    after a split prefill on the same stream grows that workspace: the smaller one stays
+    allocated, so every replay equals the eager decode and memory handed out after the
+    growth is never written by the replays."""
+    d = iva.workloads.decode_batch([700, 90, 1300], 8, 2, 64, torch.float16, seed=5,
+                                   scale=0.125, device=dev)
+    lay = d["layout"]
+    dargs = (d["q"], d["k_pool"], d["v_pool"], lay.block_tables.to(dev), lay.context_lens.to(dev))
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        eager = iva.paged_decode_attention(*dargs)
+        out = torch.empty_like(eager)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            iva.paged_decode_attention(*dargs, out=out)
+        c = make(iva, [4000, 2000], [300, 64], 8, 2, 128, torch.float16, seed=7)
+        for _ in range(2):  # grows the stream's workspace, then reuses the new one
+            iva.paged_prefill_attention(*dev_args(c, dev), split=True)
+        junk = torch.full((1 << 24,), 7, dtype=torch.int32, device=dev)  # reuse of freed memory
+        for _ in range(3):
+            out.zero_()
+            g.replay()
+            stream.synchronize()
+            assert torch.equal(out, eager)
+        assert bool((junk == 7).all())
+        del junk
+    torch.cuda.current_stream(dev).wait_stream(stream)
