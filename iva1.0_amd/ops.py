@@ -232,6 +232,7 @@ def decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head
 SPLIT_MIN_KEYS = 4096
 SPLIT_MIN_WORK = 1 << 28
 SPLIT_MAX_BATCH = 2048
+SPLIT_MAX_KV_HEADS = 32767
 
 
 def prefill_split_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int,
@@ -570,7 +571,7 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
         keys = max_blocks * bs
         if window > 0:
             keys = min(keys, window + int(max_query_len) + n_sink)
-        split = batch <= SPLIT_MAX_BATCH and (
+        split = batch <= SPLIT_MAX_BATCH and hkv <= SPLIT_MAX_KV_HEADS and (
             keys > SPLIT_MIN_KEYS or q.shape[0] * hq * keys >= SPLIT_MIN_WORK)
     if split:
         nbytes = prefill_split_workspace_bytes(batch, hq, hkv, head_dim, int(max_query_len),
