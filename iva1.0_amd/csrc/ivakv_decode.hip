@@ -539,16 +539,16 @@ __global__ __launch_bounds__(kThreads, partial_wgs_per_cu(D)) void decode_partia
 // Log-sum-exp fold of n partial (max, sum, acc) slots into one running state
 // (M, L, O) of VEC consecutive output elements idx .. idx+VEC-1 (query head g; idx
 // a multiple of VEC, so they share the head); slot(i) gives the workspace slot of
-// the i-th partial.  One online pass loads 16 partials' (max, sum, acc) together,
-// so the merge costs one memory round trip per 16 partials instead of separate max
-// / sum / accumulate passes.
-template <int VEC, typename SlotFn>
+// the i-th partial.  One online pass loads U partials' (max, sum, acc) together, so
+// the merge costs one memory round trip per U partials instead of separate max / sum
+// / accumulate passes; U is sized to the partials a unit usually has (loads past n
+// repeat the last slot, so a larger U only adds load instructions).
+template <int VEC, int U, typename SlotFn>
 __device__ inline void fold_slots(const DecodeArgs& a, int g, int idx, int D, int n, SlotFn slot,
                                   float& M, float& L,
                                   typename std::conditional<VEC == 4, f32x4, float>::type& O) {
   using OV = typename std::conditional<VEC == 4, f32x4, float>::type;
   const int G = a.G;
-  constexpr int U = 16;
   for (int i0 = 0; i0 < n; i0 += U) {
     float mv[U], lv[U];
     OV av[U];
@@ -588,6 +588,13 @@ __device__ inline void fold_slots(const DecodeArgs& a, int g, int idx, int D, in
 constexpr int kMergeVec4Units = 1024;
 constexpr int kMergeSplitUnits = 256;
 constexpr int kSplitters = 4;
+// Partials the stream walk's merges fold per round trip, by merge shape: a unit has
+// about waves / units + 1 fragments, so at most 2 when units are many enough for
+// four-element lanes (>= kMergeVec4Units), about 5 for one element per thread, and up
+// to hundreds (a quarter per splitter lane) below kMergeSplitUnits.
+constexpr int stream_fold_width(int vec, int splitters) {
+  return vec == 4 ? 4 : splitters > 1 ? 16 : 8;
+}
 
 // Log-sum-exp combine of the (M, L, O) states of lanes l, l ^ 16, l ^ 32, l ^ 48.
 __device__ inline void combine_splitters(float& M, float& L, float& O) {
@@ -635,7 +642,7 @@ struct MergeLanes {
 // Merge of n partial slots into the out rows of unit (b, h), over the elements of
 // MergeLanes<VEC, S> (spread over the workgroup and grid z: a unit is split across
 // workgroups when units are fewer than CUs).
-template <int DT, int VEC, int S, typename SlotFn>
+template <int DT, int VEC, int S, int U, typename SlotFn>
 __device__ inline void merge_slots(const DecodeArgs& a, int b, int h, int n, int D, SlotFn slot) {
   using E = typename Traits<DT>::E;
   const int G = a.G;
@@ -647,7 +654,7 @@ __device__ inline void merge_slots(const DecodeArgs& a, int b, int h, int n, int
   for (int idx = ml.first; idx < G * D; idx += ml.step) {
     float M = kNegInf, L = 0.f;
     typename std::conditional<VEC == 4, f32x4, float>::type O = {};
-    fold_slots<VEC>(a, idx / D, idx, D, cnt, [&](int i) { return slot(i0 + i); }, M, L, O);
+    fold_slots<VEC, U>(a, idx / D, idx, D, cnt, [&](int i) { return slot(i0 + i); }, M, L, O);
     if constexpr (VEC == 4) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) out[idx + r] = Traits<DT>::from_float(L > 0.f ? O[r] / L : 0.f);
@@ -666,7 +673,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a, int D) 
   const int n_parts = num_partitions(w, a);
   if (n_parts <= 1) return;
   const int64_t base = ((int64_t)b * a.Hkv + h) * a.n_parts_max;
-  merge_slots<DT, 1, 1>(a, b, h, n_parts, D, [&](int i) { return base + i; });
+  merge_slots<DT, 1, 1, 16>(a, b, h, n_parts, D, [&](int i) { return base + i; });
 }
 
 // ---------------------------------------------------------------------------
@@ -903,7 +910,8 @@ __global__ __launch_bounds__(256) void decode_stream_merge_kernel(DecodeArgs a, 
   const int64_t k0 = split.owner(first_tile), k1 = split.owner(first_tile + n - 1);
   if (k0 == k1) return;
   const int64_t base = k0 + (int64_t)b * Hkv + h;
-  merge_slots<DT, VEC, S>(a, b, h, (int)(k1 - k0 + 1), D, [&](int i) { return base + i; });
+  merge_slots<DT, VEC, S, stream_fold_width(VEC, S)>(a, b, h, (int)(k1 - k0 + 1), D,
+                                                    [&](int i) { return base + i; });
 }
 
 // Fused append's merge: grid (kv head, sequence, column split), 256 or 64 threads.  Scores the new
@@ -1017,7 +1025,8 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
     }
     float M = kNegInf, L_sum = 0.f;
     typename std::conditional<VEC == 4, f32x4, float>::type O = {};
-    fold_slots<VEC>(a, g, idx, D, fcnt, [&](int i) { return base + f0 + i; }, M, L_sum, O);
+    fold_slots<VEC, stream_fold_width(VEC, S)>(a, g, idx, D, fcnt,
+                                               [&](int i) { return base + f0 + i; }, M, L_sum, O);
     if constexpr (S > 1) combine_splitters(M, L_sum, O);
     float dot = 0.f;
 #pragma unroll
