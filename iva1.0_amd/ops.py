@@ -235,6 +235,20 @@ SPLIT_MAX_BATCH = 2048
 SPLIT_MAX_KV_HEADS = 32767
 
 
+def prefill_split_default(batch: int, num_q_heads: int, num_kv_heads: int, n_tok: int,
+                          max_query_len: int, max_blocks: int, block_size: int,
+                          window: int = 0, n_sink: int = 0) -> bool:
+    """:func:`paged_prefill_attention`'s default for ``split``: within the split path's
+    batch and kv-head limits, when the longest walk the table allows (its width in keys,
+    or window + chunk + sinks) exceeds SPLIT_MIN_KEYS, or when query rows x query heads x
+    those keys reaches SPLIT_MIN_WORK."""
+    keys = max_blocks * block_size
+    if window and window > 0:
+        keys = min(keys, window + max_query_len + max(n_sink, 0))
+    return batch <= SPLIT_MAX_BATCH and num_kv_heads <= SPLIT_MAX_KV_HEADS and (
+        keys > SPLIT_MIN_KEYS or n_tok * num_q_heads * keys >= SPLIT_MIN_WORK)
+
+
 def prefill_split_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int,
                                   head_dim: int, max_query_len: int,
                                   dtype: torch.dtype) -> int:
@@ -568,11 +582,8 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
         raise ValueError("out must be a contiguous tensor shaped and typed like q")
     max_blocks = block_tables.shape[1]
     if split is None:
-        keys = max_blocks * bs
-        if window > 0:
-            keys = min(keys, window + int(max_query_len) + n_sink)
-        split = batch <= SPLIT_MAX_BATCH and hkv <= SPLIT_MAX_KV_HEADS and (
-            keys > SPLIT_MIN_KEYS or q.shape[0] * hq * keys >= SPLIT_MIN_WORK)
+        split = prefill_split_default(batch, hq, hkv, q.shape[0], int(max_query_len), max_blocks,
+                                      bs, window, n_sink)
     if split:
         nbytes = prefill_split_workspace_bytes(batch, hq, hkv, head_dim, int(max_query_len),
                                                q.dtype)

@@ -76,3 +76,24 @@ def test_traffic_summary_scales_and_cross_checks(tmp_path, monkeypatch):
 def test_committed_traffic_summary_is_read():
     assert bench.read_traffic("c2") == json.loads(
         (ROOT / "profiles" / "decode_attn_c2_traffic.json").read_text())["hbm_bytes_per_launch"]
+
+
+def test_prefill_split_default(iva):
+    """The split-prefill default on the shapes the measurements were taken on."""
+    from importlib import import_module
+    ops = import_module("iva_amd.ops")
+    split = ops.prefill_split_default
+    # C3's prefill layer: 16 x 512 rows, 16 heads, a 48-page table -> single launch
+    assert not split(16, 16, 16, 16 * 512, 512, 48, 16)
+    # short batches (4 x 128 at 256 keys, 8 x 64 at 1024 keys) -> single launch
+    assert not split(4, 32, 8, 4 * 128, 128, 16, 16)
+    assert not split(8, 32, 8, 8 * 64, 64, 64, 16)
+    # the prefill line: 16 x 512 rows, 32 heads, 2048 keys: work bound 2^29 -> split
+    assert split(16, 32, 8, 16 * 512, 512, 128, 16)
+    # a table wider than 4096 keys (C5's pools, long prompts) -> split, even for one row
+    assert split(1, 32, 8, 1, 1, 1024, 16)
+    # ... unless a window bounds the walk: 256 + 64 + 4 keys
+    assert not split(1, 32, 8, 64, 64, 1024, 16, window=256, n_sink=4)
+    # outside the split path's limits -> single launch
+    assert not split(ops.SPLIT_MAX_BATCH + 1, 32, 8, 4096, 512, 1024, 16)
+    assert not split(4, 32768, 32768, 4, 1, 1024, 16)
