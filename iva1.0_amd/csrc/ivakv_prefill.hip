@@ -980,12 +980,14 @@ __global__ __launch_bounds__((PrefillShape<DT, D>::kThreads)) void prefill_split
     }
     prefill_rows<DT, D, kFp8>(a, bt, ctx, qstart, b, h, xb, s * seg, (s + 1) * seg,
                               rb.x + h * rb.y + s);
-    // Count the segment in: the barrier waits for every wave's partial stores (in this
-    // XCD's L2), one agent-scope release writes them back where the other XCDs read,
-    // then the arrival is counted.  The workgroup that counts the last segment
-    // acquires (drops its L2's stale lines) and merges the block.  (The item is read
-    // again from its ticket, which stays in LDS until the next one: nothing of it
-    // stays live across the walk.)
+    // Count the segment in: every wave waits until its partial stores have reached this
+    // XCD's L2 (the barrier alone waits only for LDS traffic), then thread 0's
+    // agent-scope release writes them back where the other XCDs read, and the arrival
+    // is counted.  The workgroup that counts the last segment acquires (drops its
+    // L2's stale lines) and merges the block.  (The item is read again from its
+    // ticket, which stays in LDS until the next one: nothing of it stays live across
+    // the walk.)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     const int2 vu2 = ws.vus[x + 8 * (s_ticket[it & 1] / a.blocks_x)];
     const int xb2 = a.blocks_x - 1 - s_ticket[it & 1] % a.blocks_x;
