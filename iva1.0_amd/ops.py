@@ -268,13 +268,17 @@ _RETIRED_WORKSPACES: List[torch.Tensor] = []
 
 
 def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
-    """The op-owned workspace of (device, current stream), grown to at least nbytes."""
+    """The op-owned workspace of (device, current stream), grown to at least nbytes.
+    A replacement is at least twice the size it replaces, so the retired workspaces
+    together stay smaller than the live one."""
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream(dev))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        grown = 1
         if ws is not None:
             _RETIRED_WORKSPACES.append(ws)
-        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+            grown = 2 * ws.numel()
+        ws = torch.empty(max(nbytes, grown), dtype=torch.uint8, device=dev)
         _WORKSPACES[key] = ws
     return ws
 
