@@ -264,6 +264,41 @@ def test_c2_fused_step_full_size(iva, dev):
     print(f"C2 fused step: max abs err vs fp64 oracle {err:.2e} over all 32 sequences")
 
 
+@pytest.mark.parametrize("batch", [8192, 8193, 9000])
+def test_batches_around_the_stream_walk_limit(iva, dev, batch):
+    """Up to 8192 sequences take the stream walk, more the partitioned walk: the default
+    op and the fused step at and past the switch, short contexts (empty ones included),
+    checked against the fp64 oracle on 160 sequences (both ends and a random sample);
+    the fused step's pools are bit-identical to kv_append of the new rows."""
+    gen = torch.Generator().manual_seed(batch)
+    lengths = torch.randint(0, 41, (batch,), generator=gen).tolist()
+    lengths[0], lengths[-1] = 0, 40
+    d = iva.workloads.decode_batch(lengths, 4, 2, 64, torch.float16, seed=batch % 97,
+                                   device=dev, scale=0.125)
+    lay = d["layout"]
+    bt, ctx = lay.block_tables.to(dev), lay.context_lens.to(dev)
+    pick = torch.cat([torch.arange(16), torch.arange(batch - 16, batch),
+                      torch.randperm(batch - 32, generator=gen)[:128] + 16])
+    bt_np, ctx_np = lay.block_tables[pick].numpy(), lay.context_lens[pick].numpy()
+    out = iva.paged_decode_attention(d["q"], d["k_pool"], d["v_pool"], bt, ctx)
+    ref = orc.decode_attention(to_np(d["q"][pick.to(dev)]), to_np(d["k_pool"]), to_np(d["v_pool"]),
+                               bt_np, ctx_np)
+    assert_close(out[pick.to(dev)], ref, torch.float16, what=f"batch {batch}")
+    # the fused step: the new token at position L-1 of every non-empty sequence
+    k_new = (torch.randn(batch, 2, 64, generator=gen) * 0.125).half().to(dev)
+    v_new = (torch.randn(batch, 2, 64, generator=gen) * 0.125).half().to(dev)
+    kp_f, vp_f = d["k_pool"].clone(), d["v_pool"].clone()
+    fused = iva.paged_decode_append_attention(d["q"], k_new, v_new, kp_f, vp_f, bt, ctx)
+    slots = torch.tensor([int(lay.slots(b, torch.tensor([n - 1]))[0]) if n > 0 else -1
+                          for b, n in enumerate(lengths)], dtype=torch.int32)
+    kp_a, vp_a = d["k_pool"].clone(), d["v_pool"].clone()
+    iva.kv_append(k_new, v_new, kp_a, vp_a, slots.to(dev))
+    assert torch.equal(kp_f.view(torch.int16), kp_a.view(torch.int16))
+    assert torch.equal(vp_f.view(torch.int16), vp_a.view(torch.int16))
+    ref = orc.decode_attention(to_np(d["q"][pick.to(dev)]), to_np(kp_a), to_np(vp_a), bt_np, ctx_np)
+    assert_close(fused[pick.to(dev)], ref, torch.float16, what=f"fused batch {batch}")
+
+
 def test_c4_long_context(iva, dev):
     """C4: B 4 at 32k..128k tokens, window 4096 + 4 sinks, bf16, K/V ~ N(0,1)."""
     d = iva.workloads.c4_long_context(seed=0, device=dev)
