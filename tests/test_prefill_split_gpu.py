@@ -184,6 +184,50 @@ def test_split_plan_invariants_and_garbage_workspace(iva, dev):
     assert torch.equal(out1, out2)
 
 
+def _check_plan(ws, batch, hkv, blocks_x, n_wg):
+    """Queue counters: every ticket taken once plus one failing grab per workgroup;
+    arrival counters: every split segment counted in once."""
+    ctl = ws[:256].view(torch.int32).cpu()
+    V = int(ctl[0])
+    for x in range(8):
+        units = (V - x + 7) // 8 if V > x else 0
+        assert int(ctl[32 + 4 * x]) == units * blocks_x + n_wg // 8, x
+    up = lambda v: (v + 255) & ~255
+    arrive = up(up(up(256) + (batch * hkv + SLOTS) * 8) + batch * blocks_x * 8)
+    counts = ws[arrive:arrive + 4 * SLOTS].view(torch.int32).cpu()
+    assert int(counts.sum()) == int(ctl[3]) > 0
+    return ctl
+
+
+@pytest.mark.parametrize("batch", [300, 2048])
+def test_split_large_batches(iva, dev, batch):
+    """Batches past the plan's ranking (more than 256 sequences keep their order) and,
+    at 2048 sequences with a 300-token chunk (five row blocks per unit), past the
+    row-block table the plan keeps in LDS (more than 8192 blocks: kept in the
+    workspace).  Short chunks on short contexts, with two long contexts that split;
+    against the fp64 oracle, plan invariants read back.  Batch 2049 is refused."""
+    gen = torch.Generator().manual_seed(batch)
+    lengths = torch.randint(8, 120, (batch,), generator=gen).tolist()
+    chunks = [int(torch.randint(1, min(n, 4) + 1, (1,), generator=gen)) for n in lengths]
+    lengths[7], chunks[7] = 5000, 64
+    lengths[batch - 50], chunks[batch - 50] = 3000, 300
+    hq, hkv, d = 8, 2, 64
+    c = make(iva, lengths, chunks, hq, hkv, d, torch.float16, seed=batch % 89)
+    max_q = max(chunks)
+    nbytes = iva.prefill_split_workspace_bytes(batch, hq, hkv, d, max_q, torch.float16)
+    ws = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=dev)
+    out = run(iva, dev, c, split=True, workspace=ws, max_query_len=max_q)
+    blocks_x = -(-max_q * (hq // hkv) // 256)
+    assert batch * blocks_x > 8192 or batch == 300
+    ctl = _check_plan(ws, batch, hkv, blocks_x, grid_wgs(dev))
+    assert int(ctl[1]) >= 2  # both long chunks split
+    assert_close(out, oracle(c), torch.float16, f"batch {batch}")
+    if batch == 2048:
+        c2 = make(iva, lengths + [40], chunks + [2], hq, hkv, d, torch.float16, seed=3)
+        with pytest.raises(iva._abi.IvakvError, match="2048"):
+            run(iva, dev, c2, split=True)
+
+
 def test_split_in_a_hip_graph(iva, dev):
     """The three launches captured in one HIP graph (the plan resets the queue
     counters on the device, no host read): every replay, with eager work and
