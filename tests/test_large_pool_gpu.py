@@ -260,3 +260,67 @@ def test_index_gather_scatter_past_2g_elements(iva, dev):
     assert same(out, kv)
     del kv, out
     torch.cuda.empty_cache()
+
+
+def _torch_rows(k_pool, v_pool, bt_row, length):
+    """[Hkv, L, D] fp32 K and V of one sequence by plain torch indexing of the pools."""
+    n = -(-length // BS)
+    pages = bt_row[:n].long()
+    hkv, d = k_pool.shape[1], k_pool.shape[2] * k_pool.shape[4]
+    k = k_pool[pages].permute(1, 0, 3, 2, 4).reshape(hkv, n * BS, d)[:, :length].float()
+    v = v_pool[pages].permute(1, 0, 3, 2).reshape(hkv, n * BS, d)[:, :length].float()
+    return k, v
+
+
+def _torch_attention(q, k, v, positions):
+    """fp32 causal attention of query rows q [R, Hq, D] at absolute positions over k, v
+    [Hkv, L, D] (all keys <= the row's position)."""
+    hq, hkv = q.shape[1], k.shape[0]
+    kk = k.repeat_interleave(hq // hkv, dim=0)  # [Hq, L, D]
+    vv = v.repeat_interleave(hq // hkv, dim=0)
+    s = torch.matmul(q.float().permute(1, 0, 2).contiguous(), kk.transpose(1, 2).contiguous())
+    s = s * q.shape[2] ** -0.5  # [Hq, R, L]
+    j = torch.arange(k.shape[1], device=q.device)
+    s = s.masked_fill(j[None, None, :] > positions[None, :, None], float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), vv).permute(1, 0, 2)  # [R, Hq, D]
+
+
+def test_million_token_context(iva, dev):
+    """One sequence of 2^20 positions (65,536 pages in one table row) beside a short one:
+    decode (stream and partitioned walks) and a 16-token chunk through the split prefill
+    against fp32 torch attention on the GPU, and decode with a window + sinks against the
+    fp64 oracle."""
+    lengths = [1 << 20, 33]
+    hkv, g, d = 2, 2, 64
+    dd = iva.workloads.decode_batch(lengths, hkv * g, hkv, d, torch.float16, seed=31,
+                                    device=dev, scale=d ** -0.5)
+    lay = dd["layout"]
+    bt, ctx = lay.block_tables.to(dev), lay.context_lens.to(dev)
+    refs = []
+    for b, n in enumerate(lengths):
+        k, v = _torch_rows(dd["k_pool"], dd["v_pool"], bt[b], n)
+        refs.append(_torch_attention(dd["q"][b:b + 1], k, v,
+                                     torch.tensor([n - 1], device=dev))[0])
+    ref = torch.stack(refs)
+    for kw in ({}, {"partition_pages": 256}):
+        out = iva.paged_decode_attention(dd["q"], dd["k_pool"], dd["v_pool"], bt, ctx, **kw)
+        err = float((out.float() - ref).abs().max())
+        assert err <= 2e-3, (kw, err)
+    out = iva.paged_decode_attention(dd["q"], dd["k_pool"], dd["v_pool"], bt, ctx, window=70000,
+                                     n_sink=5)
+    oref = orc.decode_attention(dd["q"].float().cpu().numpy(), dd["k_pool"].float().cpu().numpy(),
+                                dd["v_pool"].float().cpu().numpy(), lay.block_tables.numpy(),
+                                lay.context_lens.numpy(), window=70000, n_sink=5)
+    assert np.abs(out.float().cpu().numpy() - oref).max() <= 2e-3
+    qs = torch.tensor([0, 16, 32], dtype=torch.int32, device=dev)
+    qp = (torch.randn(32, hkv * g, d, generator=torch.Generator().manual_seed(32)) * 0.5)
+    qp = qp.half().to(dev)
+    out = iva.paged_prefill_attention(qp, dd["k_pool"], dd["v_pool"], bt, ctx, qs, split=True)
+    for b, n in enumerate(lengths):
+        k, v = _torch_rows(dd["k_pool"], dd["v_pool"], bt[b], n)
+        pref = _torch_attention(qp[16 * b:16 * b + 16], k, v,
+                                torch.arange(n - 16, n, device=dev))
+        err = float((out[16 * b:16 * b + 16].float() - pref).abs().max())
+        assert err <= 2e-3, (b, err)
+    del dd
+    torch.cuda.empty_cache()
