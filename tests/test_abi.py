@@ -210,3 +210,38 @@ def test_prefill_and_copy_pages_argument_checks(iva):
     assert copy(eb=3) == a.E_ARG
     assert copy(ks=FAKE) == a.E_ARG               # both factor tensors or neither
     assert copy(n=0) == a.OK
+
+
+def test_error_messages_are_per_thread(iva):
+    """ivakv_last_error is thread-local: two threads failing different entry points at
+    the same time each read back their own message after every call."""
+    import threading
+
+    a = iva._abi
+    start = threading.Barrier(2)
+    bad = []
+
+    def fail_append():
+        start.wait()
+        for _ in range(3000):
+            st = call(iva, "ivakv_append", FAKE, FAKE, 512, 64, 512, 64, FAKE, FAKE, FAKE,
+                      3, 8, 64, 16, 4, 9, None)
+            msg = a.last_error()
+            if st != a.E_DTYPE or not msg.startswith("ivakv_append"):
+                bad.append(("append", st, msg))
+
+    def fail_gather():
+        start.wait()
+        for _ in range(3000):
+            st = call(iva, "ivakv_gather", FAKE, FAKE, FAKE, FAKE, 2, 4, 8, 63, 16, 8, 64,
+                      FAKE, FAKE, a.F16, None)
+            msg = a.last_error()
+            if st == a.OK or not msg.startswith("ivakv_gather"):
+                bad.append(("gather", st, msg))
+
+    threads = [threading.Thread(target=f) for f in (fail_append, fail_gather)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not bad, bad[:3]
