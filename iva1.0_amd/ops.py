@@ -116,6 +116,16 @@ def _i32(t: torch.Tensor, name: str) -> torch.Tensor:
     return t.contiguous()
 
 
+def _buffer(t: torch.Tensor, dev: torch.device, name: str) -> torch.Tensor:
+    """A caller-supplied output or workspace: on the op's device and contiguous (the
+    library writes its data pointer's whole extent)."""
+    if t.device != dev:
+        raise RuntimeError(f"{name} is on {t.device}; the op runs on {dev}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
 def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
               slot_mapping: torch.Tensor, k_scale: Optional[torch.Tensor] = None,
               v_scale: Optional[torch.Tensor] = None,
@@ -202,6 +212,7 @@ def kv_gather(k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Te
         for t in (k_out, v_out):
             if tuple(t.shape) != shape or t.dtype != k_pool.dtype or not t.is_contiguous():
                 raise ValueError(f"gather outputs must be contiguous {shape} {k_pool.dtype}")
+            _buffer(t, dev, "gather output")
     _abi.call("ivakv_gather", k_pool.data_ptr(), v_pool.data_ptr(), block_tables.data_ptr(),
               context_lens.data_ptr(), batch, max_blocks, hkv, head_dim, bs, num_pages, out_len,
               k_out.data_ptr(), v_out.data_ptr(), dtype_code(k_pool.dtype), _stream(dev))
@@ -312,6 +323,7 @@ def _decode(entry: str, q, k_pool, v_pool, block_tables, context_lens, scale, wi
         out = torch.empty_like(q)
     elif tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous tensor shaped and typed like q")
+    _buffer(out, dev, "out")
     nbytes = decode_workspace_bytes(batch, hq, hkv, head_dim, bs, max_blocks, window, n_sink,
                                     partition_pages)
     if workspace is None:
@@ -319,6 +331,7 @@ def _decode(entry: str, q, k_pool, v_pool, block_tables, context_lens, scale, wi
     elif workspace.numel() * workspace.element_size() < nbytes:
         raise ValueError(f"workspace has {workspace.numel() * workspace.element_size()} bytes, "
                          f"{nbytes} needed")
+    _buffer(workspace, dev, "workspace")
     if scales is not None:
         _abi.call(entry, q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
                   scales[0].data_ptr(), scales[1].data_ptr(), block_tables.data_ptr(),
@@ -431,12 +444,14 @@ def paged_decode_append_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: t
         out = torch.empty_like(q)
     elif tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous tensor shaped and typed like q")
+    _buffer(out, dev, "out")
     nbytes = decode_workspace_bytes(batch, hq, hkv, head_dim, bs, max_blocks, window, n_sink)
     if workspace is None:
         workspace = _workspace(dev, nbytes)
     elif workspace.numel() * workspace.element_size() < nbytes:
         raise ValueError(f"workspace has {workspace.numel() * workspace.element_size()} bytes, "
                          f"{nbytes} needed")
+    _buffer(workspace, dev, "workspace")
     if fp8:
         _abi.call("ivakv_decode_append_attn_fp8", q.data_ptr(), k_new.data_ptr(),
                   v_new.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), scales[0].data_ptr(),
@@ -501,8 +516,9 @@ def _gather_fp8(k_pool, v_pool, block_tables, context_lens, out_len, out, k_scal
     else:
         k_out, v_out = out
         for t in (k_out, v_out):
-            if tuple(t.shape) != shape or not t.is_contiguous():
-                raise ValueError(f"gather outputs must be contiguous {shape}")
+            if tuple(t.shape) != shape or not t.is_contiguous() or t.dtype != k_out.dtype:
+                raise ValueError(f"gather outputs must be contiguous {shape}, one dtype")
+            _buffer(t, dev, "gather output")
     _abi.call("ivakv_gather_fp8", k_pool.data_ptr(), v_pool.data_ptr(), k_scale.data_ptr(),
               v_scale.data_ptr(), block_tables.data_ptr(), context_lens.data_ptr(), batch,
               max_blocks, hkv, head_dim, bs, num_pages, out_len, k_out.data_ptr(),
@@ -584,6 +600,7 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
         out = torch.empty_like(q)
     elif tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous tensor shaped and typed like q")
+    _buffer(out, dev, "out")
     max_blocks = block_tables.shape[1]
     if split is None:
         split = prefill_split_default(batch, hq, hkv, q.shape[0], int(max_query_len), max_blocks,
@@ -596,6 +613,7 @@ def paged_prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
         elif workspace.numel() * workspace.element_size() < nbytes:
             raise ValueError(f"workspace has {workspace.numel() * workspace.element_size()} "
                              f"bytes, {nbytes} needed")
+        _buffer(workspace, dev, "workspace")
         ws = (workspace.data_ptr(), workspace.numel() * workspace.element_size())
         if fp8:
             _abi.call("ivakv_prefill_attn_split_fp8", q.data_ptr(), k_pool.data_ptr(),

@@ -264,6 +264,48 @@ def test_c2_fused_step_full_size(iva, dev):
     print(f"C2 fused step: max abs err vs fp64 oracle {err:.2e} over all 32 sequences")
 
 
+def test_caller_buffers_must_be_on_the_device(iva, dev):
+    """Outputs and workspaces the caller passes in are refused before any launch when
+    they are on the CPU or not contiguous (the library writes through their pointers):
+    decode, the fused step, prefill (both paths) and gather."""
+    d = iva.workloads.decode_batch([40, 7], 8, 2, 64, torch.float16, seed=3, device=dev)
+    lay = d["layout"]
+    bt, ctx = lay.block_tables.to(dev), lay.context_lens.to(dev)
+    args = (d["q"], d["k_pool"], d["v_pool"], bt, ctx)
+    nbytes = iva.decode_workspace_bytes(2, 8, 2, 64, 16, bt.shape[1])
+    cpu_out = torch.empty_like(d["q"], device="cpu")
+    cpu_ws = torch.empty(nbytes, dtype=torch.uint8)
+    strided_ws = torch.empty(2 * nbytes, dtype=torch.uint8, device=dev)[::2]
+    with pytest.raises(RuntimeError, match="out is on cpu"):
+        iva.paged_decode_attention(*args, out=cpu_out)
+    with pytest.raises(RuntimeError, match="workspace is on cpu"):
+        iva.paged_decode_attention(*args, workspace=cpu_ws)
+    with pytest.raises(ValueError, match="workspace must be contiguous"):
+        iva.paged_decode_attention(*args, workspace=strided_ws)
+    k1 = torch.zeros(2, 2, 64, dtype=torch.float16, device=dev)
+    with pytest.raises(RuntimeError, match="out is on cpu"):
+        iva.paged_decode_append_attention(d["q"], k1, k1, d["k_pool"], d["v_pool"], bt, ctx,
+                                          out=cpu_out)
+    with pytest.raises(RuntimeError, match="workspace is on cpu"):
+        iva.paged_decode_append_attention(d["q"], k1, k1, d["k_pool"], d["v_pool"], bt, ctx,
+                                          workspace=cpu_ws)
+    qs = torch.tensor([0, 8, 11], dtype=torch.int32, device=dev)
+    qp = torch.zeros(11, 8, 64, dtype=torch.float16, device=dev)
+    for split in (False, True):
+        with pytest.raises(RuntimeError, match="out is on cpu"):
+            iva.paged_prefill_attention(qp, d["k_pool"], d["v_pool"], bt, ctx, qs, split=split,
+                                        out=torch.empty_like(qp, device="cpu"))
+    pws = iva.prefill_split_workspace_bytes(2, 8, 2, 64, 8, torch.float16)
+    with pytest.raises(RuntimeError, match="workspace is on cpu"):
+        iva.paged_prefill_attention(qp, d["k_pool"], d["v_pool"], bt, ctx, qs, split=True,
+                                    workspace=torch.empty(pws, dtype=torch.uint8))
+    shape = (2, 2, 48, 64)
+    with pytest.raises(RuntimeError, match="gather output is on cpu"):
+        iva.kv_gather(d["k_pool"], d["v_pool"], bt, ctx, out_len=48,
+                      out=(torch.empty(shape, dtype=torch.float16),
+                           torch.empty(shape, dtype=torch.float16)))
+
+
 @pytest.mark.parametrize("batch", [8192, 8193, 9000])
 def test_batches_around_the_stream_walk_limit(iva, dev, batch):
     """Up to 8192 sequences take the stream walk, more the partitioned walk: the default
