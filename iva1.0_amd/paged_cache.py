@@ -192,6 +192,8 @@ class PagedKVPool:
         """Allocates pages so the sequence can hold ``length + n_tokens`` tokens.
         On exhaustion nothing is allocated and OutOfPagesError is raised."""
         s = self._seq(seq_id)
+        if int(n_tokens) < 0:
+            raise ValueError(f"n_tokens must be >= 0, got {n_tokens}")
         want = s.length + int(n_tokens)
         need = math.ceil(want / self.block_size) - len(s.pages)
         if need <= 0:
@@ -218,7 +220,8 @@ class PagedKVPool:
 
     def allocate(self, seq_id, n_tokens: int) -> np.ndarray:
         """Reserves pages for ``n_tokens`` new tokens, advances the length and returns
-        their slot ids (the ``slot_mapping`` of an append)."""
+        their slot ids (the ``slot_mapping`` of an append).  A negative count raises
+        ValueError, as exhaustion raises OutOfPagesError, with nothing changed."""
         s = self._seq(seq_id)
         self.reserve(seq_id, n_tokens)
         start = s.length

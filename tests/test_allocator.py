@@ -52,6 +52,20 @@ def test_exhaustion_is_atomic(iva):
     assert p.length("b") == 0 and p.pages("b") == [] and p.num_free_pages == 1
 
 
+def test_negative_counts_are_refused_and_zero_is_a_no_op(iva):
+    p, _ = pool(iva)
+    p.add_sequence("a")
+    p.allocate("a", 5)
+    before = (p.length("a"), p.pages("a"), p.num_free_pages)
+    with pytest.raises(ValueError, match="n_tokens"):
+        p.allocate("a", -1)
+    with pytest.raises(ValueError, match="n_tokens"):
+        p.reserve("a", -3)
+    assert (p.length("a"), p.pages("a"), p.num_free_pages) == before
+    assert len(p.allocate("a", 0)) == 0
+    assert (p.length("a"), p.pages("a"), p.num_free_pages) == before
+
+
 def test_block_table_width_limit(iva):
     p, pc = pool(iva, max_blocks_per_seq=2)
     p.add_sequence("a")

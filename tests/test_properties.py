@@ -68,7 +68,7 @@ class PoolMachine(RuleBasedStateMachine):
         self.live.add(sid)
         return sid
 
-    @rule(sid=seqs, n=st.integers(1, 70))
+    @rule(sid=seqs, n=st.integers(0, 70))
     def allocate(self, sid, n):
         if sid not in self.live:
             return
