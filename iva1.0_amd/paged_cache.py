@@ -495,10 +495,17 @@ class PagedKVCache:
     def update(self, new_k: torch.Tensor, new_v: torch.Tensor, start_pos: int) -> None:
         """KVCache.update (rope_kv.py:98-110) on the current layer: rows of ``new_k`` /
         ``new_v`` ([B, Hkv, T, D]) land at positions [start_pos, start_pos + T).
-        Positions past the current length extend every sequence (pages are allocated)."""
+        Positions past the current length extend every sequence (pages are allocated);
+        when the pool cannot hold the whole batch's growth, OutOfPagesError is raised
+        before any sequence grows."""
         t = new_k.shape[2]
         end = int(start_pos) + t
         layer = self._cursor
+        bs = self.pool.block_size
+        need = [max(0, -(-end // bs) - len(self.pool.pages(s))) for s in self.seq_ids]
+        if sum(need) > self.pool.num_free_pages:
+            raise OutOfPagesError(f"the batch needs {sum(need)} pages, "
+                                  f"{self.pool.num_free_pages} free")
         for s in self.seq_ids:
             grow = end - self.pool.length(s)
             if grow > 0:

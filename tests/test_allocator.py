@@ -276,3 +276,20 @@ def test_churn_driver_reaches_steady_state(iva):
     for ids in (churn.ids[:64], churn.ids[-64:]):   # the oldest and the newest sequences
         bt, _ = pool.tables(ids)
         assert (np.diff(bt[:, :4], axis=1) != 1).mean() > 0.3
+
+
+def test_cache_update_exhaustion_changes_nothing(iva):
+    """PagedKVCache.update on a pool that cannot hold the whole batch's growth raises
+    before any sequence grows (the check precedes every allocation and the append)."""
+    import torch
+    from importlib import import_module
+    pc = import_module("iva_amd.paged_cache")
+    cache = pc.PagedKVCache(3, 2, 16, 0, "cpu", torch.float32, num_layers=1, max_seq_len=64,
+                            num_pages=5)
+    before = [(cache.pool.length(s), cache.pool.pages(s)) for s in cache.seq_ids]
+    free = cache.pool.num_free_pages
+    rows = torch.zeros(3, 2, 32, 16)  # 32 tokens: 2 pages per sequence, 6 > 5
+    with pytest.raises(pc.OutOfPagesError, match="batch needs 6 pages"):
+        cache.update(rows, rows, 0)
+    assert [(cache.pool.length(s), cache.pool.pages(s)) for s in cache.seq_ids] == before
+    assert cache.pool.num_free_pages == free
