@@ -301,6 +301,21 @@ int ivakv_append_rope(const void* k_new, const void* v_new, int64_t k_tok_stride
                       const int32_t* positions, int n_tok, int num_kv_heads, int head_dim,
                       int block_size, int num_pages, float theta, int dtype, hipStream_t stream);
 /*
+ * ivakv_append_rope_fp8: ivakv_append_fp8 with every K row rotated at positions[t] first
+ * (the rotation of ivakv_append_rope, rounded once to the source dtype; V rows
+ * unchanged): codes and factors equal those of ivakv_rope on the K rows followed by
+ * ivakv_append_fp8, in one launch.  Source dtype f32 / f16 / bf16, head_dim in
+ * {64, 128, 256}, block_size 16; slots outside the pool are skipped.  Replaces: the k
+ * rotation of AttentionTorch.forward (attention.py:57-59) followed by the cache append
+ * (attention.py:61-63) on a kv_cache_dtype "fp8" cache (configs/quant_infer.yaml:22,52).
+ */
+int ivakv_append_rope_fp8(const void* k_new, const void* v_new, int64_t k_tok_stride,
+                          int64_t k_head_stride, int64_t v_tok_stride, int64_t v_head_stride,
+                          void* k_pool, void* v_pool, float* k_scale, float* v_scale,
+                          const int32_t* slot_mapping, const int32_t* positions, int n_tok,
+                          int num_kv_heads, int head_dim, int block_size, int num_pages,
+                          float theta, int dtype, hipStream_t stream);
+/*
  * ivakv_copy_pages: page moves src_pages[i] -> dst_pages[i] (int32, n_moves <= 65535) of a
  * pool pair of num_pages pages, K and V tiles of every kv head (elem_bytes 1, 2 or 4), plus
  * the FP8 scaling factors when k_scale / v_scale are given (both or neither).  The source

@@ -115,6 +115,13 @@ SIGNATURES = {
         c_int, c_int, c_int, c_int, c_int,     # n_tok, Hkv, D, block_size, num_pages
         c_float, c_int, c_void_p,              # theta, dtype, stream
     ]),
+    "ivakv_append_rope_fp8": (c_int, [
+        c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,  # k_new, v_new, strides
+        c_void_p, c_void_p, c_void_p, c_void_p,  # k_pool, v_pool, k_scale, v_scale
+        c_void_p, c_void_p,                    # slot_mapping, positions
+        c_int, c_int, c_int, c_int, c_int,     # n_tok, Hkv, D, block_size, num_pages
+        c_float, c_int, c_void_p,              # theta, dtype, stream
+    ]),
     "ivakv_copy_pages": (c_int, [
         c_void_p, c_void_p, c_void_p, c_void_p,  # k_pool, v_pool, k_scale, v_scale
         c_void_p, c_void_p, c_int, c_int,      # src_pages, dst_pages, n_moves, num_pages

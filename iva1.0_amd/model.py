@@ -361,7 +361,7 @@ class PagedAttention(_AttentionBase):
             pos = kv_cache.token_positions(s) if kv_cache is not None else \
                 torch.arange(s, dtype=torch.int32, device=x.device).repeat(b)
             rope_(q.reshape(b * s, self.n_heads, self.head_dim), pos, self.rope_theta)
-            if kv_cache is None or s == 1 or kv_cache.pool.fp8:
+            if kv_cache is None or s == 1:
                 rope_(k.reshape(b * s, self.n_kv_heads, self.head_dim), pos, self.rope_theta)
             else:
                 rope_pos = pos

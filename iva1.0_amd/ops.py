@@ -141,9 +141,8 @@ def kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor, v_
     ``torch.cat`` append of ``AttentionTorch.forward`` (src/core/attention.py:61-63).
     """
     if is_fp8(k_pool):
-        if rope_positions is not None:
-            raise NotImplementedError("RoPE fused into the append is built for 16/32-bit pools")
-        return _append_fp8(k_new, v_new, k_pool, v_pool, slot_mapping, k_scale, v_scale)
+        return _append_fp8(k_new, v_new, k_pool, v_pool, slot_mapping, k_scale, v_scale,
+                           rope_positions, rope_theta)
     dev = _require_gpu(k_new, v_new, k_pool, v_pool, slot_mapping)
     num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
     if k_new.dim() != 3 or tuple(k_new.shape) != tuple(v_new.shape):
@@ -470,7 +469,8 @@ def paged_decode_append_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: t
     return out
 
 
-def _append_fp8(k_new, v_new, k_pool, v_pool, slot_mapping, k_scale, v_scale) -> None:
+def _append_fp8(k_new, v_new, k_pool, v_pool, slot_mapping, k_scale, v_scale,
+                rope_positions=None, rope_theta=10000.0) -> None:
     dev = _require_gpu(k_new, v_new, k_pool, v_pool, slot_mapping)
     num_pages, hkv, head_dim, bs = pool_geometry(k_pool, v_pool)
     k_scale, v_scale = _scales(k_pool, k_scale, v_scale)
@@ -491,6 +491,16 @@ def _append_fp8(k_new, v_new, k_pool, v_pool, slot_mapping, k_scale, v_scale) ->
         k_new = k_new.contiguous()
     if v_new.stride(2) != 1:
         v_new = v_new.contiguous()
+    if rope_positions is not None:
+        pos = _i32(rope_positions, "rope_positions").reshape(-1)
+        if pos.numel() != n_tok or pos.device != dev:
+            raise ValueError(f"rope_positions must be {n_tok} int32 values on {dev}")
+        _abi.call("ivakv_append_rope_fp8", k_new.data_ptr(), v_new.data_ptr(),
+                  k_new.stride(0), k_new.stride(1), v_new.stride(0), v_new.stride(1),
+                  k_pool.data_ptr(), v_pool.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
+                  slot_mapping.data_ptr(), pos.data_ptr(), n_tok, hkv, head_dim, bs, num_pages,
+                  float(rope_theta), code, _stream(dev))
+        return
     _abi.call("ivakv_append_fp8", k_new.data_ptr(), v_new.data_ptr(),
               k_new.stride(0), k_new.stride(1), v_new.stride(0), v_new.stride(1),
               k_pool.data_ptr(), v_pool.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),

@@ -176,6 +176,25 @@ def test_rope_in_attention_paged_vs_torch(M, dev):
     assert torch.equal(a, b)
 
 
+def test_fp8_cache_with_rope_in_attention(M, dev):
+    """kv_cache_dtype="fp8" with rope_in_attention=True: prefill chunks take the fused FP8
+    RoPE append (ivakv_append_rope_fp8), decode steps rotate K before the fused FP8 step.
+    Logits stay close to the bf16-cache model with the same RoPE (quantized pages: a
+    closeness check); graph decode == eager."""
+    _, p16 = twin_models(M, torch.bfloat16, dev, rope_in_attention=True)
+    _, p8 = twin_models(M, torch.bfloat16, dev, rope_in_attention=True, kv_cache_dtype="fp8")
+    p8.load_state_dict(p16.state_dict())
+    ids = torch.randint(0, 512, (3, 40 + 10), device=dev)
+    with torch.no_grad():
+        l16, _ = run_steps(p16, ids, 40, dev)
+        l8, cache = run_steps(p8, ids, 40, dev)
+        assert cache.pool.fp8
+        assert (l16 - l8).abs().max().item() <= 0.25
+        a = p8.generate(ids[:, :24], max_length=8, do_sample=False, eos_token_id=None, use_graph=True)
+        b = p8.generate(ids[:, :24], max_length=8, do_sample=False, eos_token_id=None, use_graph=False)
+    assert torch.equal(a, b)
+
+
 def test_reference_config_and_generate_loop(M, dev):
     """The reference's own TransformerConfig fields (no n_kv_heads, sinks or RoPE flag)
     build the paged model; the reference's generate loop (transformer.py:257-320: a

@@ -204,3 +204,56 @@ def test_copy_pages_in_a_hip_graph(iva, dev):
         want_k[[0, 5, 9]] = k0[[3, 7, 1]]
         want_v[[0, 5, 9]] = v0[[3, 7, 1]]
         assert torch.equal(k, want_k) and torch.equal(v, want_v), f"replay {rep}"
+
+
+@pytest.mark.parametrize("src", [torch.float32, torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_append_rope_fp8_equals_rope_then_append(iva, dev, src, d):
+    """ivakv_append_rope_fp8 (kv_append with rope_positions on FP8 pools): codes and
+    factors byte-identical to ivakv_rope on the K rows followed by the FP8 append (every
+    byte of both pools and both factor tables compared), with a skipped slot and one
+    outside the pool; and the dequantized K within the FP8 quantization step of the
+    oracle's rotation of the source rows."""
+    FP8 = torch.float8_e4m3fn
+    lengths = [7, 33, 20]
+    hkv = 3
+    lay = iva.workloads.permuted_layout(lengths, 12, torch.Generator().manual_seed(4))
+    n = sum(lengths)
+    gen = torch.Generator().manual_seed(d)
+    k_new = torch.randn(n, hkv, d, generator=gen).to(src)
+    v_new = torch.randn(n, hkv, d, generator=gen).to(src)
+    slots = torch.cat([lay.slots(b, torch.arange(m)) for b, m in enumerate(lengths)])
+    slots[5], slots[40] = -1, 12 * 16 + 3
+    pos = torch.cat([torch.arange(m) + 5000 * b for b, m in enumerate(lengths)]).to(torch.int32)
+    ks, vs = iva.pool_shapes(12, hkv, d, 16, FP8)
+    pools = []
+    for fused in (True, False):
+        kp = torch.full(ks, 7, dtype=torch.uint8, device=dev).view(FP8)
+        vp = torch.full(vs, 7, dtype=torch.uint8, device=dev).view(FP8)
+        ksc = torch.full(iva.scale_shape(12, hkv), 2.0, device=dev)
+        vsc = torch.full(iva.scale_shape(12, hkv), 2.0, device=dev)
+        if fused:
+            iva.kv_append(k_new.to(dev), v_new.to(dev), kp, vp, slots.to(dev), k_scale=ksc,
+                          v_scale=vsc, rope_positions=pos.to(dev), rope_theta=10000.0)
+        else:
+            k_rot = iva.rope_(k_new.to(dev).clone(), pos.to(dev), theta=10000.0)
+            iva.kv_append(k_rot, v_new.to(dev), kp, vp, slots.to(dev), k_scale=ksc, v_scale=vsc)
+        pools.append([t.view(torch.uint8).cpu() if t.dtype == FP8 else t.cpu() for t in (kp, vp, ksc, vsc)])
+    for a, b in zip(*pools):
+        assert torch.equal(a, b)
+    # against the oracle: dequantized K rows within one e4m3 step (2^-3 relative) of the
+    # exact rotation, plus the source dtype's rounding of the rotated value
+    kd, vd = orc.dequantize_pools(pools[0][0].numpy(), pools[0][1].numpy(), pools[0][2].numpy(),
+                                  pools[0][3].numpy(), np.float64)
+    exact = orc.rope(k_new.float().numpy(), pos.numpy(), 10000.0)
+    got = orc.gather(kd, vd, lay.block_tables.numpy(), lay.context_lens.numpy(),
+                     out_len=max(lengths))[0]
+    t = 0
+    for b, m in enumerate(lengths):
+        for i in range(m):
+            if t + i in (5, 40):
+                continue
+            row, ref = got[b, :, i], exact[t + i]
+            amax = np.abs(ref).max(axis=-1, keepdims=True)
+            assert (np.abs(row - ref) <= 2.0 ** -4 * np.maximum(np.abs(ref), amax / 64) + 1e-6).all()
+        t += m
