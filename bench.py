@@ -945,7 +945,8 @@ def measure_decode(args, iva, torch, dev, lengths):
 def bench_ops(args, iva, torch, dev):
     """The hot path's data-movement kernels at realistic sizes (fp16, 8 kv heads, D 128),
     each as average time over back-to-back launches captured in one HIP graph: the append of
-    16 x 512-token chunks (8192 rows; plain and with RoPE fused), the gather of the C2
+    16 x 512-token chunks (8192 rows; plain and with RoPE fused, into 16-bit and into FP8
+    pages), the gather of the C2
     batch into contiguous K/V, the kv_ops index gather / scatter kernels on a [32, 8, 4096,
     128] cache, and the compaction's page moves (4096 pages).  Bytes are what each op must
     read and write; GB/s against the 8 TB/s HBM peak."""
@@ -992,6 +993,17 @@ def bench_ops(args, iva, torch, dev):
     timed("append", lambda: iva.kv_append(k_new, v_new, k_pool, v_pool, slots), app_bytes)
     timed("append_rope", lambda: iva.kv_append(k_new, v_new, k_pool, v_pool, slots,
                                                rope_positions=pos), app_bytes + 4 * n)
+    # the same rows into FP8 pages (read fp16 rows, write codes and one factor per row)
+    k8, v8 = (torch.zeros(shape, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+              for shape in iva.pool_shapes(pages, hkv, d, 16, torch.float8_e4m3fn))
+    ks8, vs8 = (torch.ones(iva.scale_shape(pages, hkv), device=dev) for _ in range(2))
+    app8_bytes = 2 * n * hkv * d * es + 2 * n * hkv * d + 2 * n * hkv * 4 + 4 * n
+    timed("append_fp8", lambda: iva.kv_append(k_new, v_new, k8, v8, slots, k_scale=ks8,
+                                              v_scale=vs8), app8_bytes)
+    timed("append_rope_fp8", lambda: iva.kv_append(k_new, v_new, k8, v8, slots, k_scale=ks8,
+                                                   v_scale=vs8, rope_positions=pos),
+          app8_bytes + 4 * n)
+    del k8, v8, ks8, vs8
     # compaction's page moves: 4096 pages (K and V tiles of all kv heads) to free ids
     src = torch.arange(0, 8192, 2, dtype=torch.int32, device=dev)
     dst = torch.arange(32768, 32768 + 4096, dtype=torch.int32, device=dev)

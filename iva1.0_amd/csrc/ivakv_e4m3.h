@@ -10,22 +10,23 @@ namespace ivakv {
 constexpr float kFp8Max = 448.f;
 
 // float -> e4m3fn code, round to nearest even, saturating at +-448 (NaN -> 0x7F).
+// Both ranges are computed and one is selected (no branch: a divergent branch per code
+// costs more than the arithmetic of the path not taken).
 __device__ inline uint32_t e4m3_encode(float x) {
   const uint32_t u = __float_as_uint(x);
   const uint32_t sign = (u >> 24) & 0x80u;
   const uint32_t au = u & 0x7fffffffu;
-  if (au > 0x7f800000u) return sign | 0x7Fu;  // NaN
   const float a = __uint_as_float(au);
-  uint32_t code;
-  if (a < 0.015625f) {  // below 2^-6: subnormal grid step 2^-9
-    code = (uint32_t)__builtin_rintf(a * 512.f);  // 0..8 (8 = smallest normal)
-  } else {
-    // keep 3 mantissa bits with round-to-nearest-even on the float's own bits,
-    // then rebias the exponent from 127 to 7
-    const uint32_t r = (au + 0x7FFFFu + ((au >> 20) & 1u)) >> 20;
-    code = r >= (127u - 7u) * 8u + 0x7Fu ? 0x7Eu : r - (127u - 7u) * 8u;
-  }
-  return sign | (code > 0x7Eu ? 0x7Eu : code);
+  // below 2^-6: subnormal grid step 2^-9, codes 0..8 (8 = smallest normal)
+  const uint32_t sub = (uint32_t)__builtin_rintf(fminf(a, 0.015625f) * 512.f);
+  // from 2^-6 on: keep 3 mantissa bits with round-to-nearest-even on the float's own
+  // bits, then rebias the exponent from 127 to 7 (saturating at 0x7E = 448)
+  const uint32_t r = (au + 0x7FFFFu + ((au >> 20) & 1u)) >> 20;
+  const uint32_t nrm = r >= (127u - 7u) * 8u + 0x7Fu ? 0x7Eu : r - (127u - 7u) * 8u;
+  uint32_t code = a < 0.015625f ? sub : nrm;
+  code = code > 0x7Eu ? 0x7Eu : code;
+  code = au > 0x7f800000u ? 0x7Fu : code;  // NaN
+  return sign | code;
 }
 
 // e4m3fn code -> float, exactly.

@@ -1,5 +1,5 @@
-// FP8 (OCP e4m3fn) KV pages on gfx950: append with per-(slot, kv head) scaling and
-// dequantizing gather.  Decode attention over these pages is ivakv_decode_attn_fp8
+// FP8 (OCP e4m3fn) KV pages on gfx950: append with per-(slot, kv head) scaling (plain,
+// or with K rotated by RoPE on the way in) and dequantizing gather.  Decode attention over these pages is ivakv_decode_attn_fp8
 // (ivakv_decode.hip).
 //
 // Pool layout (bytes): k_pool [page][Hkv][D/16][16][16] (16-byte chunks of 16 dims,
@@ -14,16 +14,10 @@
 // Conversions are written out in integer arithmetic (round to nearest even,
 // saturating at +-448), so the codes do not depend on a hardware rounding mode.
 #include "ivakv_e4m3.h"
+#include "ivakv_rope.h"
 
 namespace ivakv {
 namespace {
-
-constexpr int64_t kMaxGrid8 = 0x7fffffff;
-
-template <typename E>
-__device__ inline float to_f(E x) { return (float)x; }
-template <>
-__device__ inline float to_f<float>(float x) { return x; }
 
 struct Append8Args {
   const void* k_new;
@@ -34,52 +28,101 @@ struct Append8Args {
   float* k_scale;
   float* v_scale;
   const int32_t* slots;
-  int n_tok, Hkv, D;
+  const int32_t* pos;  // RoPE positions (the RoPE variant only)
+  int n_tok, Hkv;
   int64_t n_slots;
+  float theta;
 };
 
-// One wave per (token, kv head) row: lane l holds dims l*PER .. l*PER+PER-1 of K
-// and V, the wave reduces max|x|, and every lane stores its codes.
-template <typename E, int PER>
+// One workgroup per 16 consecutive tokens, its four waves taking kv heads w, w + 4, ...
+// Lane l of a wave holds token r = l % 16 and chunk group g = l / 16: the 16-dim chunks
+// g, g + 4, .. of that token's K and V rows (D / 64 chunks).  A row's max |x| is
+// reduced over the four lanes of its token; each lane then stores its K chunks as
+// whole 16-byte code chunks (16 tokens in consecutive slots of a page: 256 contiguous
+// bytes per chunk) and its V codes byte by byte (assembling 4-byte words across lanes
+// measured slower: the encoding, not the stores, bounds this kernel).
+// ROPE: K is rotated first (rotate_pair, rounded once to the source dtype, as
+// ivakv_rope rounds it), with cos / sin of the workgroup's 16 tokens x D/2 pairs
+// computed once into LDS and shared by every kv head.
+template <typename E, int D, bool ROPE>
 __global__ __launch_bounds__(256) void append8_kernel(Append8Args a) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= (int64_t)a.n_tok * a.Hkv) return;  // whole wave
-  const int h = (int)(row % a.Hkv);
-  const int64_t t = row / a.Hkv;
-  const int64_t slot = a.slots[t];
-  if (slot < 0 || slot >= a.n_slots) return;
-  const int64_t page = slot / 16;
-  const int off = (int)(slot - page * 16);
-  const int64_t tile = page * a.Hkv + h;
-  const E* ks = static_cast<const E*>(a.k_new) + t * a.kts + h * a.khs;
-  const E* vs = static_cast<const E*>(a.v_new) + t * a.vts + h * a.vhs;
-  float kx[PER], vx[PER];
-  float kmax = 0.f, vmax = 0.f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    kx[i] = to_f(ks[lane * PER + i]);
-    vx[i] = to_f(vs[lane * PER + i]);
-    kmax = fmaxf(kmax, fabsf(kx[i]));
-    vmax = fmaxf(vmax, fabsf(vx[i]));
+  constexpr int NC = D / 64;  // chunks per lane
+  constexpr int HALF = D / 2;
+  __shared__ float s_cs[ROPE ? 16 * HALF : 1], s_sn[ROPE ? 16 * HALF : 1];
+  __shared__ float s_freq[ROPE ? kFreqTable : 1];
+  const int64_t t0 = (int64_t)blockIdx.x * 16;
+  if constexpr (ROPE) {
+    fill_freqs(s_freq, HALF, D, a.theta);
+    for (int e = threadIdx.x; e < 16 * HALF; e += blockDim.x) {
+      const int64_t tt = t0 + e / HALF;
+      const int p = tt < a.n_tok ? a.pos[tt] : 0;
+      pair_angle(s_freq, p, e % HALF, D, a.theta, s_cs[e], s_sn[e]);
+    }
+    __syncthreads();
   }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t t = t0 + r;
+  const bool tok = t < a.n_tok;
+  const int64_t slot = tok ? a.slots[t] : -1;
+  const bool ok = slot >= 0 && slot < a.n_slots;  // the same for the four lanes of a token
+  const int64_t page = ok ? slot / 16 : 0;
+  const int off = ok ? (int)(slot - page * 16) : 0;
+  const int64_t tc = tok ? t : t0;  // rows past the batch read the group's first row
+  for (int h = wave; h < a.Hkv; h += 4) {
+    const E* ks = static_cast<const E*>(a.k_new) + tc * a.kts + h * a.khs;
+    const E* vs = static_cast<const E*>(a.v_new) + tc * a.vts + h * a.vhs;
+    E ke[NC][16];
+    float kx[NC][16], vx[NC][16];
+    float kmax = 0.f, vmax = 0.f;
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    kmax = fmaxf(kmax, __shfl_xor(kmax, o));
-    vmax = fmaxf(vmax, __shfl_xor(vmax, o));
-  }
-  const float ksf = row_sf(kmax), vsf = row_sf(vmax);
-  uint8_t* kp = a.k_pool + tile * (int64_t)a.D * 16;
-  uint8_t* vp = a.v_pool + tile * (int64_t)a.D * 16;
+    for (int j = 0; j < NC; ++j) {
+      const int c = g + 4 * j;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int d = lane * PER + i;
-    kp[((d >> 4) * 16 + off) * 16 + (d & 15)] = (uint8_t)e4m3_encode(kx[i] * ksf);
-    vp[fp8_v_offset(d, off, a.D)] = (uint8_t)e4m3_encode(vx[i] * vsf);
-  }
-  if (lane == 0) {
-    a.k_scale[tile * 16 + off] = ksf;
-    a.v_scale[tile * 16 + off] = vsf;
+      for (int i = 0; i < 16; ++i) {
+        ke[j][i] = ks[16 * c + i];
+        vx[j][i] = rope_ld(vs[16 * c + i]);
+      }
+      if constexpr (ROPE) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int e = r * HALF + 8 * c + q;
+          rotate_pair(ke[j][2 * q], ke[j][2 * q + 1], s_cs[e], s_sn[e]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        kx[j][i] = rope_ld(ke[j][i]);
+        kmax = fmaxf(kmax, fabsf(kx[j][i]));
+        vmax = fmaxf(vmax, fabsf(vx[j][i]));
+      }
+    }
+    kmax = fmaxf(kmax, __shfl_xor(kmax, 16));
+    kmax = fmaxf(kmax, __shfl_xor(kmax, 32));
+    vmax = fmaxf(vmax, __shfl_xor(vmax, 16));
+    vmax = fmaxf(vmax, __shfl_xor(vmax, 32));
+    if (!ok) continue;
+    const float ksf = row_sf(kmax), vsf = row_sf(vmax);
+    const int64_t tile = page * a.Hkv + h;
+    uint8_t* kp = a.k_pool + tile * (int64_t)D * 16;
+    uint8_t* vp = a.v_pool + tile * (int64_t)D * 16;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = g + 4 * j;
+      uint32_t w[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        w[u] = e4m3_encode(kx[j][4 * u] * ksf) | (e4m3_encode(kx[j][4 * u + 1] * ksf) << 8) |
+               (e4m3_encode(kx[j][4 * u + 2] * ksf) << 16) | (e4m3_encode(kx[j][4 * u + 3] * ksf) << 24);
+      *reinterpret_cast<uint4*>(kp + ((int64_t)c * 16 + off) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        vp[fp8_v_offset(16 * c + i, off, D)] = (uint8_t)e4m3_encode(vx[j][i] * vsf);
+    }
+    if (g == 0) {
+      a.k_scale[tile * 16 + off] = ksf;
+      a.v_scale[tile * 16 + off] = vsf;
+    }
   }
 }
 
@@ -128,13 +171,15 @@ __global__ __launch_bounds__(256) void gather8_kernel(Gather8Args a) {
 
 using namespace ivakv;
 
-extern "C" int ivakv_append_fp8(const void* k_new, const void* v_new, int64_t k_tok_stride,
-                                int64_t k_head_stride, int64_t v_tok_stride,
-                                int64_t v_head_stride, void* k_pool, void* v_pool, float* k_scale,
-                                float* v_scale, const int32_t* slot_mapping, int n_tok,
-                                int num_kv_heads, int head_dim, int block_size, int num_pages,
-                                int dtype, hipStream_t stream) {
-  static const char* name = "ivakv_append_fp8";
+namespace {
+
+// Shared checks and launch of the two FP8 appends (positions == nullptr: no RoPE).
+int append8_entry(const char* name, const void* k_new, const void* v_new, int64_t k_tok_stride,
+                  int64_t k_head_stride, int64_t v_tok_stride, int64_t v_head_stride,
+                  void* k_pool, void* v_pool, float* k_scale, float* v_scale,
+                  const int32_t* slot_mapping, const int32_t* positions, bool rope, int n_tok,
+                  int num_kv_heads, int head_dim, int block_size, int num_pages, float theta,
+                  int dtype, hipStream_t stream) {
   if (dtype_size(dtype) == 0) return fail(IVAKV_E_DTYPE, "%s: unknown dtype code %d", name, dtype);
   if (n_tok < 0 || num_kv_heads <= 0 || num_pages < 0)
     return fail(IVAKV_E_ARG, "%s: bad sizes n_tok=%d Hkv=%d num_pages=%d", name, n_tok,
@@ -142,30 +187,64 @@ extern "C" int ivakv_append_fp8(const void* k_new, const void* v_new, int64_t k_
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(IVAKV_E_SHAPE, "%s: head_dim %d not in {64,128,256}", name, head_dim);
   if (block_size != 16) return fail(IVAKV_E_SHAPE, "%s: block_size %d != 16", name, block_size);
+  if (rope && !(theta > 0.f)) return fail(IVAKV_E_ARG, "%s: theta must be positive", name);
   if (n_tok == 0) return IVAKV_OK;
-  if (!k_new || !v_new || !k_pool || !v_pool || !k_scale || !v_scale || !slot_mapping)
+  if (!k_new || !v_new || !k_pool || !v_pool || !k_scale || !v_scale || !slot_mapping ||
+      (rope && !positions))
     return fail(IVAKV_E_ARG, "%s: null pointer argument", name);
   if (k_tok_stride < 0 || k_head_stride < 0 || v_tok_stride < 0 || v_head_stride < 0)
     return fail(IVAKV_E_ARG, "%s: negative stride", name);
   Append8Args a{k_new, v_new, k_tok_stride, k_head_stride, v_tok_stride, v_head_stride,
                 static_cast<uint8_t*>(k_pool), static_cast<uint8_t*>(v_pool), k_scale, v_scale,
-                slot_mapping, n_tok, num_kv_heads, head_dim, (int64_t)num_pages * 16};
-  const int64_t blocks = ((int64_t)n_tok * num_kv_heads + 3) / 4;
-  if (blocks > kMaxGrid8) return fail(IVAKV_E_SHAPE, "%s: too many rows", name);
-  const dim3 grid((unsigned)blocks);
-#define IVAKV_APPEND8(E)                                                            \
+                slot_mapping, positions, n_tok, num_kv_heads, (int64_t)num_pages * 16, theta};
+  const dim3 grid((unsigned)cdiv(n_tok, 16));
+#define IVAKV_APPEND8(E, R)                                                         \
   switch (head_dim) {                                                               \
-    case 64: append8_kernel<E, 1><<<grid, 256, 0, stream>>>(a); break;              \
-    case 128: append8_kernel<E, 2><<<grid, 256, 0, stream>>>(a); break;             \
-    default: append8_kernel<E, 4><<<grid, 256, 0, stream>>>(a); break;              \
+    case 64: append8_kernel<E, 64, R><<<grid, 256, 0, stream>>>(a); break;          \
+    case 128: append8_kernel<E, 128, R><<<grid, 256, 0, stream>>>(a); break;        \
+    default: append8_kernel<E, 256, R><<<grid, 256, 0, stream>>>(a); break;         \
   }
-  switch (dtype) {
-    case IVAKV_F16: IVAKV_APPEND8(_Float16); break;
-    case IVAKV_BF16: IVAKV_APPEND8(__bf16); break;
-    default: IVAKV_APPEND8(float); break;
+#define IVAKV_APPEND8_DT(R)                                                         \
+  switch (dtype) {                                                                  \
+    case IVAKV_F16: IVAKV_APPEND8(_Float16, R); break;                              \
+    case IVAKV_BF16: IVAKV_APPEND8(__bf16, R); break;                               \
+    default: IVAKV_APPEND8(float, R); break;                                        \
   }
+  if (rope) {
+    IVAKV_APPEND8_DT(true);
+  } else {
+    IVAKV_APPEND8_DT(false);
+  }
+#undef IVAKV_APPEND8_DT
 #undef IVAKV_APPEND8
   return launch_status(name);
+}
+
+}  // namespace
+
+extern "C" int ivakv_append_fp8(const void* k_new, const void* v_new, int64_t k_tok_stride,
+                                int64_t k_head_stride, int64_t v_tok_stride,
+                                int64_t v_head_stride, void* k_pool, void* v_pool, float* k_scale,
+                                float* v_scale, const int32_t* slot_mapping, int n_tok,
+                                int num_kv_heads, int head_dim, int block_size, int num_pages,
+                                int dtype, hipStream_t stream) {
+  return append8_entry("ivakv_append_fp8", k_new, v_new, k_tok_stride, k_head_stride,
+                       v_tok_stride, v_head_stride, k_pool, v_pool, k_scale, v_scale,
+                       slot_mapping, nullptr, false, n_tok, num_kv_heads, head_dim, block_size,
+                       num_pages, 1.f, dtype, stream);
+}
+
+extern "C" int ivakv_append_rope_fp8(const void* k_new, const void* v_new, int64_t k_tok_stride,
+                                     int64_t k_head_stride, int64_t v_tok_stride,
+                                     int64_t v_head_stride, void* k_pool, void* v_pool,
+                                     float* k_scale, float* v_scale, const int32_t* slot_mapping,
+                                     const int32_t* positions, int n_tok, int num_kv_heads,
+                                     int head_dim, int block_size, int num_pages, float theta,
+                                     int dtype, hipStream_t stream) {
+  return append8_entry("ivakv_append_rope_fp8", k_new, v_new, k_tok_stride, k_head_stride,
+                       v_tok_stride, v_head_stride, k_pool, v_pool, k_scale, v_scale,
+                       slot_mapping, positions, true, n_tok, num_kv_heads, head_dim, block_size,
+                       num_pages, theta, dtype, stream);
 }
 
 extern "C" int ivakv_gather_fp8(const void* k_pool, const void* v_pool, const float* k_scale,

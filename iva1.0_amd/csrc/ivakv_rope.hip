@@ -1,15 +1,8 @@
-// Rotary position embedding fused into the paged append (16/32-bit and FP8 pools),
-// rotation of query rows in place, and page moves for pool compaction, on gfx950.
-//
-// RoPE as the reference's RoPE module defines it (src/core/rope_kv.py:22-50): dims
-// (2i, 2i+1) of a head form a pair rotated by angle a = p * f_i at absolute position
-// p, with f_i = 1 / theta^(2i / D) (computed in double, stored as float, as the
-// reference's float32 buffer holds it) and a = float(p) * f_i in float:
-//   y[2i]   = x[2i] cos a - x[2i+1] sin a
-//   y[2i+1] = x[2i] sin a + x[2i+1] cos a
-// evaluated in fp32 and rounded once to the element type.
-#include "ivakv_internal.h"
-#include "ivakv_e4m3.h"
+// Rotary position embedding fused into the paged append, rotation of query rows in
+// place, and page moves for pool compaction, on gfx950.  The rotation itself (RoPE of
+// src/core/rope_kv.py:22-50) is in ivakv_rope.h; the FP8 pools' fused append is in
+// ivakv_fp8.hip.
+#include "ivakv_rope.h"
 
 namespace ivakv {
 namespace {
@@ -19,40 +12,6 @@ constexpr int64_t kMaxGridR = 0x7fffffff;
 struct alignas(16) Chunk16 {
   uint32_t w[4];
 };
-
-template <typename E>
-__device__ inline float ld(E x) { return (float)x; }
-
-template <typename E>
-__device__ inline void rotate_pair(E& x0, E& x1, float c, float s) {
-  const float a = ld(x0), b = ld(x1);
-  x0 = (E)(a * c - b * s);
-  x1 = (E)(a * s + b * c);
-}
-
-// f_i = 1 / theta^(2i / D), in double, stored as float.
-__device__ inline float inv_freq(int i, int D, float theta) {
-  return (float)(1.0 / pow((double)theta, (double)(2 * i) / (double)D));
-}
-
-// Each workgroup computes f_i once into LDS (head_dim up to 2 * kFreqTable) instead of
-// once per (token, head, pair): the double pow costs more than the row's memory traffic.
-// Pairs past the table compute f_i directly, to the same float.
-constexpr int kFreqTable = 1024;
-
-// Fills f[0, min(half, kFreqTable)); every thread of the workgroup must call it.
-__device__ inline void fill_freqs(float* f, int half, int D, float theta) {
-  for (int i = threadIdx.x; i < half && i < kFreqTable; i += blockDim.x) f[i] = inv_freq(i, D, theta);
-  __syncthreads();
-}
-
-// cos / sin of pair i at position p (accurate library sin / cos of the float angle).
-__device__ inline void pair_angle(const float* f, int p, int i, int D, float theta, float& c,
-                                  float& s) {
-  const float fi = i < kFreqTable ? f[i] : inv_freq(i, D, theta);
-  const float ang = (float)p * fi;
-  sincosf(ang, &s, &c);
-}
 
 // x [n_tok][H][D] with element strides (token, head), rotated in place at positions[t].
 // One thread per (token, head, pair).
@@ -198,94 +157,6 @@ __global__ __launch_bounds__(256) void copy_pages_kernel(Chunk16* k, Chunk16* v,
   }
 }
 
-// FP8 pools: the append of ivakv_append_fp8 with each K row rotated first.  One wave per
-// (token, kv head) row, lane l holding dims l*PER .. l*PER+PER-1 of K and V (PER = D/64;
-// at head_dim 64 the two dims of a pair sit in lanes l and l^1).  The rotation is
-// rotate_pair's, rounded once to the source dtype as ivakv_rope rounds it; the rotated
-// row is then scaled by sf = row_sf(max |x|) and encoded, so the codes and factors equal
-// those of ivakv_rope followed by ivakv_append_fp8.
-struct Append8RopeArgs {
-  const void* k_new;
-  const void* v_new;
-  int64_t kts, khs, vts, vhs;
-  uint8_t* k_pool;
-  uint8_t* v_pool;
-  float* k_scale;
-  float* v_scale;
-  const int32_t* slots;
-  const int32_t* pos;
-  int n_tok, Hkv, D;
-  int64_t n_slots;
-  float theta;
-};
-
-template <typename E, int PER>
-__global__ __launch_bounds__(256) void append8_rope_kernel(Append8RopeArgs a) {
-  __shared__ float s_freq[kFreqTable];
-  fill_freqs(s_freq, a.D / 2, a.D, a.theta);
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= (int64_t)a.n_tok * a.Hkv) return;  // whole wave
-  const int h = (int)(row % a.Hkv);
-  const int64_t t = row / a.Hkv;
-  const int64_t slot = a.slots[t];
-  if (slot < 0 || slot >= a.n_slots) return;  // whole wave
-  const int64_t page = slot / 16;
-  const int off = (int)(slot - page * 16);
-  const int64_t tile = page * a.Hkv + h;
-  const E* ks = static_cast<const E*>(a.k_new) + t * a.kts + h * a.khs;
-  const E* vs = static_cast<const E*>(a.v_new) + t * a.vts + h * a.vhs;
-  E ke[PER];
-  float kx[PER], vx[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    ke[i] = ks[lane * PER + i];
-    vx[i] = ld(vs[lane * PER + i]);
-  }
-  const int p = a.pos[t];
-  if constexpr (PER == 1) {
-    const float other = __shfl_xor(ld(ke[0]), 1);  // the pair's other dim (exact in float)
-    E x0 = (lane & 1) ? (E)other : ke[0];
-    E x1 = (lane & 1) ? ke[0] : (E)other;
-    float c, s;
-    pair_angle(s_freq, p, lane >> 1, a.D, a.theta, c, s);
-    rotate_pair(x0, x1, c, s);
-    ke[0] = (lane & 1) ? x1 : x0;
-  } else {
-#pragma unroll
-    for (int j = 0; j < PER / 2; ++j) {
-      float c, s;
-      pair_angle(s_freq, p, lane * (PER / 2) + j, a.D, a.theta, c, s);
-      rotate_pair(ke[2 * j], ke[2 * j + 1], c, s);
-    }
-  }
-  float kmax = 0.f, vmax = 0.f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    kx[i] = ld(ke[i]);
-    kmax = fmaxf(kmax, fabsf(kx[i]));
-    vmax = fmaxf(vmax, fabsf(vx[i]));
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    kmax = fmaxf(kmax, __shfl_xor(kmax, o));
-    vmax = fmaxf(vmax, __shfl_xor(vmax, o));
-  }
-  const float ksf = row_sf(kmax), vsf = row_sf(vmax);
-  uint8_t* kp = a.k_pool + tile * (int64_t)a.D * 16;
-  uint8_t* vp = a.v_pool + tile * (int64_t)a.D * 16;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int d = lane * PER + i;
-    kp[((d >> 4) * 16 + off) * 16 + (d & 15)] = (uint8_t)e4m3_encode(kx[i] * ksf);
-    vp[fp8_v_offset(d, off, a.D)] = (uint8_t)e4m3_encode(vx[i] * vsf);
-  }
-  if (lane == 0) {
-    a.k_scale[tile * 16 + off] = ksf;
-    a.v_scale[tile * 16 + off] = vsf;
-  }
-}
-
 }  // namespace
 }  // namespace ivakv
 
@@ -369,50 +240,6 @@ extern "C" int ivakv_append_rope(const void* k_new, const void* v_new, int64_t k
       else append_rope_kernel<float, false><<<g, 256, 0, stream>>>(a);
       break;
   }
-  return launch_status(name);
-}
-
-extern "C" int ivakv_append_rope_fp8(const void* k_new, const void* v_new, int64_t k_tok_stride,
-                                     int64_t k_head_stride, int64_t v_tok_stride,
-                                     int64_t v_head_stride, void* k_pool, void* v_pool,
-                                     float* k_scale, float* v_scale, const int32_t* slot_mapping,
-                                     const int32_t* positions, int n_tok, int num_kv_heads,
-                                     int head_dim, int block_size, int num_pages, float theta,
-                                     int dtype, hipStream_t stream) {
-  static const char* name = "ivakv_append_rope_fp8";
-  if (dtype_size(dtype) == 0) return fail(IVAKV_E_DTYPE, "%s: unknown dtype code %d", name, dtype);
-  if (n_tok < 0 || num_kv_heads <= 0 || num_pages < 0)
-    return fail(IVAKV_E_ARG, "%s: bad sizes n_tok=%d Hkv=%d num_pages=%d", name, n_tok,
-                num_kv_heads, num_pages);
-  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-    return fail(IVAKV_E_SHAPE, "%s: head_dim %d not in {64,128,256}", name, head_dim);
-  if (block_size != 16) return fail(IVAKV_E_SHAPE, "%s: block_size %d != 16", name, block_size);
-  if (!(theta > 0.f)) return fail(IVAKV_E_ARG, "%s: theta must be positive", name);
-  if (n_tok == 0) return IVAKV_OK;
-  if (!k_new || !v_new || !k_pool || !v_pool || !k_scale || !v_scale || !slot_mapping ||
-      !positions)
-    return fail(IVAKV_E_ARG, "%s: null pointer argument", name);
-  if (k_tok_stride < 0 || k_head_stride < 0 || v_tok_stride < 0 || v_head_stride < 0)
-    return fail(IVAKV_E_ARG, "%s: negative stride", name);
-  Append8RopeArgs a{k_new, v_new, k_tok_stride, k_head_stride, v_tok_stride, v_head_stride,
-                    static_cast<uint8_t*>(k_pool), static_cast<uint8_t*>(v_pool), k_scale,
-                    v_scale, slot_mapping, positions, n_tok, num_kv_heads, head_dim,
-                    (int64_t)num_pages * 16, theta};
-  const int64_t blocks = ((int64_t)n_tok * num_kv_heads + 3) / 4;
-  if (blocks > kMaxGridR) return fail(IVAKV_E_SHAPE, "%s: too many rows", name);
-  const dim3 grid((unsigned)blocks);
-#define IVAKV_APPEND8_ROPE(E)                                                       \
-  switch (head_dim) {                                                               \
-    case 64: append8_rope_kernel<E, 1><<<grid, 256, 0, stream>>>(a); break;         \
-    case 128: append8_rope_kernel<E, 2><<<grid, 256, 0, stream>>>(a); break;        \
-    default: append8_rope_kernel<E, 4><<<grid, 256, 0, stream>>>(a); break;         \
-  }
-  switch (dtype) {
-    case IVAKV_F16: IVAKV_APPEND8_ROPE(_Float16); break;
-    case IVAKV_BF16: IVAKV_APPEND8_ROPE(__bf16); break;
-    default: IVAKV_APPEND8_ROPE(float); break;
-  }
-#undef IVAKV_APPEND8_ROPE
   return launch_status(name);
 }
 
