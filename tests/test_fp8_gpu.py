@@ -249,3 +249,43 @@ def test_fp8_argument_errors(iva, dev):
     with pytest.raises(TypeError, match="float16 or bfloat16"):
         iva.paged_decode_append_attention(q, rows.float(), rows, *args[1:], k_scale=g["k_scale"],
                                           v_scale=g["v_scale"])
+
+
+def test_append_encodes_every_tie_and_boundary(iva, dev):
+    """The device encoder on chosen values: a row whose first element is 448 has scaling
+    factor 1, so its other elements are encoded as given.  Every e4m3 code's value, the
+    midpoints between neighbouring codes (round-to-nearest-even ties) and the floats one
+    ulp either side of them, both signs, subnormal range and the saturation edge up to
+    448, plus random floats over the whole range: codes identical to the oracle's (which
+    equals torch's float8_e4m3fn cast, tests/test_oracle.py)."""
+    vals = orc.e4m3_decode(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)  # 0 .. 448
+    mids = (vals[:-1] + vals[1:]) / 2
+    pts = np.concatenate([vals, mids]).astype(np.float32)
+    ulp = np.concatenate([np.nextafter(pts, np.float32(0)), np.nextafter(pts, np.float32(1e9))])
+    pts = np.concatenate([pts, ulp.astype(np.float32)])
+    pts = pts[(pts >= 0) & (pts <= 448)]
+    rng = np.random.default_rng(17)
+    rnd = (2.0 ** rng.uniform(-14, np.log2(448), 20000)).astype(np.float32)
+    x = np.concatenate([pts, -pts, rnd, -rnd, np.zeros(3, np.float32)])
+    d, hkv = 128, 1
+    per = d - 1
+    n = -(-x.size // per)
+    rows = np.zeros((n, hkv, d), np.float32)
+    rows[:, :, 0] = 448.0
+    flat = np.zeros(n * per, np.float32)
+    flat[:x.size] = x
+    rows[:, 0, 1:] = flat.reshape(n, per)
+    pages = -(-n // 16)
+    ks, vs = iva.pool_shapes(pages, hkv, d, 16, FP8)
+    kp = torch.zeros(ks, dtype=torch.uint8, device=dev).view(FP8)
+    vp = torch.zeros(vs, dtype=torch.uint8, device=dev).view(FP8)
+    ksc = torch.zeros(iva.scale_shape(pages, hkv), device=dev)
+    vsc = torch.zeros(iva.scale_shape(pages, hkv), device=dev)
+    src = torch.from_numpy(rows).to(dev)
+    iva.kv_append(src, src, kp, vp, torch.arange(n, dtype=torch.int32, device=dev),
+                  k_scale=ksc, v_scale=vsc)
+    assert bool((ksc.flatten()[:n] == 1).all()) and bool((vsc.flatten()[:n] == 1).all())
+    ok_k, ok_v, os_k, os_v = (orc.empty_pools(pages, hkv, d, 16, np.uint8, fill=0) +
+                              (orc.empty_scales(pages, hkv, 16), orc.empty_scales(pages, hkv, 16)))
+    orc.append_fp8(ok_k, ok_v, os_k, os_v, rows, rows, np.arange(n))
+    assert np.array_equal(u8(kp), ok_k) and np.array_equal(u8(vp), ok_v)
