@@ -218,8 +218,9 @@ int ivakv_decode_append_attn_noalloc(const void* q, const void* k_new, const voi
  *           the decode walk reads its V bytes as whole 16-byte loads
  *   k_scale, v_scale [num_pages][Hkv][BS] fp32
  * A row x of one (token, kv head) is stored as e4m3(x * sf), sf = 448 / max|x|
- * (1 for an all-zero row), clamped to [1e-8, 1e8], rounded to nearest even and
- * saturated at +-448; it reads back as code / sf.  BS = 16, head_dim in {64,128,256}.
+ * (1 for an all-zero row), clamped to [1e-8, 1e8] (a row holding a NaN or an infinity
+ * gets 1e-8, as the reference's rule evaluates), rounded to nearest even and saturated
+ * at +-448 (NaN code 0x7F); it reads back as code / sf.  BS = 16, head_dim in {64,128,256}.
  * Replaces: the reference's kv_cache_dtype "fp8" (configs/quant_infer.yaml:22,52),
  * with its scaling rule (src/quant/fp8_runtime.py:66-76) applied per row.
  *

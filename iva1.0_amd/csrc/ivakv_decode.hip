@@ -982,13 +982,13 @@ __global__ __launch_bounds__(256) void decode_fused_merge_kernel(DecodeArgs a) {
     float ka = 0.f, va = 0.f;
 #pragma unroll
     for (int j = 0; j < DL; ++j) {
-      ka = fmaxf(ka, fabsf((float)kn[lane + 64 * j]));
-      va = fmaxf(va, fabsf((float)vn[lane + 64 * j]));
+      ka = nan_max(ka, fabsf((float)kn[lane + 64 * j]));
+      va = nan_max(va, fabsf((float)vn[lane + 64 * j]));
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
-      ka = fmaxf(ka, __shfl_xor(ka, o));
-      va = fmaxf(va, __shfl_xor(va, o));
+      ka = nan_max(ka, __shfl_xor(ka, o));
+      va = nan_max(va, __shfl_xor(va, o));
     }
     sfk = row_sf(ka);
     sfv = row_sf(va);

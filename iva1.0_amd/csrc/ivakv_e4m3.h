@@ -39,11 +39,17 @@ __device__ inline float e4m3_decode(uint32_t b) {
   return (b & 0x80u) ? -v : v;
 }
 
-// Scaling factor of a row with max |x| = amax.
+// max(a, b) that keeps a NaN (fmaxf drops it): a row holding a NaN has a NaN max |x|.
+__device__ inline float nan_max(float a, float b) { return (a > b || a != a) ? a : b; }
+
+// Scaling factor of a row with max |x| = amax, the reference's rule
+// (src/quant/fp8_runtime.py:67-76): 1 for amax == 0, else 448 / amax clamped to
+// [1e-8, 1e8] as max(1e-8, min(sf, 1e8)) evaluates in Python, so a NaN amax gives 1e-8
+// (and an infinite one 448 / inf = 0, also 1e-8).
 __device__ inline float row_sf(float amax) {
-  if (!(amax > 0.f)) return 1.f;
+  if (amax == 0.f) return 1.f;
   const float sf = kFp8Max / amax;
-  return fminf(fmaxf(sf, 1e-8f), 1e8f);
+  return sf != sf ? 1e-8f : fminf(fmaxf(sf, 1e-8f), 1e8f);
 }
 
 }  // namespace ivakv

@@ -8,7 +8,8 @@
 // the decode walk reads its V bytes as whole 16-byte loads), k_scale / v_scale
 // [page][Hkv][16] fp32.  A row x of one (token, kv head) is
 // stored as codes e4m3(x * sf) with sf = 448 / max|x| (1 for an all-zero row),
-// clamped to [1e-8, 1e8] -- the reference's scaling rule
+// clamped to [1e-8, 1e8] (1e-8 for a row holding a NaN or an infinity) -- the
+// reference's scaling rule
 // (src/quant/fp8_runtime.py:66-76) applied per row -- and read back as code / sf.
 //
 // Conversions are written out in integer arithmetic (round to nearest even,
@@ -34,13 +35,27 @@ struct Append8Args {
   float theta;
 };
 
+// Codes of a, b, c, d packed into a word (byte i: the i-th value).  hw: the hardware
+// conversion (round to nearest even), for rows whose scaled values all lie below 464,
+// where it agrees with e4m3_encode (a GPU test checks every code, tie and neighbouring
+// float; values in (448, 464) round to 448 either way); rows beyond (an inf or NaN
+// element, or a max |x| so large that the clamped factor leaves it above 448) keep
+// e4m3_encode's saturation and NaN code.
+__device__ inline uint32_t encode4(float a, float b, float c, float d, bool hw) {
+  if (hw) {
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+  }
+  return e4m3_encode(a) | (e4m3_encode(b) << 8) | (e4m3_encode(c) << 16) | (e4m3_encode(d) << 24);
+}
+
 // One workgroup per 16 consecutive tokens, its four waves taking kv heads w, w + 4, ...
 // Lane l of a wave holds token r = l % 16 and chunk group g = l / 16: the 16-dim chunks
 // g, g + 4, .. of that token's K and V rows (D / 64 chunks).  A row's max |x| is
 // reduced over the four lanes of its token; each lane then stores its K chunks as
 // whole 16-byte code chunks (16 tokens in consecutive slots of a page: 256 contiguous
 // bytes per chunk) and its V codes byte by byte (assembling 4-byte words across lanes
-// measured slower: the encoding, not the stores, bounds this kernel).
+// measured slower); the codes come from the hardware conversion (encode4).
 // ROPE: K is rotated first (rotate_pair, rounded once to the source dtype, as
 // ivakv_rope rounds it), with cos / sin of the workgroup's 16 tokens x D/2 pairs
 // computed once into LDS and shared by every kv head.
@@ -74,7 +89,10 @@ __global__ __launch_bounds__(256) void append8_kernel(Append8Args a) {
     const E* vs = static_cast<const E*>(a.v_new) + tc * a.vts + h * a.vhs;
     E ke[NC][16];
     float kx[NC][16], vx[NC][16];
-    float kmax = 0.f, vmax = 0.f;
+    // max |x| drops NaN (fmaxf); the sum of |x| is non-finite exactly when the row holds
+    // an infinity or a NaN, or is so large that its factor clamps to 1e-8 anyway, so
+    // a non-finite sum stands for the reference rule's 1e-8 (row_sf of a NaN max)
+    float kmax = 0.f, vmax = 0.f, ksum = 0.f, vsum = 0.f;
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
       const int c = g + 4 * j;
@@ -95,14 +113,22 @@ __global__ __launch_bounds__(256) void append8_kernel(Append8Args a) {
         kx[j][i] = rope_ld(ke[j][i]);
         kmax = fmaxf(kmax, fabsf(kx[j][i]));
         vmax = fmaxf(vmax, fabsf(vx[j][i]));
+        ksum += fabsf(kx[j][i]);
+        vsum += fabsf(vx[j][i]);
       }
     }
     kmax = fmaxf(kmax, __shfl_xor(kmax, 16));
     kmax = fmaxf(kmax, __shfl_xor(kmax, 32));
     vmax = fmaxf(vmax, __shfl_xor(vmax, 16));
     vmax = fmaxf(vmax, __shfl_xor(vmax, 32));
+    ksum += __shfl_xor(ksum, 16);
+    ksum += __shfl_xor(ksum, 32);
+    vsum += __shfl_xor(vsum, 16);
+    vsum += __shfl_xor(vsum, 32);
+    const bool kfin = __builtin_isfinite(ksum), vfin = __builtin_isfinite(vsum);
     if (!ok) continue;
-    const float ksf = row_sf(kmax), vsf = row_sf(vmax);
+    const float ksf = kfin ? row_sf(kmax) : 1e-8f, vsf = vfin ? row_sf(vmax) : 1e-8f;
+    const bool khw = kfin && kmax * ksf < 464.f, vhw = vfin && vmax * vsf < 464.f;
     const int64_t tile = page * a.Hkv + h;
     uint8_t* kp = a.k_pool + tile * (int64_t)D * 16;
     uint8_t* vp = a.v_pool + tile * (int64_t)D * 16;
@@ -112,12 +138,17 @@ __global__ __launch_bounds__(256) void append8_kernel(Append8Args a) {
       uint32_t w[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u)
-        w[u] = e4m3_encode(kx[j][4 * u] * ksf) | (e4m3_encode(kx[j][4 * u + 1] * ksf) << 8) |
-               (e4m3_encode(kx[j][4 * u + 2] * ksf) << 16) | (e4m3_encode(kx[j][4 * u + 3] * ksf) << 24);
+        w[u] = encode4(kx[j][4 * u] * ksf, kx[j][4 * u + 1] * ksf, kx[j][4 * u + 2] * ksf,
+                       kx[j][4 * u + 3] * ksf, khw);
       *reinterpret_cast<uint4*>(kp + ((int64_t)c * 16 + off) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        vp[fp8_v_offset(16 * c + i, off, D)] = (uint8_t)e4m3_encode(vx[j][i] * vsf);
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t v4 = encode4(vx[j][4 * u] * vsf, vx[j][4 * u + 1] * vsf,
+                                    vx[j][4 * u + 2] * vsf, vx[j][4 * u + 3] * vsf, vhw);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          vp[fp8_v_offset(16 * c + 4 * u + e, off, D)] = (uint8_t)(v4 >> (8 * e));
+      }
     }
     if (g == 0) {
       a.k_scale[tile * 16 + off] = ksf;

@@ -316,11 +316,15 @@ def e4m3_decode(codes) -> np.ndarray:
 
 
 def row_scale(amax) -> np.ndarray:
-    """Scaling factor of rows with max |x| = amax (float32)."""
+    """Scaling factor of rows with max |x| = amax (float32), fp8_runtime.py:67-76:
+    1 for amax == 0, else 448 / amax clamped as ``max(1e-8, min(sf, 1e8))`` evaluates in
+    Python, where a NaN sf compares false both times and comes out as 1e-8."""
     amax = np.asarray(amax, dtype=np.float32)
-    with np.errstate(divide="ignore"):
-        sf = np.where(amax > 0, FP8_MAX / np.where(amax > 0, amax, np.float32(1)), np.float32(1))
-    return np.clip(sf, np.float32(1e-8), np.float32(1e8)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        sf = FP8_MAX / np.where(amax == 0, np.float32(1), amax)
+    sf = np.where(amax == 0, np.float32(1), sf)
+    sf = np.where(np.isnan(sf), np.float32(1e-8), np.clip(sf, np.float32(1e-8), np.float32(1e8)))
+    return sf.astype(np.float32)
 
 
 def quantize_rows(x: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:

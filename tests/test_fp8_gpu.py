@@ -289,3 +289,32 @@ def test_append_encodes_every_tie_and_boundary(iva, dev):
                               (orc.empty_scales(pages, hkv, 16), orc.empty_scales(pages, hkv, 16)))
     orc.append_fp8(ok_k, ok_v, os_k, os_v, rows, rows, np.arange(n))
     assert np.array_equal(u8(kp), ok_k) and np.array_equal(u8(vp), ok_v)
+
+
+def test_append_rows_beyond_the_scaled_range(iva, dev):
+    """Rows whose scaled values would leave +-448 take the integer encoder: an inf element
+    (factor 448 / inf clamped to 1e-8), a NaN element, and a max |x| of 1e12 (factor
+    clamped to 1e-8, so values up to 1e4 saturate at 448).  Codes and factors equal the
+    oracle's, rows of ordinary scale beside them included."""
+    d, hkv, n = 64, 2, 6
+    rng = np.random.default_rng(3)
+    rows = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    rows[0, 0, 5] = np.inf
+    rows[1, 1, 7] = -np.inf
+    rows[2, 0, 9] = np.nan
+    rows[3, 1, :] *= 1e12
+    rows[4, 0, :] *= 1e-9
+    ks, vs = iva.pool_shapes(1, hkv, d, 16, FP8)
+    kp = torch.zeros(ks, dtype=torch.uint8, device=dev).view(FP8)
+    vp = torch.zeros(vs, dtype=torch.uint8, device=dev).view(FP8)
+    ksc = torch.zeros(iva.scale_shape(1, hkv), device=dev)
+    vsc = torch.zeros(iva.scale_shape(1, hkv), device=dev)
+    src = torch.from_numpy(rows).to(dev)
+    iva.kv_append(src, src, kp, vp, torch.arange(n, dtype=torch.int32, device=dev),
+                  k_scale=ksc, v_scale=vsc)
+    ok_k, ok_v = orc.empty_pools(1, hkv, d, 16, np.uint8, fill=0)
+    os_k, os_v = orc.empty_scales(1, hkv, 16), orc.empty_scales(1, hkv, 16)
+    os_k[:], os_v[:] = 0, 0
+    orc.append_fp8(ok_k, ok_v, os_k, os_v, rows, rows, np.arange(n))
+    assert np.array_equal(u8(kp), ok_k) and np.array_equal(u8(vp), ok_v)
+    assert np.array_equal(ksc.cpu().numpy(), os_k) and np.array_equal(vsc.cpu().numpy(), os_v)

@@ -473,10 +473,19 @@ def test_e4m3_encode_matches_torch_rounding():
 
 
 def test_row_scale_is_the_reference_rule():
-    """fp8_runtime.py:66-76: sf = 448 / amax, 1 for amax == 0, clamped to [1e-8, 1e8]."""
-    amax = np.array([0.0, 1.0, 448.0, 3.5, 1e-12, 1e12], np.float32)
-    exp = [1.0, 448.0, 1.0, np.float32(448.0) / np.float32(3.5), 1e8, np.float32(1e-8)]
-    assert np.array_equal(orc.row_scale(amax), np.array(exp, np.float32))
+    """fp8_runtime.py:66-76: sf = 448 / amax, 1 for amax == 0, clamped to [1e-8, 1e8]
+    by max(1e-8, min(sf, 1e8)) -- evaluated here with Python's own min / max on every
+    amax, non-finite ones included (a NaN sf comes out as 1e-8)."""
+    amax = np.array([0.0, 1.0, 448.0, 3.5, 1e-12, 1e12, np.inf, np.nan], np.float32)
+
+    def reference(a):  # the rule's own steps, in Python floats
+        if a == 0:
+            return 1.0
+        sf = 448.0 / a if a != np.inf else 0.0
+        return max(1e-8, min(sf, 1e8))
+    exp = np.array([reference(float(a)) for a in amax], np.float32)
+    exp[3] = np.float32(448.0) / np.float32(3.5)  # the build divides in float32
+    assert np.array_equal(orc.row_scale(amax), exp)
 
 
 def test_fp8_rows_round_trip_and_layout():
