@@ -431,7 +431,9 @@ int ivakv_index_gather(const void* kv, int64_t s_b, int64_t s_h, int64_t s_s, in
 /*
  * Index scatter, in place: kv[b, h, indices[j], :] = values[b, h, j, :] with
  * values strides (v_b, v_h, v_s, v_d).  Indices outside [0, seq_len) are
- * skipped; duplicate indices leave one of the written rows (unspecified which).
+ * skipped.  With duplicate indices each 16-byte chunk of such a row comes from one of
+ * the duplicates (unspecified which, and not necessarily the same for every chunk), as
+ * torch's index_put leaves duplicates unspecified.
  * Replaces: kv_scatter_kernel + the scatter branch of KVOpsTriton
  * (src/kernels_t/kv_ops_triton.py:43-65,125-140); the functional (clone, then
  * scatter) form is kept by the Python op.

@@ -740,7 +740,8 @@ def kv_ops(kv_cache: torch.Tensor, indices: torch.Tensor, values: Optional[torch
     (src/kernels_t/kv_ops_triton.py:150-156):
       * ``"gather"``:  returns ``kv_cache[:, :, indices, :]`` as a new ``[B, H, N, D]`` tensor;
       * ``"scatter"``: returns a copy of ``kv_cache`` with ``[:, :, indices[j], :]`` replaced
-        by ``values[:, :, j, :]`` (the input is not modified);
+        by ``values[:, :, j, :]`` (the input is not modified; with duplicate indices each
+        16-byte chunk of such a row comes from one of the duplicates, unspecified which);
       * ``ValueError`` for a scatter without values or an unknown operation
         (kv_ops_triton.py:126-127,142-143).
     Differences, both deliberate: the gather output keeps the cache dtype (the reference
