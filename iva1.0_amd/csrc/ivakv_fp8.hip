@@ -49,7 +49,9 @@ __device__ inline uint32_t encode4(float a, float b, float c, float d, bool hw) 
   return e4m3_encode(a) | (e4m3_encode(b) << 8) | (e4m3_encode(c) << 16) | (e4m3_encode(d) << 24);
 }
 
-// One workgroup per 16 consecutive tokens, its four waves taking kv heads w, w + 4, ...
+// One workgroup per 16 consecutive tokens and group of kv heads (grid y): wave w of
+// workgroup (x, y) takes kv heads 4y + w, 4y + w + 4 gridDim.y, ... (a few tokens: one
+// head per wave, so the rows' round trips overlap; many: every head in one workgroup).
 // Lane l of a wave holds token r = l % 16 and chunk group g = l / 16: the 16-dim chunks
 // g, g + 4, .. of that token's K and V rows (D / 64 chunks).  A row's max |x| is
 // reduced over the four lanes of its token; each lane then stores its K chunks as
@@ -84,7 +86,7 @@ __global__ __launch_bounds__(256) void append8_kernel(Append8Args a) {
   const int64_t page = ok ? slot / 16 : 0;
   const int off = ok ? (int)(slot - page * 16) : 0;
   const int64_t tc = tok ? t : t0;  // rows past the batch read the group's first row
-  for (int h = wave; h < a.Hkv; h += 4) {
+  for (int h = 4 * (int)blockIdx.y + wave; h < a.Hkv; h += 4 * (int)gridDim.y) {
     const E* ks = static_cast<const E*>(a.k_new) + tc * a.kts + h * a.khs;
     const E* vs = static_cast<const E*>(a.v_new) + tc * a.vts + h * a.vhs;
     E ke[NC][16];
@@ -228,7 +230,9 @@ int append8_entry(const char* name, const void* k_new, const void* v_new, int64_
   Append8Args a{k_new, v_new, k_tok_stride, k_head_stride, v_tok_stride, v_head_stride,
                 static_cast<uint8_t*>(k_pool), static_cast<uint8_t*>(v_pool), k_scale, v_scale,
                 slot_mapping, positions, n_tok, num_kv_heads, (int64_t)num_pages * 16, theta};
-  const dim3 grid((unsigned)cdiv(n_tok, 16));
+  // Every kv head in one workgroup when the tokens alone fill the device (the RoPE
+  // angles are then computed once per token); else one kv head per wave.
+  const dim3 grid((unsigned)cdiv(n_tok, 16), n_tok >= 2048 ? 1u : (unsigned)cdiv(num_kv_heads, 4));
 #define IVAKV_APPEND8(E, R)                                                         \
   switch (head_dim) {                                                               \
     case 64: append8_kernel<E, 64, R><<<grid, 256, 0, stream>>>(a); break;          \
