@@ -86,6 +86,42 @@ def test_append_fp8_bit_exact(iva, dev, src, d):
     assert np.array_equal(g["v_scale"].cpu().numpy(), o["v_scale"])
 
 
+@pytest.mark.parametrize("src", [torch.float32, torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("rope", [False, True], ids=["plain", "rope"])
+def test_append_fp8_from_unaligned_strided_rows(iva, dev, src, rope):
+    """Source rows that start one element into a wider buffer (aligned to the element
+    only) and a kv head stride larger than head_dim: codes and factors equal those of the
+    same rows appended from a contiguous copy, plain or with RoPE fused (and, plain, the
+    oracle's)."""
+    d, hkv = 128, 3
+    c = fp8_case(iva, [17, 40, 3], hkv, d, src, seed=41, decades=0)
+    n = c["k_new"].shape[0]
+    wide_k = torch.zeros(n, hkv, d + 8, dtype=src, device=dev)
+    wide_v = torch.zeros(n, hkv, d + 8, dtype=src, device=dev)
+    k_src, v_src = wide_k[..., 1:d + 1], wide_v[..., 1:d + 1]
+    k_src.copy_(c["k_new"].to(dev))
+    v_src.copy_(c["v_new"].to(dev))
+    assert k_src.data_ptr() % 16 and v_src.data_ptr() % 16
+    pos = (torch.arange(n, dtype=torch.int32) * 37).to(dev)
+    kw = dict(rope_positions=pos) if rope else {}
+    out = []
+    for k_in, v_in in ((k_src, v_src), (c["k_new"].to(dev), c["v_new"].to(dev))):
+        g = {k: c[k].clone().to(dev) for k in ("k_pool", "v_pool", "k_scale", "v_scale")}
+        g["k_pool"], g["v_pool"] = g["k_pool"].view(FP8), g["v_pool"].view(FP8)
+        iva.kv_append(k_in, v_in, g["k_pool"], g["v_pool"], c["slots"].to(dev),
+                      k_scale=g["k_scale"], v_scale=g["v_scale"], **kw)
+        out.append([u8(g["k_pool"]), u8(g["v_pool"]), g["k_scale"].cpu().numpy(),
+                    g["v_scale"].cpu().numpy()])
+    for a, b in zip(*out):
+        assert np.array_equal(a, b)
+    if not rope:  # and both equal the oracle's append
+        o = dict(k_pool=c["k_pool"].numpy().copy(), v_pool=c["v_pool"].numpy().copy(),
+                 k_scale=c["k_scale"].numpy().copy(), v_scale=c["v_scale"].numpy().copy())
+        orc.append_fp8(o["k_pool"], o["v_pool"], o["k_scale"], o["v_scale"],
+                       c["k_new"].float().numpy(), c["v_new"].float().numpy(), c["slots"].numpy())
+        assert np.array_equal(out[0][0], o["k_pool"]) and np.array_equal(out[0][1], o["v_pool"])
+
+
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16], ids=str)
 def test_gather_fp8_exact(iva, dev, out_dtype):
     c = fp8_case(iva, [17, 40, 3, 0], 2, 128, torch.float16, seed=3)
