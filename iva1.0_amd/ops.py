@@ -237,8 +237,9 @@ def decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head
 # batch, when a walk may exceed SPLIT_MIN_KEYS keys (a chunk late in a long context:
 # 2-3.4x on one 512-token chunk at 8k-64k) or when the launch's work bound, query rows x
 # query heads x keys, reaches SPLIT_MIN_WORK (enough work that the persistent grid's
-# balance pays for the plan and merge launches: 16 x 512 rows at 2048 keys, 7 % faster
-# in fp16; shorter prefills are 2-11 us slower split).
+# longest-first order pays for the plan launch: the ragged prefill chunks of a
+# continuous-batching step take 25 % less time split, and 16 x 512 rows at 2048 keys take
+# the same time either way; shorter prefills are 2-11 us slower split).
 SPLIT_MIN_KEYS = 4096
 SPLIT_MIN_WORK = 1 << 28
 SPLIT_MAX_BATCH = 2048
