@@ -209,9 +209,9 @@ struct TileOps {
     const E* kp = static_cast<const E*>(a.k_pool) + tile;
     const E* vp = static_cast<const E*>(a.v_pool) + tile;
 #pragma unroll
-    for (int j = 0; j < KLD; ++j) t.k[j] = *reinterpret_cast<const Chunk16*>(kp + ((4 * j + lq) * kBS + ln) * X);
+    for (int j = 0; j < KLD; ++j) t.k[j] = load_once<Chunk16>(kp + ((4 * j + lq) * kBS + ln) * X);
 #pragma unroll
-    for (int m = 0; m < NB; ++m) t.v[m] = *reinterpret_cast<const VChunk*>(vp + (16 * m + ln) * kBS + 4 * lq);
+    for (int m = 0; m < NB; ++m) t.v[m] = load_once<VChunk>(vp + (16 * m + ln) * kBS + 4 * lq);
     __asm__ volatile("" ::: "memory");
   }
 
@@ -290,18 +290,18 @@ struct TileOps8 {
     const uint8_t* kp = static_cast<const uint8_t*>(a.k_pool) + tile * kTileBytes;
     const uint8_t* vp = static_cast<const uint8_t*>(a.v_pool) + tile * kTileBytes;
 #pragma unroll
-    for (int i = 0; i < KL; ++i) t.k[i] = *reinterpret_cast<const Chunk16*>(kp + ((4 * i + lq) * kBS + ln) * 16);
+    for (int i = 0; i < KL; ++i) t.k[i] = load_once<Chunk16>(kp + ((4 * i + lq) * kBS + ln) * 16);
     // Words m = 0 .. NB-1 (dims 16m + ln, keys 4lq .. 4lq+3) are consecutive in the
     // FP8 V tile order (fp8_v_offset): NB / 4 16-byte loads.
     const uint8_t* vl = vp + fp8_v_offset(ln, 4 * lq, D);
 #pragma unroll
     for (int m = 0; m < NB; m += 4) {
-      const Chunk16 c = *reinterpret_cast<const Chunk16*>(vl + 4 * m);
+      const Chunk16 c = load_once<Chunk16>(vl + 4 * m);
 #pragma unroll
       for (int j = 0; j < 4; ++j) t.v[m + j] = c.w[j];
     }
-    t.ks = *reinterpret_cast<const f32x4*>(a.k_scale + tile * kBS + 4 * lq);
-    t.vs = *reinterpret_cast<const f32x4*>(a.v_scale + tile * kBS + 4 * lq);
+    t.ks = load_once<f32x4>(a.k_scale + tile * kBS + 4 * lq);
+    t.vs = load_once<f32x4>(a.v_scale + tile * kBS + 4 * lq);
     __asm__ volatile("" ::: "memory");
   }
 
@@ -818,11 +818,13 @@ __global__ __launch_bounds__(kStreamThreads, Ops::kWGsPerCU) void decode_stream_
   };
 
   // 3. The ring: the load cursor runs kRing tiles ahead of the compute
-  //    cursor.  Past the wave's last tile it stays there and re-loads it (an L2
-  //    hit) into padding slots that score() masks.  Every slot also loads the
-  //    query rows of its tile's unit (an L2 hit after the first): a q load only
-  //    at unit changes would sit on a branch whose join makes the compiler
-  //    drain the ring before every tile.
+  //    cursor.  Past the wave's last tile it stays there and loads padding slots
+  //    that score() masks, from page 0 (as for an invalid page id): every wave
+  //    reads that same tile, an L2 hit, where re-reading the wave's own last tile
+  //    would miss (the streaming hint lets its lines go early).  Every slot also
+  //    loads the query rows of its tile's unit (an L2 hit after the first): a q
+  //    load only at unit changes would sit on a branch whose join makes the
+  //    compiler drain the ring before every tile.
   Cursor lc = c0r, cc = c0r;
   int issued = 0;
   typename Ops::QReg qb[kRing];
@@ -830,7 +832,8 @@ __global__ __launch_bounds__(kStreamThreads, Ops::kWGsPerCU) void decode_stream_
   int64_t pb[kRing];
   auto issue = [&](int s) {
     Ops::load_q(a, lc.b, lc.h, ln, lq, qb[s]);
-    pb[s] = phys_page(a, bt, lc.b, logical_page(lc.w, lc.v));
+    const int64_t p = phys_page(a, bt, lc.b, logical_page(lc.w, lc.v));
+    pb[s] = issued < count ? p : -1;
     Ops::load_tile(a, pb[s], lc.h, ln, lq, tb[s]);
     if (++issued < count) advance(lc);
   };

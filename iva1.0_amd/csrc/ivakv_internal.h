@@ -26,6 +26,43 @@ inline int dtype_size(int dtype) {
   }
 }
 
+// Non-temporal (streaming) load / store of a 4-, 8- or 16-byte value: the hint for
+// data a kernel touches once, which HBM-bound kernels here read and write faster with
+// it (measured per kernel; plain where a kernel's measurements favoured plain).
+typedef uint32_t nt_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t nt_u32x2 __attribute__((ext_vector_type(2)));
+template <class T>
+__device__ inline T load_nt(const void* p) {
+  static_assert(sizeof(T) == 16 || sizeof(T) == 8 || sizeof(T) == 4, "4, 8 or 16 bytes");
+  if constexpr (sizeof(T) == 16)
+    return __builtin_bit_cast(T, __builtin_nontemporal_load(static_cast<const nt_u32x4*>(p)));
+  else if constexpr (sizeof(T) == 8)
+    return __builtin_bit_cast(T, __builtin_nontemporal_load(static_cast<const nt_u32x2*>(p)));
+  else
+    return __builtin_bit_cast(T, __builtin_nontemporal_load(static_cast<const uint32_t*>(p)));
+}
+template <class T>
+__device__ inline void store_nt(void* p, const T& v) {
+  static_assert(sizeof(T) == 16 || sizeof(T) == 8 || sizeof(T) == 4, "4, 8 or 16 bytes");
+  if constexpr (sizeof(T) == 16)
+    __builtin_nontemporal_store(__builtin_bit_cast(nt_u32x4, v), static_cast<nt_u32x4*>(p));
+  else if constexpr (sizeof(T) == 8)
+    __builtin_nontemporal_store(__builtin_bit_cast(nt_u32x2, v), static_cast<nt_u32x2*>(p));
+  else
+    __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, v), static_cast<uint32_t*>(p));
+}
+// Load / store with the hint when NT.
+template <bool NT, class T>
+__device__ inline T ld(const void* p) {
+  if constexpr (NT) return load_nt<T>(p);
+  else return *static_cast<const T*>(p);
+}
+template <bool NT, class T>
+__device__ inline void st(void* p, const T& v) {
+  if constexpr (NT) store_nt<T>(p, v);
+  else *static_cast<T*>(p) = v;
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Ceil division for non-negative ints.

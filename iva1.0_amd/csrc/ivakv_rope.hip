@@ -36,7 +36,8 @@ __global__ __launch_bounds__(256) void rope_kernel(E* x, int64_t ts, int64_t hs,
 
 // Paged append with K rotated: one thread per (token, group of up to eight kv heads,
 // 16-byte chunk), the chunk's pairs rotated before the store.  Sources and pools that
-// allow it (16-byte aligned rows) move whole 16-byte chunks (VEC).
+// allow it (16-byte aligned rows) move whole 16-byte chunks (VEC), whose loads and K
+// stores carry the non-temporal hint (8192 rows: 15.6 µs against 19.2 µs without).
 struct AppendRopeArgs {
   const void* k_new;
   const void* v_new;
@@ -92,8 +93,8 @@ __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
     if (u < nh) {
       if constexpr (VEC) {  // 16-byte source chunks
         Row rk, rv;
-        rk.c = *reinterpret_cast<const Chunk16*>(kb + (h0 + u) * a.khs);
-        rv.c = *reinterpret_cast<const Chunk16*>(vb + (h0 + u) * a.vhs);
+        rk.c = ld<true, Chunk16>(kb + (h0 + u) * a.khs);
+        rv.c = ld<true, Chunk16>(vb + (h0 + u) * a.vhs);
 #pragma unroll
         for (int j = 0; j < X; ++j) {
           k[u][j] = rk.e[j];
@@ -124,7 +125,7 @@ __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
         Row rk;
 #pragma unroll
         for (int j = 0; j < X; ++j) rk.e[j] = k[u][j];
-        *reinterpret_cast<Chunk16*>(kd) = rk.c;
+        st<true, Chunk16>(kd, rk.c);
       } else {
 #pragma unroll
         for (int j = 0; j < X; ++j) kd[j] = k[u][j];
@@ -138,7 +139,8 @@ __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
 // Page moves: page src[i] -> dst[i] of every pool tensor (K and V tiles of all kv
 // heads, and the FP8 scaling factors when given).  Grid (chunk block, move), 16
 // bytes per thread.  A move whose source or destination id lies outside
-// [0, num_pages) is skipped.
+// [0, num_pages) is skipped.  Reads and writes carry the non-temporal hint (4096 moves:
+// 82 µs against 89 µs without).
 __global__ __launch_bounds__(256) void copy_pages_kernel(Chunk16* k, Chunk16* v, Chunk16* ks,
                                                          Chunk16* vs, const int32_t* src,
                                                          const int32_t* dst, int num_pages,
@@ -148,11 +150,11 @@ __global__ __launch_bounds__(256) void copy_pages_kernel(Chunk16* k, Chunk16* v,
   if (s < 0 || s >= num_pages || d < 0 || d >= num_pages) return;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < page_chunks;
        i += (int64_t)gridDim.x * blockDim.x) {
-    k[d * page_chunks + i] = k[s * page_chunks + i];
-    v[d * page_chunks + i] = v[s * page_chunks + i];
+    st<true, Chunk16>(k + d * page_chunks + i, ld<true, Chunk16>(k + s * page_chunks + i));
+    st<true, Chunk16>(v + d * page_chunks + i, ld<true, Chunk16>(v + s * page_chunks + i));
     if (ks && i < scale_chunks) {
-      ks[d * scale_chunks + i] = ks[s * scale_chunks + i];
-      vs[d * scale_chunks + i] = vs[s * scale_chunks + i];
+      st<true, Chunk16>(ks + d * scale_chunks + i, ld<true, Chunk16>(ks + s * scale_chunks + i));
+      st<true, Chunk16>(vs + d * scale_chunks + i, ld<true, Chunk16>(vs + s * scale_chunks + i));
     }
   }
 }
