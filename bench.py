@@ -117,10 +117,18 @@ def parse_args():
     return p.parse_args()
 
 
+def append_bytes(n_tok, hkv, d, esize):
+    """Bytes an append of n_tok rows moves: the K and V rows read (2 n Hkv D esize) and
+    written into their slots (as many), plus the int32 slot map.  The one formula of every
+    append figure here (the C2 step, the ops and C5 lines); like the gather's, it counts
+    reads and writes, twice the rows' size BASELINE.md's append term counts."""
+    return 4 * n_tok * hkv * d * esize + 4 * n_tok
+
+
 def algorithmic_bytes(lengths, hq, hkv, d, esize, bs=16):
     """Per-step algorithmic bytes: append of one row per sequence, decode attention."""
     b = len(lengths)
-    append = 2 * b * hkv * d * esize + 4 * b
+    append = append_bytes(b, hkv, d, esize)
     attn = (sum(2 * n * hkv * d * esize for n in lengths)   # K + V of attended rows
             + 2 * b * hq * d * esize                          # q in, out
             + sum(4 * math.ceil(n / bs) for n in lengths)     # block-table entries
@@ -564,19 +572,28 @@ def bench_c2fp8(args, iva, torch, dev):
                         "ivakv_decode_attn_fp8"}
 
 
+C4_RESIDENT_POOLS = 16
+
+
 def bench_c4(args, iva, torch, dev):
     """C4: long-context decode, bf16, B 4 at 32k/64k/96k/128k, GQA 32/8, D 128, window
-    4096 + 4 sinks (union); GB/s on attended bytes.  Attention (walk + merge) and the walk
-    alone, each as a HIP graph of back-to-back launches over rotated pools (1.34 GB
-    each), plus the same eagerly."""
+    4096 + 4 sinks (union); GB/s on attended bytes.  The pools are what a sliding-window
+    PagedKVCache keeps resident (the sink pages and the window's; the rest released after
+    each forward): 67.6 MB each, so 16 of them are rotated (1.08 GB) for the MALL not to
+    serve repeats.  Attention (walk + merge) and the walk alone, each as a HIP graph of
+    back-to-back launches over the rotated pools, plus the same eagerly."""
     wl = iva.workloads
     measure = _timer(torch, dev)
     sets = []
-    for i in range(args.pools):
-        d = wl.c4_long_context(seed=10 + i, device=dev)
+    n_pools = max(args.pools, C4_RESIDENT_POOLS)
+    for i in range(n_pools):
+        d = wl.c4_long_context(seed=10 + i, device=dev, resident_window=True)
         lay = d["layout"]
         sets.append((d["q"], d["k_pool"], d["v_pool"], lay.block_tables.to(dev),
                      lay.context_lens.to(dev), torch.empty_like(d["q"])))
+    resident = sets[0][1].numel() * sets[0][1].element_size() * 2
+    full_pages = sum(math.ceil(n / 16) for n in wl.C4_LENGTHS)
+    full_bytes = full_pages * 8 * 128 * 16 * 2 * 2
     w, ns = wl.C4_WINDOW, wl.C4_SINKS
     batch, max_blocks = sets[0][0].shape[0], sets[0][3].shape[1]
     ws = torch.empty(iva.decode_workspace_bytes(batch, 32, 8, 128, 16, max_blocks, w, ns),
@@ -624,7 +641,9 @@ def bench_c4(args, iva, torch, dev):
             "dtype": "bf16", "config": {"lengths": wl.C4_LENGTHS, "window": w, "sinks": ns,
                                         "heads": "32/8", "head_dim": 128,
                                         "launch": "hip graph of back-to-back launches",
-                                        "pools_rotated": args.pools},
+                                        "pools_rotated": n_pools,
+                                        "pool": "resident window: sink + window pages only"},
+            "resident_bytes": resident, "full_context_bytes": full_bytes,
             "attention_us": round(t_attn, 2), "walk_us": round(t_walk, 2),
             "walk_gbps": round(byts / (t_walk * 1e-6) / 1e9, 1),
             "walk_frac": round(byts / (t_walk * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
@@ -720,7 +739,7 @@ def bench_c5(args, iva, torch, dev):
         rows["decode_seqs"].append(len(dec_ids))
         rows["decode_bytes"].append(sum(2 * n * hkv * d * 2 for n in dec_lens)
                                     + 2 * len(dec_ids) * hq * d * 2)
-        rows["append_bytes"].append(4 * n_chunk * hkv * d * 2 + 4 * n_chunk)
+        rows["append_bytes"].append(append_bytes(n_chunk, hkv, d, 2))
         rows["prefill_flop"].append(sum(4 * d * hq * sum(range(L - n + 1, L + 1))
                                         for (_, n), L in zip(plan["prefill"], pre_lens)))
         rows["completed"].append(done)
@@ -1010,7 +1029,7 @@ def bench_ops(args, iva, torch, dev):
     slots = [(perm[i * (n // 16):(i + 1) * (n // 16)].repeat_interleave(16) * 16
               + torch.arange(n) % 16).int().to(dev) for i in range(n_app)]
     pos = (torch.arange(n) % 2048).int().to(dev)
-    app_bytes = 4 * n * hkv * d * es + 4 * n
+    app_bytes = append_bytes(n, hkv, d, es)
     timed("append", lambda i: iva.kv_append(rows[i][0], rows[i][1], k_pool, v_pool, slots[i]),
           app_bytes, n_app)
     timed("append_rope", lambda i: iva.kv_append(rows[i][0], rows[i][1], k_pool, v_pool, slots[i],
@@ -1130,7 +1149,9 @@ def main():
                   "algorithmic_bytes": t_attn, "attention_us": round(mt["attn_us"], 3),
                   "step_us": round(mt["step_ms"] * 1e3, 3),
                   "step_gbs": round((t_append + t_attn) / (mt["step_ms"] * 1e-3) / 1e9, 1),
-                  "traffic": read_traffic("4096")}
+                  "traffic": read_traffic("4096"),
+                  "traffic_source": "profiles/decode_attn_ctx4096_traffic.json (committed "
+                                    "counter runs; not measured in this run)"}
     if args.copy_calibration:
         src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(7)
         dst = torch.empty_like(src)
@@ -1190,7 +1211,12 @@ def main():
                    args.partition_pages else "ivakv_decode_append_attn (fused)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": walk_name,
+                     "traffic": traffic,
+                     "traffic_source": (f"profiles/{traffic_path(args.context).name}: committed "
+                                        "rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this walk, "
+                                        "scaled by a plain copy; not measured in this run")
+                     if traffic is not None else None,
+                     "kernel": walk_name,
                      "kernel_us": round(walk_us, 3), "algorithmic_bytes": attn_b,
                      "frac_of_measured_read_reference":
                          round(achieved / ceiling["read_reference_gbs"], 4) if ceiling else None},

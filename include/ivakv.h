@@ -190,11 +190,14 @@ int ivakv_decode_append_attn(const void* q, const void* k_new, const void* v_new
 /*
  * ivakv_decode_append_attn without a workspace argument: the same plan, kernels and
  * results as ivakv_decode_append_attn, with the decode workspace taken from a
- * file-scope device array of the library (64 MiB per device, held from the first call
- * on a device until the process ends).  It allocates nothing: no hipMalloc, hipFree or
- * allocating library call.  A geometry whose workspace exceeds 64 MiB (see
- * ivakv_decode_workspace_size; e.g. more than ~12k (sequence, kv head) units at GQA 4,
- * D 128) returns IVAKV_E_WORKSPACE before any launch.  Every call on one device shares
+ * file-scope device array of the library (64 MiB per device).  The array sits in a code
+ * object of its own (ivakv_noalloc.hip), which a device maps on the first call of this
+ * entry point there and holds until the process ends; the library's other entry points
+ * leave it unmapped.  It allocates nothing: no hipMalloc, hipFree or allocating library
+ * call.  A geometry whose workspace exceeds 64 MiB (see ivakv_decode_workspace_size: at
+ * GQA 4, D 128 a slot takes 2080 B and 4096 slots are the wave budget, so more than
+ * ~28k (sequence, kv head) units, ~3.5k sequences at 8 kv heads) returns
+ * IVAKV_E_WORKSPACE before any launch.  Every call on one device shares
  * that device's array: calls that overlap on one device (different streams, or
  * threads) race and must be serialised by the caller.  Nothing in the array needs to
  * start at zero.

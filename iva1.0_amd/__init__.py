@@ -31,7 +31,7 @@ from .ops import (
     scale_shape,
 )
 from .model import PagedAttention, Transformer, TransformerConfig, get_attention
-from .paged_cache import OutOfPagesError, PagedKVCache, PagedKVPool
+from .paged_cache import OutOfPagesError, PagedKVCache, PagedKVPool, create_kv_cache
 
 __all__ = [
     "OutOfPagesError",
@@ -40,6 +40,7 @@ __all__ = [
     "PagedKVPool",
     "Transformer",
     "TransformerConfig",
+    "create_kv_cache",
     "get_attention",
     "chunk_elems",
     "copy_pages",

@@ -26,7 +26,6 @@
 //     stream walk's page prefix in LDS): grid (kv head, sequence, partition) of 4-wave
 //     workgroups; a partition of part_pages pages is split over the 4 waves
 //     and merged through LDS, then across partitions by decode_merge_kernel.
-#include <mutex>
 #include <type_traits>
 
 #include "ivakv_e4m3.h"
@@ -1230,40 +1229,6 @@ int single_partition_pages(int batch, int num_kv_heads, int max_blocks, int wind
   return (int64_t)batch * num_kv_heads >= cus ? max_eff : 0;
 }
 
-// Scratch of ivakv_decode_append_attn_noalloc: the decode workspace (one fp32 partial
-// per wave budget slot and per (sequence, kv head), then the batch's page prefix) in a
-// file-scope device array, so that entry point allocates nothing.  Every device the
-// library runs on holds its own copy until the process ends.  In host code the name
-// `scratch` is a host-side stand-in, not a device address: the address comes from
-// hipGetSymbolAddress, looked up once per device (with that device current) and kept.
-constexpr size_t kScratchBytes = (size_t)64 << 20;
-static __device__ __align__(256) unsigned char scratch[kScratchBytes];
-
-constexpr int kMaxScratchDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxScratchDevices] = {};
-
-// Device address of this device's scratch array (looked up on the first call per device).
-int scratch_address(const char* name, void** ptr) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return fail(IVAKV_E_LAUNCH, "%s: hipGetDevice: %s", name, hipGetErrorString(e));
-  if (dev < 0 || dev >= kMaxScratchDevices)
-    return fail(IVAKV_E_ARG, "%s: device %d outside the %d devices the scratch table holds", name,
-                dev, kMaxScratchDevices);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
-    void* p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !p)
-      return fail(IVAKV_E_LAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", name, dev,
-                  hipGetErrorString(e));
-    g_scratch_ptr[dev] = p;
-  }
-  *ptr = g_scratch_ptr[dev];
-  return IVAKV_OK;
-}
-
 int decode_entry(Stage stage, const char* name, const void* q, const void* k_pool,
                  const void* v_pool, const int32_t* block_tables, const int32_t* context_lens,
                  void* out, void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
@@ -1454,17 +1419,17 @@ extern "C" int ivakv_decode_attn_fp8(const void* q, const void* k_pool, const vo
                       n_sink, 0, dtype, stream, nullptr, nullptr, k_scale, v_scale, true);
 }
 
-// The fused decode step with its workspace in the library's static scratch (no
-// allocation anywhere).  Same plan, kernels and results as ivakv_decode_append_attn.
-extern "C" int ivakv_decode_append_attn_noalloc(const void* q, const void* k_new,
-                                                const void* v_new, void* k_pool, void* v_pool,
-                                                const int32_t* block_tables,
-                                                const int32_t* context_lens, void* out,
-                                                int batch, int num_q_heads, int num_kv_heads,
-                                                int head_dim, int block_size, int max_blocks,
-                                                int num_pages, float scale, int window,
-                                                int n_sink, int dtype, hipStream_t stream) {
-  static const char* name = "ivakv_decode_append_attn_noalloc";
+// The fused decode step with a workspace of at most `capacity` bytes that get_ws
+// supplies (called once, after the plan, when the plan needs one and a launch follows):
+// ivakv_decode_append_attn_noalloc (ivakv_noalloc.hip) passes its static scratch.
+// Same plan, kernels and results as ivakv_decode_append_attn.
+int ivakv::decode_append_attn_capped(const char* name, const void* q, const void* k_new,
+                                     const void* v_new, void* k_pool, void* v_pool,
+                                     const int32_t* block_tables, const int32_t* context_lens,
+                                     void* out, int batch, int num_q_heads, int num_kv_heads,
+                                     int head_dim, int block_size, int max_blocks, int num_pages,
+                                     float scale, int window, int n_sink, int dtype,
+                                     hipStream_t stream, size_t capacity, WorkspaceSource get_ws) {
   if (dtype_size(dtype) == 0) return fail(IVAKV_E_DTYPE, "%s: unknown dtype code %d", name, dtype);
   const int pp = block_size == kBS && n_sink >= 0
                      ? single_partition_pages(batch, num_kv_heads, max_blocks, window, n_sink)
@@ -1473,17 +1438,17 @@ extern "C" int ivakv_decode_append_attn_noalloc(const void* q, const void* k_new
   const int st = make_plan(name, kFused, batch, num_q_heads, num_kv_heads, head_dim, block_size,
                            max_blocks, window, n_sink, pp, &plan);
   if (st != IVAKV_OK) return st;
-  if (plan.ws_bytes > kScratchBytes)
+  if (plan.ws_bytes > capacity)
     return fail(IVAKV_E_WORKSPACE,
                 "%s: this geometry needs %zu bytes of workspace, more than the %zu bytes of "
                 "the library's static scratch; call ivakv_decode_append_attn with a workspace",
-                name, plan.ws_bytes, kScratchBytes);
+                name, plan.ws_bytes, capacity);
   if (batch == 0) return IVAKV_OK;
   void* ws = nullptr;
-  const int sst = scratch_address(name, &ws);
+  const int sst = get_ws(name, &ws);
   if (sst != IVAKV_OK) return sst;
   return decode_entry(kFused, name, q, k_pool, v_pool, block_tables, context_lens, out, ws,
-                      kScratchBytes, batch, num_q_heads, num_kv_heads, head_dim, block_size,
+                      capacity, batch, num_q_heads, num_kv_heads, head_dim, block_size,
                       max_blocks, num_pages, scale, window, n_sink, pp, dtype, stream, k_new,
                       v_new);
 }

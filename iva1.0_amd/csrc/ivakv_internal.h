@@ -17,6 +17,20 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // when the launch failed, IVAKV_OK otherwise.
 int launch_status(const char* what);
 
+// Supplies a workspace's device address for the entry point `name`, or an error status.
+typedef int (*WorkspaceSource)(const char* name, void** ptr);
+
+// ivakv_decode_append_attn with its workspace from get_ws instead of an argument, for a
+// plan of at most `capacity` bytes (IVAKV_E_WORKSPACE beyond, before any launch).
+// Defined in ivakv_decode.hip.
+int decode_append_attn_capped(const char* name, const void* q, const void* k_new,
+                              const void* v_new, void* k_pool, void* v_pool,
+                              const int32_t* block_tables, const int32_t* context_lens, void* out,
+                              int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                              int block_size, int max_blocks, int num_pages, float scale,
+                              int window, int n_sink, int dtype, hipStream_t stream,
+                              size_t capacity, WorkspaceSource get_ws);
+
 inline int dtype_size(int dtype) {
   switch (dtype) {
     case IVAKV_F32: return 4;

@@ -335,7 +335,10 @@ class PagedAttention(_AttentionBase):
     returned in its place.  Without a cache a causal step runs the same kernels on a
     one-layer paged cache of its own tokens, and None is returned, as the reference
     returns (attention.py:74-75).  Non-causal attention (``config.causal`` False) is
-    evaluated in torch on the gathered pages: the paged kernels are causal.
+    evaluated in torch on the gathered pages: the paged kernels are causal.  With a
+    sliding window, once the forward's last layer is enqueued the cache releases the
+    pages no later query can see (:meth:`PagedKVCache.release_window`; the sink pages
+    stay resident), so a long sequence holds about window + sinks tokens per layer.
     """
 
     def forward(self, x: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
@@ -355,6 +358,8 @@ class PagedAttention(_AttentionBase):
         q, k, v = self._project(x)
         n_sink = _sink_count(sink_cfg, self.sink_tokens)
         window = sliding_window if sliding_window and sliding_window > 0 else None
+        if kv_cache is not None and kv_cache.current_layer == 0:
+            kv_cache.note_window(window, n_sink)
         rope_pos = None  # K rows rotated inside the append instead of separately
         if self.rope:
             # absolute positions of the new tokens, token-major [B * s] int32 on the device
@@ -408,6 +413,10 @@ class PagedAttention(_AttentionBase):
                     torch.ones(s, total, dtype=torch.bool, device=x.device)
                 out = _attend(q.transpose(1, 2), kc, vc, self.scale, allowed[None, None])
                 out = out.transpose(1, 2)
+        if kv_cache is not None and returned is not None and kv_cache.current_layer == 0:
+            # the forward's last layer is enqueued: with a sliding window, the pages no later
+            # query can see go back to the pool (sink pages stay)
+            kv_cache.release_window()
         out = out.reshape(b, s, self.d_model)
         return self.o_proj(out), (kv_cache if returned is not None else None)
 

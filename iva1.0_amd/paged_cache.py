@@ -392,8 +392,14 @@ class PagedKVCache:
     def __init__(self, batch_size: int, n_heads: int, head_dim: int, seq_len: int = 0,
                  device=None, dtype: torch.dtype = torch.float16, *, num_layers: int = 1,
                  block_size: int = 16, max_seq_len: int = 4096, num_pages: Optional[int] = None,
-                 pool: Optional[PagedKVPool] = None, compute_dtype: Optional[torch.dtype] = None):
+                 pool: Optional[PagedKVPool] = None, compute_dtype: Optional[torch.dtype] = None,
+                 release_window: bool = True):
         self.batch_size = int(batch_size)
+        # sliding-window attention: pages no later query can see go back to the pool
+        # after each forward (release_window), the sink pages stay resident
+        self.window_release = bool(release_window)
+        self._window: Optional[Tuple[int, int]] = None     # (window, n_sink) noted this forward
+        self._released: Optional[Tuple[int, int]] = None   # strictest policy applied so far
         self.n_heads = int(n_heads)
         self.head_dim = int(head_dim)
         self.device = torch.device(device) if device is not None else torch.device("cuda")
@@ -524,6 +530,53 @@ class PagedKVCache:
             if self.pool.has_sequence(s):
                 self.pool.free(s)
 
+    # ------------------------------------------------------ window release
+    @property
+    def window_policy(self) -> Optional[Tuple[int, int]]:
+        """(window, n_sink) the current forward attends with, or None (full context)."""
+        return self._window
+
+    def note_window(self, window: Optional[int], n_sink: int = 0) -> None:
+        """Records the sliding window and attention sinks the forward about to run attends
+        with (decode and prefill queries at position p see [0, n_sink) and
+        [p - window + 1, p]; the decode kernels' union, src/core/attention.py:83-93,
+        115-148).  Once pages outside a window were released, a forward may only attend
+        to what stayed resident: a window no larger and sinks within the kept sink pages;
+        anything else raises ValueError."""
+        w = int(window) if window is not None and int(window) > 0 else 0
+        ns = max(int(n_sink), 0) if w else 0
+        if self._released is not None:
+            rw, rs = self._released
+            kept_sinks = math.ceil(rs / self.block_size) * self.block_size
+            if w == 0 or w > rw or ns > kept_sinks:
+                raise ValueError(
+                    f"pages outside a window of {rw} tokens (+ {rs} sink tokens) were released; "
+                    f"a forward with window {w or None} and {ns} sinks would read them "
+                    "(construct the cache with release_window=False to keep every page)")
+        self._window = (w, ns) if w else None
+
+    def release_window(self) -> int:
+        """Returns to the pool the pages that no later query of this cache can see under
+        the noted window (:meth:`PagedKVPool.release_outside_window`): with length L only
+        the sink pages and [L - window, L) stay resident, so a long sequence holds about
+        window + sinks tokens per layer.  Released positions read back as zeros through
+        ``k`` / ``v`` / ``get_slice``.  A no-op without a window, with
+        ``release_window=False``, or in static decode (its captured graph holds the block
+        table; :meth:`end_static_decode` releases).  Returns the pages released."""
+        if self._window is None or not self.window_release or self._static is not None:
+            return 0
+        w, ns = self._window
+        n = sum(self.pool.release_outside_window(s, w, ns) for s in self.seq_ids)
+        if n:
+            rw, rs = self._released if self._released is not None else (w, ns)
+            self._released = (min(rw, w), min(rs, ns))
+            self._bt_gen = -1
+        return n
+
+    def resident_pages(self) -> int:
+        """Pages this cache's sequences hold (per layer)."""
+        return sum(1 for s in self.seq_ids for p in self.pool.pages(s) if p >= 0)
+
     # ------------------------------------------------------- layer cursor
     def _tables(self) -> Tuple[torch.Tensor, torch.Tensor]:
         """Device block table (copied again only when the pool's tables changed since the
@@ -584,6 +637,7 @@ class PagedKVCache:
                 self.pool.allocate(s, grow)
         self._static = None
         self._bt_gen = -1
+        self.release_window()
 
     def _static_step(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, int, int]:
         st = self._static
@@ -673,3 +727,18 @@ class PagedKVCache:
                   torch.from_numpy(slots).to(self.device), **self.pool.scales(layer_only))
         if commit:
             self.seq_len = t
+
+
+def create_kv_cache(batch_size: int, n_heads: int, head_dim: int, seq_len: int,
+                    device=None, dtype: torch.dtype = torch.float16, **kwargs) -> PagedKVCache:
+    """The paged counterpart of the reference's factory ``create_kv_cache(batch_size,
+    n_heads, head_dim, seq_len, device, dtype=torch.float16)`` (src/core/rope_kv.py:165-173):
+    same arguments and meaning (``seq_len`` zero rows per sequence to start with, as
+    ``KVCache`` allocates), returning a :class:`PagedKVCache`.  Keyword arguments go to
+    the PagedKVCache constructor (``num_layers``, ``max_seq_len``, ``num_pages``, ``pool``,
+    ``block_size``, ``compute_dtype``, ``release_window``); ``max_seq_len`` defaults to
+    ``seq_len`` (at least one page), and the pool grows no further than the pages it
+    reserves for that."""
+    kwargs.setdefault("max_seq_len", max(int(seq_len), 1))
+    return PagedKVCache(batch_size, n_heads, head_dim, seq_len, device, dtype, **kwargs)
+

@@ -145,10 +145,46 @@ C4_WINDOW = 4096
 C4_SINKS = 4
 
 
+def window_layout(lengths: List[int], window: int, n_sink: int, gen: torch.Generator,
+                  block_size: int = BLOCK_SIZE) -> PagedLayout:
+    """The block tables a sliding-window cache holds once the pages outside the window and
+    the sinks are released (PagedKVPool.release_outside_window): sequence b of length L
+    keeps the sink pages [0, ceil(n_sink / bs)) and the pages from (L - window) // bs on;
+    the entries between are -1.  The kept pages are a seeded permutation of a pool of
+    exactly that many pages."""
+    sink_pages = math.ceil(max(int(n_sink), 0) / block_size)
+    keep = []
+    for n in lengths:
+        n_log = math.ceil(int(n) / block_size)
+        first = max((int(n) - int(window)) // block_size, sink_pages) if window > 0 else sink_pages
+        keep.append(list(range(min(sink_pages, n_log))) + list(range(first, n_log)))
+    num_pages = max(sum(len(k) for k in keep), 1)
+    perm = torch.randperm(num_pages, generator=gen).to(torch.int32)
+    mb = max([math.ceil(int(n) / block_size) for n in lengths] + [1])
+    bt = torch.full((len(lengths), mb), -1, dtype=torch.int32)
+    cur = 0
+    for b, k in enumerate(keep):
+        bt[b, k] = perm[cur:cur + len(k)]
+        cur += len(k)
+    return PagedLayout([int(n) for n in lengths], bt, num_pages, block_size)
+
+
 def c4_long_context(seed: int = 0, device=None, lengths: Optional[List[int]] = None,
-                    dtype: torch.dtype = torch.bfloat16) -> dict:
-    """C4: 4 long sequences, window 4096 + 4 sinks, bf16, K/V ~ N(0, 1)."""
-    d = decode_batch(lengths or C4_LENGTHS, 32, 8, 128, dtype, seed, device, scale=1.0)
+                    dtype: torch.dtype = torch.bfloat16, resident_window: bool = False) -> dict:
+    """C4: 4 long sequences, window 4096 + 4 sinks, bf16, K/V ~ N(0, 1).  With
+    ``resident_window`` the pool holds only the pages a sliding-window cache keeps
+    resident (window_layout: the sink pages and the window's), as PagedKVCache does after
+    each forward; otherwise every page of every context."""
+    lengths = lengths or C4_LENGTHS
+    if not resident_window:
+        d = decode_batch(lengths, 32, 8, 128, dtype, seed, device, scale=1.0)
+    else:
+        gen = torch.Generator().manual_seed(seed)
+        layout = window_layout(lengths, C4_WINDOW, C4_SINKS, gen)
+        k_pool, v_pool = random_pools(layout.num_pages, 8, 128, dtype, seed, device, 1.0)
+        q = _randn((len(lengths), 32, 128), seed * 1000 + 13, device, dtype, 1.0)
+        d = dict(lengths=list(lengths), layout=layout, k_pool=k_pool, v_pool=v_pool, q=q,
+                 num_q_heads=32, num_kv_heads=8, head_dim=128)
     d.update(window=C4_WINDOW, n_sink=C4_SINKS)
     return d
 

@@ -293,3 +293,36 @@ def test_cache_update_exhaustion_changes_nothing(iva):
         cache.update(rows, rows, 0)
     assert [(cache.pool.length(s), cache.pool.pages(s)) for s in cache.seq_ids] == before
     assert cache.pool.num_free_pages == free
+
+
+def test_cache_window_policy_releases_and_guards(iva):
+    """PagedKVCache's window release (host bookkeeping only): the noted window's
+    invisible pages go back to the pool, the sink page stays, and a later forward may not
+    widen the window or its sinks past what stayed resident."""
+    from importlib import import_module
+    pc = import_module("iva_amd.paged_cache")
+    p = pc.PagedKVPool(64, 2, 64, 16, allocate_storage=False, device="cpu", max_seqs=8)
+    cache = pc.PagedKVCache(2, 2, 64, 0, "cpu", pool=p)
+    for s in cache.seq_ids:
+        p.allocate(s, 300)                      # 19 pages each
+    cache.seq_len = 300
+    assert cache.resident_pages() == 38
+    assert cache.release_window() == 0          # no window noted: nothing happens
+    cache.note_window(64, 4)
+    assert cache.window_policy == (64, 4)
+    released = cache.release_window()
+    # visible: [0, 4) and [236, 300) -> pages 0 and 14..18 stay
+    assert released == 2 * 13 and cache.resident_pages() == 2 * 6
+    assert all(p.pages(s)[1:14] == [-1] * 13 for s in cache.seq_ids)
+    for bad in ((128, 4), (None, 0), (64, 17)):
+        with pytest.raises(ValueError, match="released"):
+            cache.note_window(*bad)
+    cache.note_window(32, 16)                   # sinks within the kept page, smaller window
+    keep = pc.PagedKVCache(1, 2, 64, 0, "cpu", pool=p, release_window=False)
+    p.allocate(keep.seq_ids[0], 300)
+    keep.seq_len = 300
+    keep.note_window(64, 4)
+    assert keep.release_window() == 0 and keep.resident_pages() == 19
+    keep.note_window(None)                      # nothing was released: any window is fine
+    c2 = pc.create_kv_cache(2, 2, 64, 0, "cpu", pool=p)
+    assert isinstance(c2, pc.PagedKVCache) and c2.seq_len == 0 and c2.batch_size == 2

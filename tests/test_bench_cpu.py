@@ -33,7 +33,8 @@ def test_c2_algorithmic_bytes(iva):
     lengths = iva.workloads.c2_lengths(seed=0)
     append, attn = bench.algorithmic_bytes(lengths, 32, 8, 128, 2)
     assert attn == 287_114_504
-    assert append == 2 * 32 * 8 * 128 * 2 + 4 * 32
+    # the append's one formula: K and V rows read and written, plus the slot map
+    assert append == bench.append_bytes(32, 8, 128, 2) == 4 * 32 * 8 * 128 * 2 + 4 * 32
     # every sequence at 4096 (the target_4k figure)
     assert bench.algorithmic_bytes([4096] * 32, 32, 8, 128, 2)[1] == 537_428_096
 

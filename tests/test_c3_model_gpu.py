@@ -1,8 +1,8 @@
-"""Config C3 at its own geometry on the GPU: the dense decoder (d_model 1024, 16 layers,
-16 heads, head_dim 64, vocab 32000, RMSNorm + SwiGLU, random init, bf16) with
-attn_impl="hip_paged" against the same model on the torch backend (identical weights),
-8 prompts of 512 uniform-random ids and 32 greedy steps (the batch and step count of C3
-reduced; the geometry is C3's).
+"""Config C3 on the GPU: the dense decoder (d_model 1024, 16 layers, 16 heads, head_dim
+64, vocab 32000, RMSNorm + SwiGLU, random init, bf16) with attn_impl="hip_paged" against
+the same model on the torch backend (identical weights): 8 prompts of 512 uniform-random
+ids and 32 greedy steps (plus the HIP-graph decode check), and C3 at full size, 16
+prompts and 256 greedy steps.
 
 The reference's generate cannot pin tokens (its LM head draws a new random weight on
 every call, src/core/heads.py:31-41), so C3 is pinned against this build's torch
@@ -27,6 +27,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = 0.09375
 MIN_COMPARED = 32   # of 8 x 32 = 256 steps
+MIN_COMPARED_FULL = 512   # of 16 x 256 = 4096 steps
 
 
 @pytest.fixture(scope="module")
@@ -35,20 +36,29 @@ def M(iva):
     return import_module("iva_amd.model")
 
 
-def test_c3_geometry_logits_and_greedy_tokens(M, dev):
+@pytest.fixture(scope="module")
+def c3_models(M, dev):
+    """The torch-backend and hip_paged C3 models with identical random weights, and the
+    fp32 model with the same weights."""
     base = dict(d_model=1024, n_layers=16, n_heads=16, vocab_size=32000, seq_len=4096,
                 dropout=0.0)
     torch.manual_seed(0)
     ref = M.Transformer(M.TransformerConfig(attn_impl="torch", **base)).to(dev, torch.bfloat16).eval()
     paged = M.Transformer(M.TransformerConfig(attn_impl="hip_paged", **base)).to(dev, torch.bfloat16).eval()
     paged.load_state_dict(ref.state_dict())
-    prompts = torch.randint(0, 32000, (8, 512), generator=torch.Generator().manual_seed(0)).to(dev)
-    r = check_greedy_parity(ref, paged, prompts, steps=32, tol=TOL, min_compared=MIN_COMPARED)
-    print(f"C3: max |logit diff| {r['max_logit_diff']:.4f}, {r['compared']} steps compared, "
-          f"first divergences (step, torch margin) {r['first_divergence']}", flush=True)
-
     gold = M.Transformer(M.TransformerConfig(attn_impl="torch", **base)).to(dev).eval()
     gold.load_state_dict({k: v.float() for k, v in ref.state_dict().items()})
+    return ref, paged, gold
+
+
+def check_c3(c3_models, batch, steps, min_compared):
+    ref, paged, gold = c3_models
+    dev = next(ref.parameters()).device
+    prompts = torch.randint(0, 32000, (batch, 512), generator=torch.Generator().manual_seed(0)).to(dev)
+    r = check_greedy_parity(ref, paged, prompts, steps=steps, tol=TOL, min_compared=min_compared)
+    print(f"C3 {batch} x (512 + {steps}): max |logit diff| {r['max_logit_diff']:.4f}, "
+          f"{r['compared']} steps compared, first divergences (step, torch margin) "
+          f"{r['first_divergence']}", flush=True)
     l_gold = teacher_forced_logits(gold, r["tokens"], 512)
     err_ref = (r["l_ref"] - l_gold).abs()
     err_pag = (r["l_pag"] - l_gold).abs()
@@ -56,9 +66,19 @@ def test_c3_geometry_logits_and_greedy_tokens(M, dev):
           f"paged max {err_pag.max().item():.4f} mean {err_pag.mean().item():.5f}", flush=True)
     assert err_pag.mean() <= 1.1 * err_ref.mean()
     assert err_pag.max() <= 1.5 * err_ref.max()
+    return prompts
 
+
+def test_c3_geometry_logits_and_greedy_tokens(c3_models):
+    prompts = check_c3(c3_models, 8, 32, MIN_COMPARED)
+    paged = c3_models[1]
     with torch.no_grad():   # the HIP-graph decode emits the eager decode's tokens
         a = paged.generate(prompts[:4], max_length=8, do_sample=False, eos_token_id=None,
                            use_graph=True)
         b = paged.generate(prompts[:4], max_length=8, do_sample=False, eos_token_id=None)
     assert torch.equal(a, b)
+
+
+def test_c3_full_size(c3_models):
+    """C3 as BASELINE.json states it: 16 prompts of 512 ids, 256 greedy steps."""
+    check_c3(c3_models, 16, 256, MIN_COMPARED_FULL)

@@ -5,6 +5,8 @@ with identical weights.
     outputs agree to 2e-5 (the decode kernel's fp32 bound is 1e-5 on attention
     output; the projections add fp32 rounding);
   * window + sink masks through the model (decode kernel page walk vs dense masks);
+  * the no-cache forward (one-layer paged cache of the input's own tokens) vs the torch
+    backend without a cache, module and model;
   * Transformer bf16 (config C3's shape family, scaled down): teacher-forced logits of
     prefill + 16 decode steps agree within bf16 tolerance, and greedy tokens agree
     wherever the torch backend's top-2 margin exceeds twice that tolerance, over a
@@ -73,6 +75,31 @@ def test_attention_module_fp32(M, dev):
             b, _ = ta(x[:, t:t + 1], kv_cache=tcache)
             assert (a - b).abs().max().item() <= 2e-5, f"decode step {t}"
     assert pcache.seq_len == tcache.seq_len == 150
+
+
+def test_no_cache_forward_matches_torch_backend(M, dev):
+    """Without a cache (the path of a plain ``model(input_ids)`` and of the reference's
+    generate_stream, src/api/generate.py:183-188) PagedAttention runs the paged append and
+    prefill kernels on a one-layer cache of its own tokens and returns None, as
+    AttentionTorch does (src/core/attention.py:74-75)."""
+    cfg = M.TransformerConfig(d_model=512, n_layers=1, n_heads=8, n_kv_heads=2, vocab_size=64,
+                              dropout=0.0, attn_impl="hip_paged")
+    torch.manual_seed(5)
+    pa = M.PagedAttention(cfg).to(dev).eval()
+    ta = M.AttentionTorch(M.TransformerConfig(**{**cfg.__dict__, "attn_impl": "torch"})).to(dev).eval()
+    ta.load_state_dict(pa.state_dict())
+    x = torch.randn(3, 333, 512, device=dev) * 0.5
+    with torch.no_grad():
+        for window, sinks in ((None, None), (40, {"sink_tokens": 4})):
+            a, ca = pa(x, sliding_window=window, sink_cfg=sinks)
+            b, cb = ta(x, sliding_window=window, sink_cfg=sinks)
+            assert ca is None and cb is None
+            assert (a - b).abs().max().item() <= 2e-5, f"window {window}"
+    ref, paged = twin_models(M, torch.float32, dev, sliding_window=64, sink_tokens=4)
+    ids = torch.randint(0, 512, (2, 200), device=dev)
+    with torch.no_grad():
+        lr, lp = ref(ids)["logits"], paged(ids)["logits"]
+    assert (lr - lp).abs().max().item() <= 1e-4
 
 
 def test_window_and_sinks_through_the_model(M, dev):

@@ -3,7 +3,8 @@ library's static scratch) against ivakv_decode_append_attn with a caller workspa
 through the C ABI: identical outputs and identical pools (bit for bit: same plan, same
 kernels), on calls in a row with shrinking inputs (the scratch keeps the previous
 call's contents), on the stream walk and on the one-partition path; a geometry whose
-workspace exceeds the scratch is refused before any launch."""
+workspace exceeds the scratch is refused before any launch; the scratch is mapped on a
+device by the first noalloc call there, not by the rest of the library."""
 from __future__ import annotations
 
 import math
@@ -61,6 +62,27 @@ CALLS = [
 ]
 
 
+def test_scratch_is_mapped_by_the_first_noalloc_call(iva, dev):
+    """The 64 MiB scratch sits in a code object of its own: the workspace entry point and
+    the rest of the library leave it unmapped, the first noalloc call on the device maps
+    it (device free memory drops by at least 64 MiB then, and not before).  This file is
+    the only caller of the noalloc entry, and this test its first call in the process."""
+    lengths = [700, 1500, 33]
+    w, kn, vn, bt, ctx = _step_inputs(iva, lengths, 32, 8, 128, torch.float16, 31, dev)
+    _run(iva, "ivakv_decode_append_attn", w, kn, vn, bt, ctx, 0, 0, dev)
+    torch.cuda.synchronize(dev)
+    free0 = torch.cuda.mem_get_info(dev)[0]
+    _run(iva, "ivakv_decode_append_attn", w, kn, vn, bt, ctx, 0, 0, dev)
+    free1 = torch.cuda.mem_get_info(dev)[0]
+    _run(iva, "ivakv_decode_append_attn_noalloc", w, kn, vn, bt, ctx, 0, 0, dev)
+    free2 = torch.cuda.mem_get_info(dev)[0]
+    mib = 1 << 20
+    print(f"device free memory: {free0 / mib:.0f} MiB, after a workspace call "
+          f"{free1 / mib:.0f}, after the first noalloc call {free2 / mib:.0f}", flush=True)
+    assert free0 - free1 < 64 * mib
+    assert free1 - free2 >= 64 * mib
+
+
 def test_noalloc_matches_the_workspace_entry(iva, dev):
     for i, (name, lengths, hq, hkv, d, dtype, window, n_sink) in enumerate(CALLS):
         if lengths is None:
@@ -77,10 +99,15 @@ def test_noalloc_matches_the_workspace_entry(iva, dev):
 
 def test_noalloc_refuses_a_workspace_beyond_the_scratch(iva, dev):
     a = iva._abi
-    fake = 0x10000
     # 8192 sequences x 8 kv heads at GQA 4, D 128: (4096 + 65536) slots x 2080 B > 64 MiB
-    st = a.lib().ivakv_decode_append_attn_noalloc(fake, fake, fake, fake, fake, fake, fake,
-                                                   fake, 8192, 32, 8, 128, 16, 256, 4096,
+    assert iva.decode_workspace_bytes(8192, 32, 8, 128, 16, 256) > 64 << 20
+    # null pointers: were the size check ever to pass, the entry point's null-pointer
+    # check would refuse the call before any launch
+    st = a.lib().ivakv_decode_append_attn_noalloc(None, None, None, None, None, None, None,
+                                                   None, 8192, 32, 8, 128, 16, 256, 4096,
                                                    0.088, 0, 0, a.F16, None)
     assert st == a.E_WORKSPACE
     assert "static scratch" in a.last_error()
+    # 3520 sequences x 8 kv heads (28,160 units) fit, 3600 (28,800) do not
+    assert iva.decode_workspace_bytes(3520, 32, 8, 128, 16, 256) <= 64 << 20
+    assert iva.decode_workspace_bytes(3600, 32, 8, 128, 16, 256) > 64 << 20
