@@ -56,6 +56,8 @@ constexpr int kMaxStreamBatch = 8192;
 // tile).  One 4-wave workgroup per CU keeps 2 x 8 KiB slots per wave in flight at
 // D 128 on 16-bit pages, enough to hold HBM busy; 4 KiB slots (D 64 at 16 bits,
 // D 128 on FP8 pages) need two workgroups per CU for as many bytes in flight.
+// (Deeper rings at one workgroup per CU, 3 or 4 slots of 4 KiB, measured no faster
+// on the C2 FP8 walk: 42.0-43.2 against 41.8-42.0 µs per attention.)
 constexpr int64_t kWG2SlotBytes = 4096;
 constexpr int walk_wgs_per_cu(int64_t slot_bytes) { return slot_bytes <= kWG2SlotBytes ? 2 : 1; }
 
@@ -106,10 +108,18 @@ __device__ inline int num_partitions(const PageWalk& w, const DecodeArgs& a) {
   return n < a.n_parts_max ? n : a.n_parts_max;
 }
 
-// Online-softmax state of one wave: lane holds head ln's running max (the same
+// Lazy rescaling: the reference max m_run of a head moves only when a tile's max
+// exceeds it by more than kLazyLog2 (log2 units), so the weights p = 2^(s - m_run)
+// stay <= 2^kLazyLog2 (exact in the 16-bit P operands) and the O and l rescale,
+// NB * 4 multiplies per tile, runs only on those rare tiles (a wave-uniform branch).
+// (O, l) relative to any m_run is a valid log-sum-exp state, so the merges are
+// unchanged.
+constexpr float kLazyLog2 = 8.f;
+
+// Online-softmax state of one wave: lane holds head ln's reference max (the same
 // in every k-group), its k-group's share of the running sum, and
 // O^T[16m + 4lq + r][ln] in acc[m][r].
-template <int NB>
+template <int NB, bool LAZY = true>
 struct SoftmaxState {
   f32x4 acc[NB];
   float m_run, l_run;
@@ -130,15 +140,22 @@ struct SoftmaxState {
     float mx = fmaxf(fmaxf(sl[0], sl[1]), fmaxf(sl[2], sl[3]));
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == kNegInf ? 0.f : m_new;
-    const float alpha = exp2_fast(m_run - m_use);
+    // -inf + kLazyLog2 is -inf: the first finite tile max always moves it.  Without
+    // LAZY (fp32 at head_dim 256, where the branch costs registers the ring needs) the
+    // reference max follows every increase and the rescale runs every tile.
+    const bool grow = LAZY ? mx > m_run + kLazyLog2 : mx > m_run;
+    if (!LAZY || __builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float m_new = grow ? mx : m_run;
+      const float alpha = grow ? exp2_fast(m_run - m_new) : 1.f;
+      l_run *= alpha;
+#pragma unroll
+      for (int m = 0; m < NB; ++m) acc[m] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = m_run == kNegInf ? 0.f : m_run;
 #pragma unroll
     for (int r = 0; r < 4; ++r) p[r] = exp2_fast(sl[r] - m_use);
-    l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    m_run = m_new;
-#pragma unroll
-    for (int m = 0; m < NB; ++m) acc[m] *= alpha;
+    l_run += (p[0] + p[1]) + (p[2] + p[3]);
   }
 };
 
@@ -161,6 +178,13 @@ __device__ inline void rows_visible(const PageWalk& w, int lp, bool live, const 
   }
 }
 
+// Whether every row of logical page lp is visible (wave-uniform: lp, live and the
+// walk are): then no V row needs masking.
+__device__ inline bool page_visible(const PageWalk& w, int lp, bool live, const DecodeArgs& a) {
+  const int pos0 = lp * kBS;
+  return live && pos0 + kBS <= w.L && (pos0 >= w.win_start || pos0 + kBS <= a.n_sink);
+}
+
 // Register-level tile machinery of one wave (lane = 16 * lq + ln) for pools of
 // the query dtype DT.  Interface shared with TileOps8: QReg / TileReg register
 // sets, load_q, load_tile, score.
@@ -179,7 +203,10 @@ struct TileOps {
   static constexpr int NB = D / 16;              // 16-dim blocks (PV MFMAs per tile)
   static constexpr int64_t kTile = (int64_t)D * kBS;  // elements of one tile
   static constexpr int kRing = kPageBufs;             // stream walk: tiles in flight
-  using State = SoftmaxState<NB>;
+  // fp32 at head_dim 256: a two-tile ring takes 256 of the 512 registers, and the
+  // branches below would spill; its masking and rescaling stay branch-free.
+  static constexpr bool kMaskBranch = !(DT == IVAKV_F32 && D == 256);
+  using State = SoftmaxState<NB, kMaskBranch>;
   struct QReg {
     Chunk16 c[KLD];
   };
@@ -227,10 +254,16 @@ struct TileOps {
     float sl[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) sl[r] = vis[r] ? s[r] * a.scale_log2 : kNegInf;
-    // Rows that are not attended may hold any bits (0 * NaN would poison acc).
-    // Branch-free: no block boundary between the MFMAs and their first use.
+    // Rows that are not attended may hold any bits (0 * NaN would poison acc): a
+    // page with such rows (a sequence's last, a window's first, padding or an invalid
+    // id) zeroes them, behind a wave-uniform branch that full pages skip (except for
+    // fp32 at head_dim 256, whose two-tile ring leaves no registers for it).  The
+    // scores above are selects, so no block boundary separates the MFMAs from their
+    // first use.
+    if (!kMaskBranch || !page_visible(w, lp, live, a)) {
 #pragma unroll
-    for (int m = 0; m < NB; ++m) Tr::mask_rows(t.v[m], vis);
+      for (int m = 0; m < NB; ++m) Tr::mask_rows(t.v[m], vis);
+    }
     float p[4];
     st.fold(sl, p);
     // O^T += V^T . P^T
@@ -331,9 +364,14 @@ struct TileOps8 {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       sl[r] = vis[r] ? s[r] * (a.scale_log2 * __builtin_amdgcn_rcpf(t.ks[r])) : kNegInf;
-    // Zero the bytes of rows that are not attended (any bits, NaN codes included).
-    const uint32_t keep = (vis[0] ? 0xFFu : 0u) | (vis[1] ? 0xFF00u : 0u) |
-                          (vis[2] ? 0xFF0000u : 0u) | (vis[3] ? 0xFF000000u : 0u);
+    // Zero the bytes of rows that are not attended (any bits, NaN codes included),
+    // on pages that have such rows (a wave-uniform branch full pages skip).
+    if (!page_visible(w, lp, live, a)) {
+      const uint32_t keep = (vis[0] ? 0xFFu : 0u) | (vis[1] ? 0xFF00u : 0u) |
+                            (vis[2] ? 0xFF0000u : 0u) | (vis[3] ? 0xFF000000u : 0u);
+#pragma unroll
+      for (int m = 0; m < NB; ++m) t.v[m] &= keep;
+    }
     float p[4];
     st.fold(sl, p);
     float pv_in[4];
@@ -342,8 +380,7 @@ struct TileOps8 {
     const typename Tr::PVec pv = Tr::pack_p(pv_in);
 #pragma unroll
     for (int m = 0; m < NB; ++m) {
-      const uint32_t vb = t.v[m] & keep;
-      const Chunk8 vh{{cvt2<false>(vb), cvt2<true>(vb)}};
+      const Chunk8 vh{{cvt2<false>(t.v[m]), cvt2<true>(t.v[m])}};
       st.acc[m] = Tr::pv(vh, pv, st.acc[m]);
     }
   }
