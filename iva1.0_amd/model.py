@@ -272,10 +272,17 @@ class _AttentionBase(nn.Module):
     def _apply_rope(self, x: torch.Tensor, rope_state: Optional[torch.Tensor]) -> torch.Tensor:
         return x  # attention.py:112-113: RoPE is a no-op inside attention
 
-    def _check_mask(self, attention_mask: Optional[torch.Tensor]) -> None:
-        if attention_mask is not None and not bool(attention_mask.all()):
-            raise NotImplementedError("padding masks are not supported with a KV cache; "
-                                      "give every sequence of a batch the same length")
+    @staticmethod
+    def _key_mask(attention_mask: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+        """The reference's padding mask (src/core/attention.py:95-97): ``attention_mask``
+        [B, M] (0 = masked) is broadcast against the scores [B, H, S, K] as
+        ``attention_mask.unsqueeze(1).unsqueeze(2)``, so it masks keys when M == K and
+        every key of a row when M == 1 (a padded single-token step); other widths fail
+        to broadcast, as in the reference.  Returns that [B, 1, 1, M] bool "key kept"
+        tensor, or None when there is no mask or nothing is masked."""
+        if attention_mask is None or bool(attention_mask.all()):
+            return None
+        return (attention_mask != 0).unsqueeze(1).unsqueeze(2)
 
 
 class AttentionTorch(_AttentionBase):
@@ -310,14 +317,15 @@ class AttentionTorch(_AttentionBase):
                                  dtype=k.dtype)
             new.k, new.v = k, v
             kv_cache = new
-        self._check_mask(attention_mask)
+        key_ok = self._key_mask(attention_mask)
         q_pos = torch.arange(start, start + s, device=x.device)
         k_pos = torch.arange(k.shape[2], device=x.device)
         if self.causal:
             allowed = _visible(q_pos, k_pos, sliding_window, _sink_count(sink_cfg, self.sink_tokens))
         else:
             allowed = torch.ones(s, k.shape[2], dtype=torch.bool, device=x.device)
-        out = _attend(q, k, v, self.scale, allowed[None, None])
+        allowed = allowed[None, None] if key_ok is None else allowed[None, None] & key_ok
+        out = _attend(q, k, v, self.scale, allowed)
         out = out.transpose(1, 2).contiguous().view(b, s, self.d_model)
         return self.o_proj(out), kv_cache
 
@@ -339,6 +347,11 @@ class PagedAttention(_AttentionBase):
     sliding window, once the forward's last layer is enqueued the cache releases the
     pages no later query can see (:meth:`PagedKVCache.release_window`; the sink pages
     stay resident), so a long sequence holds about window + sinks tokens per layer.
+    A padding mask (``attention_mask`` with zeros, src/core/attention.py:95-97) is applied
+    as the reference broadcasts it (:meth:`_key_mask`): the step's rows are still appended
+    and gathered by the kernels, and the masked attention is evaluated on the gathered
+    keys in torch.  A row whose every key is masked gives zeros, where the reference's
+    softmax over all -inf gives NaN (which its next layer then spreads to every row).
     """
 
     def forward(self, x: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
@@ -349,7 +362,7 @@ class PagedAttention(_AttentionBase):
             raise NotImplementedError("the paged attention path is for inference (model.eval())")
         if kv_cache is not None and not isinstance(kv_cache, PagedKVCache):
             kv_cache = self._adopt(kv_cache, x)
-        self._check_mask(attention_mask)
+        key_ok = self._key_mask(attention_mask)
         b, s, _ = x.shape
         returned = kv_cache
         if kv_cache is None and self.causal:
@@ -371,12 +384,17 @@ class PagedAttention(_AttentionBase):
             else:
                 rope_pos = pos
         if kv_cache is None:  # non-causal without a cache
-            allowed = torch.ones(s, s, dtype=torch.bool, device=x.device)
+            allowed = torch.ones(s, s, dtype=torch.bool, device=x.device)[None, None]
+            if key_ok is not None:
+                allowed = allowed & key_ok
             out = _attend(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), self.scale,
-                          allowed[None, None])
+                          allowed)
             out = out.transpose(1, 2)
         else:
-            decode = s == 1 and self.causal
+            # a padding mask: the rows are appended (ivakv_append) and gathered
+            # (ivakv_gather) by the kernels, and the masked attention evaluated on the
+            # gathered keys in torch (the paged attention kernels take no per-key mask)
+            decode = s == 1 and self.causal and key_ok is None
             fp8 = kv_cache.pool.fp8
             view = kv_cache.layer_step(k.contiguous(), v.contiguous(), append=not decode,
                                        rope_positions=rope_pos, rope_theta=self.rope_theta)
@@ -390,7 +408,8 @@ class PagedAttention(_AttentionBase):
                     view.block_tables, view.context_lens, scale=self.scale, window=window or 0,
                     n_sink=n_sink if window else 0, **view.scales)
                 out = o.view(b, 1, self.n_heads, self.head_dim)
-            elif self.causal and (not fp8 or q.dtype in (torch.float16, torch.bfloat16)):
+            elif self.causal and key_ok is None and (not fp8 or q.dtype in (torch.float16,
+                                                                          torch.bfloat16)):
                 # the chunk's rows sit at positions start .. start+s-1 of every sequence
                 # (FP8 pages: dequantized inside the kernel, ivakv_prefill_attn_fp8)
                 qs = torch.arange(0, (b + 1) * s, s, dtype=torch.int32, device=x.device)
@@ -401,8 +420,9 @@ class PagedAttention(_AttentionBase):
                     **view.scales)
                 out = o.view(b, s, self.n_heads, self.head_dim)
             else:
-                # non-causal (or fp32 queries on FP8 pages): gather (dequantized for FP8)
-                # and evaluate the masked attention of the new tokens in torch
+                # non-causal, a padding mask, or fp32 queries on FP8 pages: gather
+                # (dequantized for FP8) and evaluate the masked attention of the new
+                # tokens in torch
                 total = view.start + s
                 kw = dict(view.scales, out_dtype=q.dtype) if fp8 else {}
                 kc, vc = kv_gather(view.k_pool, view.v_pool, view.block_tables,
@@ -411,7 +431,8 @@ class PagedAttention(_AttentionBase):
                 k_pos = torch.arange(total, device=x.device)
                 allowed = _visible(q_pos, k_pos, window, n_sink) if self.causal else \
                     torch.ones(s, total, dtype=torch.bool, device=x.device)
-                out = _attend(q.transpose(1, 2), kc, vc, self.scale, allowed[None, None])
+                allowed = allowed[None, None] if key_ok is None else allowed[None, None] & key_ok
+                out = _attend(q.transpose(1, 2), kc, vc, self.scale, allowed)
                 out = out.transpose(1, 2)
         if kv_cache is not None and returned is not None and kv_cache.current_layer == 0:
             # the forward's last layer is enqueued: with a sliding window, the pages no later

@@ -141,3 +141,56 @@ def test_rope_in_attention_incremental_equals_full(M):
     plain.load_state_dict(model.state_dict())
     with torch.no_grad():
         assert not torch.allclose(plain(ids)["logits"], full, atol=1e-3)  # RoPE does act
+
+
+def _reference_masked_attention(ta, x, attention_mask):
+    """The reference's AttentionTorch.forward without a cache (src/core/attention.py:
+    77-107: scores, causal tril, the padding mask broadcast as mask.unsqueeze(1).unsqueeze(2),
+    softmax, PV), evaluated step by step in float64 with the module's weights; GQA by
+    repeat_interleave of the kv heads."""
+    b, s, d = x.shape
+    hq, hkv, hd = ta.n_heads, ta.n_kv_heads, ta.head_dim
+    xd = x.double()
+    q = (xd @ ta.q_proj.weight.double().T).view(b, s, hq, hd).transpose(1, 2)
+    k = (xd @ ta.k_proj.weight.double().T).view(b, s, hkv, hd).transpose(1, 2)
+    v = (xd @ ta.v_proj.weight.double().T).view(b, s, hkv, hd).transpose(1, 2)
+    k = k.repeat_interleave(hq // hkv, dim=1)
+    v = v.repeat_interleave(hq // hkv, dim=1)
+    scores = q @ k.transpose(-2, -1) * (1.0 / hd ** 0.5)
+    scores = scores.masked_fill(torch.tril(torch.ones(s, s)) == 0, float("-inf"))
+    scores = scores.masked_fill(attention_mask.unsqueeze(1).unsqueeze(2) == 0, float("-inf"))
+    out = torch.softmax(scores, dim=-1) @ v
+    out = out.transpose(1, 2).reshape(b, s, d)
+    return out @ ta.o_proj.weight.double().T
+
+
+def test_padding_mask_follows_the_reference(M):
+    """The padding mask of the torch backend (the paged backend shares its semantics; its
+    GPU test compares the two): where the reference's row has a visible key the outputs
+    agree with the float64 evaluation of the reference's expression; a row whose every key
+    is masked is zero where the reference's softmax is NaN; a mask of width 1 masks
+    whole rows (the reference's broadcast); other widths fail to broadcast, as there."""
+    torch.manual_seed(0)
+    ta = M.AttentionTorch(small_cfg(M)).eval()
+    x = torch.randn(3, 9, 64)
+    mask = torch.tensor([[0, 0, 0, 1, 1, 1, 1, 1, 1],      # left padding
+                         [1, 1, 1, 1, 1, 1, 0, 0, 0],      # right padding
+                         [1, 0, 1, 1, 0, 1, 1, 1, 1]])     # holes
+    with torch.no_grad():
+        out, _ = ta(x, attention_mask=mask)
+    ref = _reference_masked_attention(ta, x, mask)
+    nan_rows = torch.isnan(ref).any(dim=-1)
+    assert bool(nan_rows[0, :3].all()) and not bool(nan_rows[1:].any())
+    assert float((out.double() - ref)[~nan_rows].abs().max()) < 1e-5
+    assert float(out[nan_rows].abs().max()) == 0.0
+    # unmasked rows see exactly the unmasked keys: the same as attending without the mask
+    # to a sequence that lacks the padded positions (right padding, sequence 1)
+    with torch.no_grad():
+        short, _ = ta(x[1:2, :6])
+    assert float((out[1, :6] - short[0]).abs().max()) < 1e-5
+    with torch.no_grad():   # width 1: the reference's broadcast over every key
+        o1, _ = ta(x[:, :1], attention_mask=torch.tensor([[1], [0], [1]]))
+        o0, _ = ta(x[:, :1])
+    assert float(o1[1].abs().max()) == 0.0 and torch.allclose(o1[[0, 2]], o0[[0, 2]])
+    with pytest.raises(RuntimeError):
+        ta(x, attention_mask=torch.ones(3, 5, dtype=torch.long).index_fill_(1, torch.tensor([0]), 0))

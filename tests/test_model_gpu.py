@@ -7,6 +7,8 @@ with identical weights.
   * window + sink masks through the model (decode kernel page walk vs dense masks);
   * the no-cache forward (one-layer paged cache of the input's own tokens) vs the torch
     backend without a cache, module and model;
+  * padding masks (no cache, and a masked prefill followed by masked single-token steps)
+    vs the torch backend;
   * Transformer bf16 (config C3's shape family, scaled down): teacher-forced logits of
     prefill + 16 decode steps agree within bf16 tolerance, and greedy tokens agree
     wherever the torch backend's top-2 margin exceeds twice that tolerance, over a
@@ -100,6 +102,37 @@ def test_no_cache_forward_matches_torch_backend(M, dev):
     with torch.no_grad():
         lr, lp = ref(ids)["logits"], paged(ids)["logits"]
     assert (lr - lp).abs().max().item() <= 1e-4
+
+
+def test_padding_masks_match_the_torch_backend(M, dev):
+    """Padding masks (the reference's broadcast, src/core/attention.py:95-97) on the paged
+    backend: the step's rows go through the append and gather kernels, the masked
+    attention is evaluated on the gathered keys; against the torch backend with the same
+    weights, without a cache (left padding, right padding, holes; fully masked rows are
+    zero in both) and with one (a masked prefill, then single-token steps whose width-1
+    masks keep or drop whole rows)."""
+    ref, paged = twin_models(M, torch.float32, dev, sliding_window=None)
+    ids = torch.randint(0, 512, (3, 40), device=dev)
+    mask = torch.ones(3, 40, dtype=torch.long, device=dev)
+    mask[0, :7] = 0
+    mask[1, 31:] = 0
+    mask[2, 5:9] = 0
+    with torch.no_grad():
+        lr = ref(ids, attention_mask=mask)["logits"]
+        lp = paged(ids, attention_mask=mask)["logits"]
+        assert (lr - lp).abs().max().item() <= 1e-4
+        cr = ref.new_kv_cache(3, 48, device=dev)
+        cp = paged.new_kv_cache(3, 48, device=dev)
+        outs = []
+        for m in (ref, paged):
+            c = cr if m is ref else cp
+            o = [m(ids[:, :32], attention_mask=mask[:, :32], kv_cache=c)["logits"]]
+            for t, keep in zip(range(32, 40), ([1, 1, 1], [1, 0, 1], [0, 1, 1], [1, 1, 1])* 2):
+                step_mask = torch.tensor(keep, device=dev).view(3, 1)
+                o.append(m(ids[:, t:t + 1], attention_mask=step_mask, kv_cache=c)["logits"])
+            outs.append(torch.cat(o, dim=1))
+        assert (outs[0] - outs[1]).abs().max().item() <= 1e-4
+        assert cp.seq_len == 40
 
 
 def test_window_and_sinks_through_the_model(M, dev):
