@@ -87,6 +87,21 @@ def test_append_fp8_bit_exact(iva, dev, src, d):
 
 
 @pytest.mark.parametrize("src", [torch.float32, torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_append_fp8_whole_pages_bit_exact(iva, dev, src, d):
+    """Chunk appends whose 16-token groups each fill one page in slot order, mixed with
+    groups that do not (a sequence of 20 tokens, a group spanning two sequences), on 5 kv
+    heads: codes and factors equal the oracle's."""
+    c = fp8_case(iva, [32, 48, 20, 12, 16], 5, d, src, seed=d + 3)
+    g, o = append_both(iva, dev, c)
+    torch.cuda.synchronize()
+    assert np.array_equal(u8(g["k_pool"]), o["k_pool"])
+    assert np.array_equal(u8(g["v_pool"]), o["v_pool"])
+    assert np.array_equal(g["k_scale"].cpu().numpy(), o["k_scale"])
+    assert np.array_equal(g["v_scale"].cpu().numpy(), o["v_scale"])
+
+
+@pytest.mark.parametrize("src", [torch.float32, torch.float16, torch.bfloat16], ids=str)
 @pytest.mark.parametrize("rope", [False, True], ids=["plain", "rope"])
 def test_append_fp8_from_unaligned_strided_rows(iva, dev, src, rope):
     """Source rows that start one element into a wider buffer (aligned to the element
