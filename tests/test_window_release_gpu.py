@@ -15,7 +15,12 @@ wholly between the sink pages and L - window are never read again.
   * model level: hip_paged generation with a sliding window and sinks gives logits
     bit-identical to the same cache with release_window=False, while the released
     cache's resident pages stay at the window + sink pages;
-  * a forward with a larger window than the released one is refused.
+  * a forward with a larger window than the released one is refused;
+  * a released table stays valid through fork (the fork shares the resident pages and
+    keeps the released entries) and compaction (the resident pages move down, the
+    released entries stay -1): decode attention is bit-identical to the unreleased pool's;
+  * the model-level check on FP8 pages too (scaling factors of released pages are never
+    read again).
 """
 from __future__ import annotations
 
@@ -42,8 +47,8 @@ def rows(n, seed, dev, dtype):
     return (torch.randn(n, HKV, D, generator=g, device=dev) * 0.5).to(dtype)
 
 
-def filled_pool(PC, iva, dev, dtype, num_pages):
-    pool = PC.PagedKVPool(num_pages, HKV, D, BS, 1, dtype, dev, max_seqs=len(LENGTHS),
+def filled_pool(PC, iva, dev, dtype, num_pages, max_seqs=len(LENGTHS)):
+    pool = PC.PagedKVPool(num_pages, HKV, D, BS, 1, dtype, dev, max_seqs=max_seqs,
                           max_blocks_per_seq=math.ceil((max(LENGTHS) + 512) / BS))
     for i, n in enumerate(LENGTHS):
         pool.add_sequence(i)
@@ -132,22 +137,61 @@ def test_release_keeps_decode_and_prefill_bit_identical(PC, iva, dev, dtype):
         assert not bool(kr[i][:, ~keep].any()), "released positions gather as zeros"
 
 
+def test_release_then_fork_and_compact(PC, iva, dev):
+    dtype = torch.bfloat16
+    need = sum(math.ceil(n / BS) for n in LENGTHS) + 8
+    full = filled_pool(PC, iva, dev, dtype, need)
+    rel = filled_pool(PC, iva, dev, dtype, need, max_seqs=len(LENGTHS) + 1)
+    ids = list(range(len(LENGTHS)))
+    released = sum(rel.release_outside_window(i, WINDOW, SINKS) for i in ids)
+    assert released > 0
+    fork_of = 1                     # 9000 tokens: a partial last page, copied by the fork
+    rel.fork(fork_of, len(LENGTHS))
+    assert LENGTHS[fork_of] % BS and rel.pages(len(LENGTHS))[-1] != rel.pages(fork_of)[-1]
+    assert rel.pages(len(LENGTHS))[:-1] == rel.pages(fork_of)[:-1]   # -1 entries included
+    live = rel.num_pages - rel.num_free_pages
+    moved = rel.compact()
+    assert moved > 0 and rel.num_pages - rel.num_free_pages == live
+    for i in ids + [len(LENGTHS)]:   # resident pages now below `live`, released ones -1
+        pg = rel.pages(i)
+        n = LENGTHS[i] if i < len(LENGTHS) else LENGTHS[fork_of]
+        assert all(p < live for p in pg)
+        assert sum(p < 0 for p in pg) == (n - WINDOW) // BS - math.ceil(SINKS / BS)
+
+    g = torch.Generator(device=dev).manual_seed(11)
+    q = (torch.randn(len(LENGTHS), HQ, D, generator=g, device=dev) * 0.5).to(dtype)
+    kw = dict(window=WINDOW, n_sink=SINKS)
+    # the same batch shape on both pools (the walk's split, and so its rounding, depends
+    # on the batch): the unreleased pool lists the forked sequence's source twice
+    q4 = torch.cat([q, q[fork_of:fork_of + 1]])
+    bt_full, ctx = full.device_tables(ids + [fork_of])
+    o_full = iva.paged_decode_attention(q4, full.k_pools[0], full.v_pools[0], bt_full, ctx, **kw)
+    bt_rel, ctx_rel = rel.device_tables(ids + [len(LENGTHS)])
+    assert torch.equal(ctx, ctx_rel)
+    o_rel = iva.paged_decode_attention(q4, rel.k_pools[0], rel.v_pools[0], bt_rel, ctx_rel, **kw)
+    assert torch.equal(o_full.view(torch.int16), o_rel.view(torch.int16))
+
+
 @pytest.fixture(scope="module")
 def M(iva):
     from importlib import import_module
     return import_module("iva_amd.model")
 
 
-def test_model_window_release(M, PC, dev):
+@pytest.mark.parametrize("pages", ["bf16", "fp8"])
+def test_model_window_release(M, PC, dev, pages):
     cfg = dict(d_model=256, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=512, seq_len=1024,
                dropout=0.0, sliding_window=48, sink_tokens=4, attn_impl="hip_paged")
+    if pages == "fp8":
+        cfg["kv_cache_dtype"] = "fp8"
+    page_dtype = torch.float8_e4m3fn if pages == "fp8" else torch.bfloat16
     torch.manual_seed(0)
     model = M.Transformer(M.TransformerConfig(**cfg)).to(dev, torch.bfloat16).eval()
     ids = torch.randint(0, 512, (3, 300), device=dev)
 
     def run(release):
-        cache = PC.PagedKVCache(3, 2, 64, 0, dev, torch.bfloat16, num_layers=2, max_seq_len=300,
-                                release_window=release)
+        cache = PC.PagedKVCache(3, 2, 64, 0, dev, page_dtype, num_layers=2, max_seq_len=300,
+                                release_window=release, compute_dtype=torch.bfloat16)
         resident = []
         with torch.no_grad():
             outs = [model(ids[:, :100], kv_cache=cache)["logits"]]
@@ -159,6 +203,7 @@ def test_model_window_release(M, PC, dev):
 
     l_keep, c_keep, r_keep = run(False)
     l_rel, c_rel, r_rel = run(True)
+    assert c_rel.pool.fp8 == (pages == "fp8")
     assert torch.equal(l_keep.view(torch.int16), l_rel.view(torch.int16))
     assert c_rel.seq_len == c_keep.seq_len == 300
     assert r_keep[-1] == 3 * math.ceil(300 / 16)
