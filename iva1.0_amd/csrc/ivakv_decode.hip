@@ -203,6 +203,10 @@ struct TileOps {
   static constexpr int NB = D / 16;              // 16-dim blocks (PV MFMAs per tile)
   static constexpr int64_t kTile = (int64_t)D * kBS;  // elements of one tile
   static constexpr int kRing = kPageBufs;             // stream walk: tiles in flight
+  // Query rows reloaded into every ring slot (false) or only when a slot's unit
+  // changes: the reload is hidden behind 8 KiB tiles (C2 walk 47.5 µs against 48.2
+  // with the per-unit form).
+  static constexpr bool kQPerUnit = false;
   // fp32 at head_dim 256: a two-tile ring takes 256 of the 512 registers, and the
   // branches below would spill; its masking and rescaling stay branch-free.
   static constexpr bool kMaskBranch = !(DT == IVAKV_F32 && D == 256);
@@ -296,6 +300,10 @@ struct TileOps8 {
   // The plain ring: a deeper one (as many bytes in flight as for 16-bit pages)
   // measured slower, the FP8 walk being issue-bound rather than latency-bound.
   static constexpr int kRing = kPageBufs;
+  // Query rows loaded into a ring slot only when the slot's unit changes: with 4 KiB
+  // tiles the per-slot reload costs (C2 FP8 attention 41.2-41.5 µs against
+  // 38.7-38.8 µs loading per unit).
+  static constexpr bool kQPerUnit = true;
   using State = SoftmaxState<NB>;
   struct QReg {
     Chunk16 c[2 * KL];  // c[2i + half]: dims 16 * (4i + lq) + 8 * half .. + 8
@@ -857,17 +865,28 @@ __global__ __launch_bounds__(kStreamThreads, Ops::kWGsPerCU) void decode_stream_
   //    cursor.  Past the wave's last tile it stays there and loads padding slots
   //    that score() masks, from page 0 (as for an invalid page id): every wave
   //    reads that same tile, an L2 hit, where re-reading the wave's own last tile
-  //    would miss (the streaming hint lets its lines go early).  Every slot also
-  //    loads the query rows of its tile's unit (an L2 hit after the first): a q
-  //    load only at unit changes would sit on a branch whose join makes the
-  //    compiler drain the ring before every tile.
+  //    would miss (the streaming hint lets its lines go early).  Each slot holds
+  //    the query rows of its tile's unit: loaded with every tile (an L2 hit after
+  //    the first), or with kQPerUnit only when the slot's unit changes (a
+  //    wave-uniform branch; the waits on the ring's tiles stay as they are).
   Cursor lc = c0r, cc = c0r;
   int issued = 0;
   typename Ops::QReg qb[kRing];
   typename Ops::TileReg tb[kRing];
   int64_t pb[kRing];
+  int qunit[kRing];  // unit (b * Hkv + h) whose query rows qb[s] holds (kQPerUnit)
+#pragma unroll
+  for (int s = 0; s < kRing; ++s) qunit[s] = -1;
   auto issue = [&](int s) {
-    Ops::load_q(a, lc.b, lc.h, ln, lq, qb[s]);
+    if constexpr (Ops::kQPerUnit) {
+      const int unit = lc.b * Hkv + lc.h;  // wave-uniform
+      if (unit != qunit[s]) {
+        Ops::load_q(a, lc.b, lc.h, ln, lq, qb[s]);
+        qunit[s] = unit;
+      }
+    } else {
+      Ops::load_q(a, lc.b, lc.h, ln, lq, qb[s]);
+    }
     const int64_t p = phys_page(a, bt, lc.b, logical_page(lc.w, lc.v));
     pb[s] = issued < count ? p : -1;
     Ops::load_tile(a, pb[s], lc.h, ln, lq, tb[s]);
