@@ -298,7 +298,7 @@ struct TileOps8 {
   static constexpr int NB = D / 16;
   static constexpr int64_t kTileBytes = (int64_t)D * kBS;
   // The plain ring: a deeper one (as many bytes in flight as for 16-bit pages)
-  // measured slower, the FP8 walk being issue-bound rather than latency-bound.
+  // measured slower.
   static constexpr int kRing = kPageBufs;
   // Query rows loaded into a ring slot only when the slot's unit changes: with 4 KiB
   // tiles the per-slot reload costs (C2 FP8 attention 41.2-41.5 µs against
