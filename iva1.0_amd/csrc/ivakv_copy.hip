@@ -70,7 +70,10 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
 // (one head per lane: eight rounds of single round trips).  K chunks are stored whole
 // (256 contiguous bytes per 16 consecutive slots); each V chunk is spread over X rows
 // of the page's [D][bs] tile.  Row loads and K stores carry the non-temporal hint
-// (8192 rows from HBM: 14.9 µs against 17.7 µs with neither).
+// (8192 rows from HBM: 14.9 µs against 17.7 µs with neither).  Blocks run in
+// XCD-contiguous order (xcd_contiguous_block).  Groups of 32 or 64 consecutive tokens
+// per lane group (fewer split pages, 16 / 32 bytes per token per load) measured
+// 21 / 33 µs against 14.8 µs on 8192 aligned rows.
 constexpr int kAppendHeads = 8;
 
 template <typename E>
@@ -78,7 +81,7 @@ __global__ __launch_bounds__(256) void append_vec_kernel(AppendArgs a) {
   constexpr int X = 16 / sizeof(E);
   const int nch = a.D / X;
   const int ngrp = cdiv(a.Hkv, kAppendHeads);
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t gid = xcd_contiguous_block(blockIdx.x, gridDim.x) * blockDim.x + threadIdx.x;
   if (gid >= (int64_t)cdiv(a.n_tok, 16) * 16 * ngrp * nch) return;
   const int t_lo = (int)(gid & 15);
   const int64_t g1 = gid >> 4;

@@ -67,7 +67,7 @@ __global__ __launch_bounds__(256) void append8_kernel(Append8Args a) {
   constexpr int HALF = D / 2;
   __shared__ float s_cs[ROPE ? 16 * HALF : 1], s_sn[ROPE ? 16 * HALF : 1];
   __shared__ float s_freq[ROPE ? kFreqTable : 1];
-  const int64_t t0 = (int64_t)blockIdx.x * 16;
+  const int64_t t0 = xcd_contiguous_block(blockIdx.x, gridDim.x) * 16;
   if constexpr (ROPE) {
     fill_freqs(s_freq, HALF, D, a.theta);
     for (int e = threadIdx.x; e < 16 * HALF; e += blockDim.x) {

@@ -79,6 +79,18 @@ __device__ inline void st(void* p, const T& v) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Logical index of workgroup b of n (a 1-D grid dimension) such that each XCD runs a
+// contiguous range of them: workgroups are dispatched to the 8 XCDs round-robin (b on
+// XCD b % 8), and XCD x takes logical blocks x * q + min(x, r) .. (q = n / 8, r = n % 8).
+// A bijection on [0, n) whatever the dispatch does; with round-robin dispatch,
+// neighbouring logical blocks share an L2.  The appends use it so the partial 32-byte
+// sectors where a chunk's pages straddle two token groups merge in one L2 before they
+// are written back (a page-unaligned 8192-row chunk append: 20.4 -> 17.4 us).
+__device__ inline int64_t xcd_contiguous_block(int64_t b, int64_t n) {
+  const int64_t q = n >> 3, r = n & 7, x = b & 7;
+  return x * q + (x < r ? x : r) + (b >> 3);
+}
+
 // Ceil division for non-negative ints.
 __host__ __device__ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 

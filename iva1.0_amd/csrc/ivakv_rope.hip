@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
   // so K and V stores coalesce.
   __shared__ float s_freq[kFreqTable];
   fill_freqs(s_freq, a.D / 2, a.D, a.theta);
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t gid = xcd_contiguous_block(blockIdx.x, gridDim.x) * blockDim.x + threadIdx.x;
   if (gid >= (int64_t)cdiv(a.n_tok, 16) * 16 * ngrp * nch) return;
   const int t_lo = (int)(gid & 15);
   const int64_t g1 = gid >> 4;
