@@ -1040,6 +1040,23 @@ def bench_ops(args, iva, torch, dev):
           app_bytes, n_app)
     timed("append_rope", lambda i: iva.kv_append(rows[i][0], rows[i][1], k_pool, v_pool, slots[i],
                                                  rope_positions=pos), app_bytes + 4 * n, n_app)
+
+    # the same rows as 16 chunks of 512 tokens that each start mid-page (offsets 1..15),
+    # as chunked prefill after decode steps lands them (other pages than the above)
+    def unaligned_slots(i):
+        out, base = [], 8192 + i * 16 * 33
+        for ch in range(16):
+            o = 1 + (i * 16 + ch) % 15
+            pg = perm[base + ch * 33: base + ch * 33 + 33]
+            p = o + torch.arange(512)
+            out.append(pg[p // 16] * 16 + p % 16)
+        return torch.cat(out).int().to(dev)
+
+    slots_u = [unaligned_slots(i) for i in range(n_app)]
+    timed("append_unaligned", lambda i: iva.kv_append(rows[i][0], rows[i][1], k_pool, v_pool,
+                                                      slots_u[i]), app_bytes, n_app,
+          extra={"slots": "16 chunks of 512 rows, each starting at page offset 1..15"})
+    del slots_u
     # the same rows into FP8 pages (read fp16 rows, write codes and one factor per row)
     k8, v8 = (torch.zeros(shape, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
               for shape in iva.pool_shapes(pages, hkv, d, 16, torch.float8_e4m3fn))
