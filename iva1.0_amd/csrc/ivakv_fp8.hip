@@ -49,7 +49,8 @@ __device__ inline uint32_t encode4(float a, float b, float c, float d, bool hw) 
   return e4m3_encode(a) | (e4m3_encode(b) << 8) | (e4m3_encode(c) << 16) | (e4m3_encode(d) << 24);
 }
 
-// One workgroup per 16 consecutive tokens and group of kv heads (grid y): wave w of
+// One workgroup per 16 consecutive tokens (token groups in XCD-contiguous order,
+// xcd_contiguous_block) and group of kv heads (grid y): wave w of
 // workgroup (x, y) takes kv heads 4y + w, 4y + w + 4 gridDim.y, ... (a few tokens: one
 // head per wave, so the rows' round trips overlap; many: every head in one workgroup).
 // Lane l of a wave holds token r = l % 16 and chunk group g = l / 16: the 16-dim chunks

@@ -62,7 +62,7 @@ __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
   const int ngrp = cdiv(a.Hkv, kRopeHeads);
   // Thread order (token % 16, chunk, head group, token / 16), as in append_kernel: 16
   // consecutive tokens (consecutive slots of a page in a chunk append) per lane group,
-  // so K and V stores coalesce.
+  // so K and V stores coalesce; workgroups in XCD-contiguous order, as append_vec_kernel.
   __shared__ float s_freq[kFreqTable];
   fill_freqs(s_freq, a.D / 2, a.D, a.theta);
   const int64_t gid = xcd_contiguous_block(blockIdx.x, gridDim.x) * blockDim.x + threadIdx.x;
