@@ -179,8 +179,9 @@ def _counter_rows(directory: str):
     if not files:
         raise SystemExit(f"no *counter_collection.csv under {directory}")
     for f in files:
-        for row in csv.DictReader(f.open()):
-            yield row.get("Kernel_Name", ""), row.get("Counter_Name", ""), float(row["Counter_Value"])
+        with f.open() as fh:
+            for row in csv.DictReader(fh):
+                yield row.get("Kernel_Name", ""), row.get("Counter_Name", ""), float(row["Counter_Value"])
 
 
 def _mean_kib(directory: str, counter: str, match) -> float:
