@@ -121,7 +121,7 @@ def append_bytes(n_tok, hkv, d, esize):
     """Bytes an append of n_tok rows moves: the K and V rows read (2 n Hkv D esize) and
     written into their slots (as many), plus the int32 slot map.  The one formula of every
     append figure here (the C2 step, the ops and C5 lines); like the gather's, it counts
-    reads and writes, twice the rows' size BASELINE.md's append term counts."""
+    reads and writes, twice the rows' size alone."""
     return 4 * n_tok * hkv * d * esize + 4 * n_tok
 
 
