@@ -221,6 +221,45 @@ def test_decode_appends_and_prefill_chunk(iva, dev):
         assert np.array_equal(bits(vo[b, :, :n + 1]), bits(rows_v[b].transpose(0, 1)))
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=str)
+def test_chunks_starting_mid_page(iva, dev, dtype):
+    """Chunked prefill after decode steps: every sequence already holds L_b rows (most not
+    a multiple of 16), and one call appends a 512-row chunk to each of 10 sequences, so
+    every chunk starts mid-page and neighbouring token groups share pages.  Pools
+    bit-identical to the oracle's; with RoPE fused, bit-identical to rope_ followed by
+    the plain append of the rotated rows."""
+    gen = torch.Generator().manual_seed(21)
+    prior = [int(x) for x in torch.randint(1, 900, (10,), generator=gen)]
+    prior[0], prior[1] = 16 * 7, 16 * 3 + 15    # one aligned start, one a row before a page
+    chunk, hkv, d = 512, 8, 128
+    total = [n + chunk for n in prior]
+    num_pages = sum(-(-n // 16) for n in total) + 5
+    lay = iva.workloads.permuted_layout(total, num_pages, gen)
+    n_tok = 10 * chunk
+    k_new = torch.randn(n_tok, hkv, d, generator=gen).to(dtype)
+    v_new = torch.randn(n_tok, hkv, d, generator=gen).to(dtype)
+    slots = torch.cat([lay.slots(b, torch.arange(n, n + chunk)) for b, n in enumerate(prior)])
+    assert sum(n % 16 != 0 for n in prior) >= 8
+    k_pool, v_pool = new_pools(iva, dev, num_pages, hkv, d, 16, dtype, canary=0x1234)
+    iva.kv_append(k_new.to(dev), v_new.to(dev), k_pool, v_pool, slots.to(dev))
+    ok, ov = oracle_pools(num_pages, hkv, d, 16, dtype, canary=0x1234)
+    orc.append(ok, ov, bits(k_new), bits(v_new), slots.numpy())
+    assert np.array_equal(bits(k_pool), ok) and np.array_equal(bits(v_pool), ov)
+    if dtype == torch.float32:
+        return
+    pos = torch.cat([torch.arange(n, n + chunk) for n in prior]).to(torch.int32).to(dev)
+    kf, vf = new_pools(iva, dev, num_pages, hkv, d, 16, dtype, canary=0x1234)
+    iva.kv_append(k_new.to(dev), v_new.to(dev), kf, vf, slots.to(dev), rope_positions=pos)
+    kr, vr = new_pools(iva, dev, num_pages, hkv, d, 16, dtype, canary=0x1234)
+    k_rot = iva.rope_(k_new.to(dev).clone(), pos)
+    iva.kv_append(k_rot, v_new.to(dev), kr, vr, slots.to(dev))
+    assert torch.equal(bits_t(kf), bits_t(kr)) and torch.equal(bits_t(vf), bits_t(vr))
+
+
+def bits_t(t: torch.Tensor) -> torch.Tensor:
+    return t.view(BITS[t.dtype][0])
+
+
 def test_argument_errors(iva, dev):
     k_pool, v_pool = new_pools(iva, dev, 4, 2, 64, 16, torch.float16)
     rows = torch.zeros(3, 2, 64, dtype=torch.float16, device=dev)

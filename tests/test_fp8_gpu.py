@@ -101,6 +101,50 @@ def test_append_fp8_whole_pages_bit_exact(iva, dev, src, d):
     assert np.array_equal(g["v_scale"].cpu().numpy(), o["v_scale"])
 
 
+@pytest.mark.parametrize("src", [torch.float16, torch.bfloat16], ids=str)
+def test_append_fp8_chunks_starting_mid_page(iva, dev, src):
+    """One call appends a 512-row chunk to each of 10 sequences that already hold L_b
+    rows (most not a multiple of 16), so every chunk starts mid-page and neighbouring
+    token groups share pages: codes and factors equal the oracle's; with RoPE fused,
+    byte-identical to rope_ followed by the FP8 append of the rotated rows."""
+    gen = torch.Generator().manual_seed(23)
+    prior = [int(x) for x in torch.randint(1, 900, (10,), generator=gen)]
+    prior[0] = 16 * 5
+    chunk, hkv, d = 512, 8, 128
+    total = [n + chunk for n in prior]
+    num_pages = sum(-(-n // 16) for n in total) + 3
+    lay = iva.workloads.permuted_layout(total, num_pages, gen)
+    k_new = (torch.randn(10 * chunk, hkv, d, generator=gen) * d ** -0.5).to(src)
+    v_new = (torch.randn(10 * chunk, hkv, d, generator=gen) * d ** -0.5).to(src)
+    slots = torch.cat([lay.slots(b, torch.arange(n, n + chunk)) for b, n in enumerate(prior)])
+    ks, vs = iva.pool_shapes(num_pages, hkv, d, 16, FP8)
+    base = dict(k_pool=torch.randint(0, 256, ks, dtype=torch.uint8, generator=gen),
+                v_pool=torch.randint(0, 256, vs, dtype=torch.uint8, generator=gen),
+                k_scale=torch.rand(iva.scale_shape(num_pages, hkv), generator=gen) + 0.5,
+                v_scale=torch.rand(iva.scale_shape(num_pages, hkv), generator=gen) + 0.5,
+                k_new=k_new, v_new=v_new, slots=slots)
+    g, o = append_both(iva, dev, base)
+    torch.cuda.synchronize()
+    assert np.array_equal(u8(g["k_pool"]), o["k_pool"]) and np.array_equal(u8(g["v_pool"]), o["v_pool"])
+    assert np.array_equal(g["k_scale"].cpu().numpy(), o["k_scale"])
+    assert np.array_equal(g["v_scale"].cpu().numpy(), o["v_scale"])
+    pos = torch.cat([torch.arange(n, n + chunk) for n in prior]).to(torch.int32).to(dev)
+    out = []
+    for fused in (True, False):
+        t = {k: base[k].clone().to(dev) for k in ("k_pool", "v_pool", "k_scale", "v_scale")}
+        t["k_pool"], t["v_pool"] = t["k_pool"].view(FP8), t["v_pool"].view(FP8)
+        if fused:
+            iva.kv_append(k_new.to(dev), v_new.to(dev), t["k_pool"], t["v_pool"], slots.to(dev),
+                          k_scale=t["k_scale"], v_scale=t["v_scale"], rope_positions=pos)
+        else:
+            k_rot = iva.rope_(k_new.to(dev).clone(), pos)
+            iva.kv_append(k_rot, v_new.to(dev), t["k_pool"], t["v_pool"], slots.to(dev),
+                          k_scale=t["k_scale"], v_scale=t["v_scale"])
+        out.append([u8(t["k_pool"]), u8(t["v_pool"]), t["k_scale"].cpu().numpy(), t["v_scale"].cpu().numpy()])
+    for a_, b_ in zip(*out):
+        assert np.array_equal(a_, b_)
+
+
 @pytest.mark.parametrize("src", [torch.float32, torch.float16, torch.bfloat16], ids=str)
 @pytest.mark.parametrize("rope", [False, True], ids=["plain", "rope"])
 def test_append_fp8_from_unaligned_strided_rows(iva, dev, src, rope):
