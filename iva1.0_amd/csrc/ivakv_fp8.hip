@@ -49,16 +49,51 @@ __device__ inline uint32_t encode4(float a, float b, float c, float d, bool hw) 
   return e4m3_encode(a) | (e4m3_encode(b) << 8) | (e4m3_encode(c) << 16) | (e4m3_encode(d) << 24);
 }
 
+// Value of lane l ^ 1 (ctrl 0xB1) or l ^ 2 (0x4E) inside each group of four lanes (DPP
+// quad permutation; every lane of the wave active).
+template <int kCtrl>
+__device__ inline float quad_swap(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                               kCtrl, 0xF, 0xF, false));
+}
+
+// One lane's share of a token's K or V row: chunks g, g + 4, .. of 16 elements, each
+// loaded as whole 16-byte words.
+template <typename E, int D>
+struct RowShare {
+  static constexpr int kWords = sizeof(E);  // 16-byte words per 16-element chunk
+  uint4 w[D / 64][kWords];
+};
+template <typename E>
+struct Chunk16 {
+  E e[16];
+};
+
+template <typename E, int D>
+__device__ inline void load_share(const E* row, int g, RowShare<E, D>& s) {
+#pragma unroll
+  for (int j = 0; j < D / 64; ++j)
+#pragma unroll
+    for (int w = 0; w < RowShare<E, D>::kWords; ++w)
+      s.w[j][w] = *reinterpret_cast<const uint4*>(row + 16 * (g + 4 * j) + w * (16 / (int)sizeof(E)));
+}
+
 // One workgroup per 16 consecutive tokens (token groups in XCD-contiguous order,
 // xcd_contiguous_block) and group of kv heads (grid y): wave w of
 // workgroup (x, y) takes kv heads 4y + w, 4y + w + 4 gridDim.y, ... (a few tokens: one
 // head per wave, so the rows' round trips overlap; many: every head in one workgroup).
-// Lane l of a wave holds token r = l % 16 and chunk group g = l / 16: the 16-dim chunks
-// g, g + 4, .. of that token's K and V rows (D / 64 chunks).  A row's max |x| is
-// reduced over the four lanes of its token; each lane then stores its K chunks as
-// whole 16-byte code chunks (16 tokens in consecutive slots of a page: 256 contiguous
-// bytes per chunk) and its V codes byte by byte (assembling 4-byte words across lanes
-// measured slower); the codes come from the hardware conversion (encode4).
+// Each lane holds one token r and chunk group g: the 16-dim chunks g, g + 4, .. of
+// that token's K and V rows (D / 64 chunks).  A group whose 16 tokens fill one page in
+// order (a page-aligned chunk append) puts the tokens across lanes (r = l % 16,
+// g = l / 16: each K store instruction writes 16 consecutive rows of a chunk, 256
+// contiguous bytes); any other group puts a token's four lanes side by side (r = l / 4,
+// g = l % 4), so the V byte stores of a group split over two pages touch fewer lines
+// (8192 rows as 16 chunks starting mid-page 15.4 -> 14.5 us, and 13.4 -> 12.8 us aligned
+// with the uniform branch below).  A row's max |x| is reduced over the four lanes of its
+// token (shuffles, or DPP quad permutations); each lane then stores its K chunks as
+// whole 16-byte code chunks and its V codes byte by byte (assembling 4-byte words
+// across lanes measured slower).  The codes come from the hardware conversion
+// (encode4) in one branch-free block when every row of the wave allows it.
 // ROPE: K is rotated first (rotate_pair, rounded once to the source dtype, as
 // ivakv_rope rounds it), with cos / sin of the workgroup's 16 tokens x D/2 pairs
 // computed once into LDS and shared by every kv head.
@@ -79,7 +114,12 @@ __global__ __launch_bounds__(256) void append8_kernel(Append8Args a) {
     __syncthreads();
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane & 15, g = lane >> 4;
+  // Lane layout only (any slots are handled either way): the group's first and last
+  // tokens at the first and last row of one page.
+  const int32_t s_first = a.slots[t0];
+  const int32_t s_last = t0 + 15 < a.n_tok ? a.slots[t0 + 15] : -1;
+  const bool whole = s_first >= 0 && (s_first & 15) == 0 && s_last == s_first + 15;
+  const int r = whole ? (lane & 15) : (lane >> 2), g = whole ? (lane >> 4) : (lane & 3);
   const int64_t t = t0 + r;
   const bool tok = t < a.n_tok;
   const int64_t slot = tok ? a.slots[t] : -1;
@@ -88,8 +128,9 @@ __global__ __launch_bounds__(256) void append8_kernel(Append8Args a) {
   const int off = ok ? (int)(slot - page * 16) : 0;
   const int64_t tc = tok ? t : t0;  // rows past the batch read the group's first row
   for (int h = 4 * (int)blockIdx.y + wave; h < a.Hkv; h += 4 * (int)gridDim.y) {
-    const E* ks = static_cast<const E*>(a.k_new) + tc * a.kts + h * a.khs;
-    const E* vs = static_cast<const E*>(a.v_new) + tc * a.vts + h * a.vhs;
+    RowShare<E, D> kr, vr;
+    load_share<E, D>(static_cast<const E*>(a.k_new) + tc * a.kts + h * a.khs, g, kr);
+    load_share<E, D>(static_cast<const E*>(a.v_new) + tc * a.vts + h * a.vhs, g, vr);
     E ke[NC][16];
     float kx[NC][16], vx[NC][16];
     // max |x| drops NaN (fmaxf); the sum of |x| is non-finite exactly when the row holds
@@ -99,10 +140,12 @@ __global__ __launch_bounds__(256) void append8_kernel(Append8Args a) {
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
       const int c = g + 4 * j;
+      const Chunk16<E> kc = __builtin_bit_cast(Chunk16<E>, kr.w[j]);
+      const Chunk16<E> vc = __builtin_bit_cast(Chunk16<E>, vr.w[j]);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        ke[j][i] = ks[16 * c + i];
-        vx[j][i] = rope_ld(vs[16 * c + i]);
+        ke[j][i] = kc.e[i];
+        vx[j][i] = rope_ld(vc.e[i]);
       }
       if constexpr (ROPE) {
 #pragma unroll
@@ -120,39 +163,58 @@ __global__ __launch_bounds__(256) void append8_kernel(Append8Args a) {
         vsum += fabsf(vx[j][i]);
       }
     }
-    kmax = fmaxf(kmax, __shfl_xor(kmax, 16));
-    kmax = fmaxf(kmax, __shfl_xor(kmax, 32));
-    vmax = fmaxf(vmax, __shfl_xor(vmax, 16));
-    vmax = fmaxf(vmax, __shfl_xor(vmax, 32));
-    ksum += __shfl_xor(ksum, 16);
-    ksum += __shfl_xor(ksum, 32);
-    vsum += __shfl_xor(vsum, 16);
-    vsum += __shfl_xor(vsum, 32);
+    if (whole) {
+      kmax = fmaxf(kmax, __shfl_xor(kmax, 16));
+      kmax = fmaxf(kmax, __shfl_xor(kmax, 32));
+      vmax = fmaxf(vmax, __shfl_xor(vmax, 16));
+      vmax = fmaxf(vmax, __shfl_xor(vmax, 32));
+      ksum += __shfl_xor(ksum, 16);
+      ksum += __shfl_xor(ksum, 32);
+      vsum += __shfl_xor(vsum, 16);
+      vsum += __shfl_xor(vsum, 32);
+    } else {
+      kmax = fmaxf(kmax, quad_swap<0xB1>(kmax));
+      vmax = fmaxf(vmax, quad_swap<0xB1>(vmax));
+      ksum += quad_swap<0xB1>(ksum);
+      vsum += quad_swap<0xB1>(vsum);
+      kmax = fmaxf(kmax, quad_swap<0x4E>(kmax));
+      vmax = fmaxf(vmax, quad_swap<0x4E>(vmax));
+      ksum += quad_swap<0x4E>(ksum);
+      vsum += quad_swap<0x4E>(vsum);
+    }
     const bool kfin = __builtin_isfinite(ksum), vfin = __builtin_isfinite(vsum);
-    if (!ok) continue;
     const float ksf = kfin ? row_sf(kmax) : 1e-8f, vsf = vfin ? row_sf(vmax) : 1e-8f;
     const bool khw = kfin && kmax * ksf < 464.f, vhw = vfin && vmax * vsf < 464.f;
+    // wave-uniform: every row of the wave takes the hardware conversion
+    const bool all_hw = __builtin_amdgcn_ballot_w64(ok && !(khw && vhw)) == 0;
+    if (!ok) continue;  // a token's four lanes share ok: reductions read active lanes only
     const int64_t tile = page * a.Hkv + h;
     uint8_t* kp = a.k_pool + tile * (int64_t)D * 16;
     uint8_t* vp = a.v_pool + tile * (int64_t)D * 16;
+    auto put = [&](bool kh, bool vh) {
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      const int c = g + 4 * j;
-      uint32_t w[4];
+      for (int j = 0; j < NC; ++j) {
+        const int c = g + 4 * j;
+        uint32_t w[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        w[u] = encode4(kx[j][4 * u] * ksf, kx[j][4 * u + 1] * ksf, kx[j][4 * u + 2] * ksf,
-                       kx[j][4 * u + 3] * ksf, khw);
-      *reinterpret_cast<uint4*>(kp + ((int64_t)c * 16 + off) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+        for (int u = 0; u < 4; ++u)
+          w[u] = encode4(kx[j][4 * u] * ksf, kx[j][4 * u + 1] * ksf, kx[j][4 * u + 2] * ksf,
+                         kx[j][4 * u + 3] * ksf, kh);
+        *reinterpret_cast<uint4*>(kp + ((int64_t)c * 16 + off) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t v4 = encode4(vx[j][4 * u] * vsf, vx[j][4 * u + 1] * vsf,
-                                    vx[j][4 * u + 2] * vsf, vx[j][4 * u + 3] * vsf, vhw);
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t v4 = encode4(vx[j][4 * u] * vsf, vx[j][4 * u + 1] * vsf,
+                                      vx[j][4 * u + 2] * vsf, vx[j][4 * u + 3] * vsf, vh);
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          vp[fp8_v_offset(16 * c + 4 * u + e, off, D)] = (uint8_t)(v4 >> (8 * e));
+          for (int e = 0; e < 4; ++e)
+            vp[fp8_v_offset(16 * c + 4 * u + e, off, D)] = (uint8_t)(v4 >> (8 * e));
+        }
       }
-    }
+    };
+    if (all_hw)
+      put(true, true);
+    else
+      put(khw, vhw);
     if (g == 0) {
       a.k_scale[tile * 16 + off] = ksf;
       a.v_scale[tile * 16 + off] = vsf;
