@@ -101,6 +101,53 @@ def test_append_fp8_whole_pages_bit_exact(iva, dev, src, d):
     assert np.array_equal(g["v_scale"].cpu().numpy(), o["v_scale"])
 
 
+@pytest.mark.parametrize("n_groups", [12, 160], ids=["few_tokens", "many_tokens"])
+def test_append_fp8_groups_that_only_look_page_aligned(iva, dev, n_groups):
+    """Token groups whose first slot starts a page and whose last slot ends it, with
+    anything in between: the rows of that page permuted, a skipped slot, rows of other
+    pages, and a duplicate-free mix with plain page-order groups and groups that start
+    mid-page. Codes and factors equal the oracle's (the kernel picks its lane layout
+    from a group's first and last slot; the result must not depend on it). 12 groups
+    take the one-head-per-wave launch, 160 the every-head-per-workgroup one."""
+    gen = torch.Generator().manual_seed(71 + n_groups)
+    hkv, d = 8, 128
+    num_pages = 2 * n_groups + 4
+    pages = torch.randperm(num_pages, generator=gen)
+    rows = []
+    for i in range(n_groups):
+        p, q = int(pages[2 * i]), int(pages[2 * i + 1])
+        kind = i % 4
+        if kind == 0:  # page order
+            s = p * 16 + torch.arange(16)
+        elif kind == 1:  # first and last in place, the rows between permuted
+            s = p * 16 + torch.cat([torch.tensor([0]), 1 + torch.randperm(14, generator=gen),
+                                    torch.tensor([15])])
+        elif kind == 2:  # first and last of one page, the rows between from another page
+            s = torch.cat([torch.tensor([p * 16]), q * 16 + 1 + torch.arange(14),
+                           torch.tensor([p * 16 + 15])])
+        else:  # starts mid-page and runs into the next page
+            off = int(torch.randint(1, 16, (1,), generator=gen))
+            s = torch.cat([p * 16 + torch.arange(off, 16), q * 16 + torch.arange(off)])
+        rows.append(s)
+    slots = torch.cat(rows).to(torch.int32)
+    slots[16 * 1 + 5] = -1  # a skipped slot inside a permuted group
+    n_tok = slots.numel()
+    ks, vs = iva.pool_shapes(num_pages, hkv, d, 16, FP8)
+    mag = 10.0 ** ((torch.rand(n_tok, hkv, 1, generator=gen) - 0.5) * 6.0)
+    c = dict(k_pool=torch.randint(0, 256, ks, dtype=torch.uint8, generator=gen),
+             v_pool=torch.randint(0, 256, vs, dtype=torch.uint8, generator=gen),
+             k_scale=torch.rand(iva.scale_shape(num_pages, hkv), generator=gen) + 0.5,
+             v_scale=torch.rand(iva.scale_shape(num_pages, hkv), generator=gen) + 0.5,
+             k_new=(torch.randn(n_tok, hkv, d, generator=gen) * mag).half(),
+             v_new=(torch.randn(n_tok, hkv, d, generator=gen) * mag).half(), slots=slots)
+    g, o = append_both(iva, dev, c)
+    torch.cuda.synchronize()
+    assert np.array_equal(u8(g["k_pool"]), o["k_pool"])
+    assert np.array_equal(u8(g["v_pool"]), o["v_pool"])
+    assert np.array_equal(g["k_scale"].cpu().numpy(), o["k_scale"])
+    assert np.array_equal(g["v_scale"].cpu().numpy(), o["v_scale"])
+
+
 @pytest.mark.parametrize("src", [torch.float16, torch.bfloat16], ids=str)
 def test_append_fp8_chunks_starting_mid_page(iva, dev, src):
     """One call appends a 512-row chunk to each of 10 sequences that already hold L_b
