@@ -1079,6 +1079,16 @@ def bench_ops(args, iva, torch, dev):
            for i in range(n_mv)]
     timed("copy_pages", lambda i: iva.copy_pages(k_pool, v_pool, src[i], dst[i]),
           2 * 4096 * 2 * hkv * 16 * d * es + 8 * 4096, n_mv)
+    # the same page moves at the chunk append's size (512 pages: the bytes an 8192-row
+    # append reads and writes), 16 sets: what a plain copy of that size reaches, start-up
+    # and tail included
+    src = [torch.arange(1024 * i, 1024 * (i + 1), 2, dtype=torch.int32, device=dev)
+           for i in range(16)]
+    dst = [torch.arange(40960 + 512 * i, 40960 + 512 * (i + 1), dtype=torch.int32, device=dev)
+           for i in range(16)]
+    timed("copy_pages_512", lambda i: iva.copy_pages(k_pool, v_pool, src[i], dst[i]),
+          2 * 512 * 2 * hkv * 16 * d * es + 8 * 512, 16,
+          extra={"pages": 512, "note": "the bytes of the 8192-row append"})
     del k_pool, v_pool
     # gather of the C2 batch into contiguous [B, Hkv, max L, D]: 4 batches (pools and
     # outputs)
