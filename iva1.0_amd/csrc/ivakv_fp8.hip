@@ -189,25 +189,26 @@ __global__ __launch_bounds__(256) void append8_kernel(Append8Args a) {
     const bool all_hw = __builtin_amdgcn_ballot_w64(ok && !(khw && vhw)) == 0;
     if (!ok) continue;  // a token's four lanes share ok: reductions read active lanes only
     const int64_t tile = page * a.Hkv + h;
-    uint8_t* kp = a.k_pool + tile * (int64_t)D * 16;
-    uint8_t* vp = a.v_pool + tile * (int64_t)D * 16;
+    // The lane's K chunk g and V byte of (dim 16 g, row off); every other store of the
+    // head is at a compile-time distance from these (fp8_v_offset(16 c + dl, off, D) =
+    // dl * D + (off / 4) * (D / 4) + 4 c + off % 4), so one address serves them all.
+    uint8_t* kp = a.k_pool + tile * (int64_t)D * 16 + (g * 16 + off) * 16;
+    uint8_t* vp = a.v_pool + tile * (int64_t)D * 16 + fp8_v_offset(16 * g, off, D);
     auto put = [&](bool kh, bool vh) {
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
-        const int c = g + 4 * j;
         uint32_t w[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u)
           w[u] = encode4(kx[j][4 * u] * ksf, kx[j][4 * u + 1] * ksf, kx[j][4 * u + 2] * ksf,
                          kx[j][4 * u + 3] * ksf, kh);
-        *reinterpret_cast<uint4*>(kp + ((int64_t)c * 16 + off) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+        *reinterpret_cast<uint4*>(kp + j * 4 * 16 * 16) = make_uint4(w[0], w[1], w[2], w[3]);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const uint32_t v4 = encode4(vx[j][4 * u] * vsf, vx[j][4 * u + 1] * vsf,
                                       vx[j][4 * u + 2] * vsf, vx[j][4 * u + 3] * vsf, vh);
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            vp[fp8_v_offset(16 * c + 4 * u + e, off, D)] = (uint8_t)(v4 >> (8 * e));
+          for (int e = 0; e < 4; ++e) vp[(4 * u + e) * D + 16 * j] = (uint8_t)(v4 >> (8 * e));
         }
       }
     };
