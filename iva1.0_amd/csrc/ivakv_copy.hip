@@ -74,43 +74,50 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
 // XCD-contiguous order (xcd_contiguous_block).  Groups of 32 or 64 consecutive tokens
 // per lane group (fewer split pages, 16 / 32 bytes per token per load) measured
 // 21 / 33 µs against 14.8 µs on 8192 aligned rows.
+// Few rows (a decode step's one token per sequence, each to its own page; short
+// chunks): one head per lane in 64-thread workgroups (HEADS = 1), so the stores spread
+// over many CUs instead of the few workgroups eight heads per lane would give.  Rows of
+// 8 kv heads x 128 dims from HBM: a 32-sequence decode step 14.0 -> 2.9 us, 256
+// sequences 16.4 -> 5.7 us, one 512-row chunk 6.1 -> 3.2 us, 2048 rows 7.6 -> 7.1 us;
+// at 8192 rows eight heads per lane stay ahead (15.6 against 18.5 us).
 constexpr int kAppendHeads = 8;
+constexpr int64_t kFewAppendThreads = 1024 * 64;  // below 1024 waves: one head per lane
 
-template <typename E>
+template <typename E, int HEADS>
 __global__ __launch_bounds__(256) void append_vec_kernel(AppendArgs a) {
   constexpr int X = 16 / sizeof(E);
   const int nch = a.D / X;
-  const int ngrp = cdiv(a.Hkv, kAppendHeads);
+  const int ngrp = cdiv(a.Hkv, HEADS);
   const int64_t gid = xcd_contiguous_block(blockIdx.x, gridDim.x) * blockDim.x + threadIdx.x;
   if (gid >= (int64_t)cdiv(a.n_tok, 16) * 16 * ngrp * nch) return;
   const int t_lo = (int)(gid & 15);
   const int64_t g1 = gid >> 4;
   const int c = (int)(g1 % nch);
   const int64_t g2 = g1 / nch;
-  const int h0 = (int)(g2 % ngrp) * kAppendHeads;
+  const int h0 = (int)(g2 % ngrp) * HEADS;
   const int64_t t = (g2 / ngrp) * 16 + t_lo;
   if (t >= a.n_tok) return;
   const int64_t slot = a.slots[t];
   if (slot < 0 || slot >= a.n_slots) return;
   const int64_t page = slot / a.bs;
   const int off = (int)(slot - page * a.bs);
-  const int nh = min(kAppendHeads, a.Hkv - h0);
+  const int nh = min(HEADS, a.Hkv - h0);
   const E* ks = static_cast<const E*>(a.k_new) + t * a.kts + (int64_t)c * X;
   const E* vs = static_cast<const E*>(a.v_new) + t * a.vts + (int64_t)c * X;
   union Row {
     Chunk16 c16;
     E e[X];
   };
-  Row k[kAppendHeads], v[kAppendHeads];
+  Row k[HEADS], v[HEADS];
 #pragma unroll
-  for (int u = 0; u < kAppendHeads; ++u) {
+  for (int u = 0; u < HEADS; ++u) {
     if (u < nh) {
       k[u].c16 = ld<true, Chunk16>(ks + (h0 + u) * a.khs);
       v[u].c16 = ld<true, Chunk16>(vs + (h0 + u) * a.vhs);
     }
   }
 #pragma unroll
-  for (int u = 0; u < kAppendHeads; ++u) {
+  for (int u = 0; u < HEADS; ++u) {
     if (u < nh) {
       const int64_t head_base = page * a.Hkv + h0 + u;
       E* kd = static_cast<E*>(a.k_pool) + ((head_base * nch + c) * a.bs + off) * X;
@@ -291,16 +298,21 @@ extern "C" int ivakv_append(const void* k_new, const void* v_new, int64_t k_tok_
   const bool vec = aligned16(k_new) && aligned16(v_new) && aligned16(k_pool) && aligned16(v_pool) &&
                    (k_tok_stride % X == 0) && (k_head_stride % X == 0) &&
                    (v_tok_stride % X == 0) && (v_head_stride % X == 0);
-  const int64_t per_tok = vec ? (int64_t)cdiv(num_kv_heads, kAppendHeads) : num_kv_heads;
-  const int64_t total = (int64_t)cdiv(n_tok, 16) * 16 * per_tok * (head_dim / X);
-  const unsigned grid = blocks_for(total, 256);
+  const int64_t lanes_per_head_group = (int64_t)cdiv(n_tok, 16) * 16 * (head_dim / X);
+  const bool few = vec && lanes_per_head_group * cdiv(num_kv_heads, kAppendHeads) < kFewAppendThreads;
+  const int64_t per_tok = vec && !few ? (int64_t)cdiv(num_kv_heads, kAppendHeads) : num_kv_heads;
+  const int64_t total = lanes_per_head_group * per_tok;
+  const int threads = few ? 64 : 256;
+  const unsigned grid = blocks_for(total, threads);
   if ((int64_t)grid > kMaxGrid) return fail(IVAKV_E_SHAPE, "ivakv_append: too many rows");
   if (es == 4) {
-    if (vec) append_vec_kernel<uint32_t><<<grid, 256, 0, stream>>>(a);
-    else append_kernel<uint32_t><<<grid, 256, 0, stream>>>(a);
+    if (few) append_vec_kernel<uint32_t, 1><<<grid, threads, 0, stream>>>(a);
+    else if (vec) append_vec_kernel<uint32_t, kAppendHeads><<<grid, threads, 0, stream>>>(a);
+    else append_kernel<uint32_t><<<grid, threads, 0, stream>>>(a);
   } else {
-    if (vec) append_vec_kernel<uint16_t><<<grid, 256, 0, stream>>>(a);
-    else append_kernel<uint16_t><<<grid, 256, 0, stream>>>(a);
+    if (few) append_vec_kernel<uint16_t, 1><<<grid, threads, 0, stream>>>(a);
+    else if (vec) append_vec_kernel<uint16_t, kAppendHeads><<<grid, threads, 0, stream>>>(a);
+    else append_kernel<uint16_t><<<grid, threads, 0, stream>>>(a);
   }
   return launch_status("ivakv_append");
 }
