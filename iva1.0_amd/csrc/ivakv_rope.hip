@@ -53,13 +53,16 @@ struct AppendRopeArgs {
 
 // Lanes rotate up to kRopeHeads kv heads of one (token, chunk): cos / sin depend on the
 // position and the pair only, so they are computed once per lane, not once per head.
+// Few rows (decode steps, short chunks) take one head per lane in 64-thread
+// workgroups (HEADS = 1), spreading the stores over many CUs, as ivakv_append does.
 constexpr int kRopeHeads = 8;
+constexpr int64_t kFewRopeThreads = 1024 * 64;  // below 1024 waves: one head per lane
 
-template <typename E, bool VEC>
+template <typename E, bool VEC, int HEADS>
 __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
   constexpr int X = 16 / sizeof(E);
   const int nch = a.D / X;
-  const int ngrp = cdiv(a.Hkv, kRopeHeads);
+  const int ngrp = cdiv(a.Hkv, HEADS);
   // Thread order (token % 16, chunk, head group, token / 16), as in append_kernel: 16
   // consecutive tokens (consecutive slots of a page in a chunk append) per lane group,
   // so K and V stores coalesce; workgroups in XCD-contiguous order, as append_vec_kernel.
@@ -71,14 +74,14 @@ __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
   const int64_t g1 = gid >> 4;
   const int c = (int)(g1 % nch);
   const int64_t g2 = g1 / nch;
-  const int h0 = (int)(g2 % ngrp) * kRopeHeads;
+  const int h0 = (int)(g2 % ngrp) * HEADS;
   const int64_t t = (g2 / ngrp) * 16 + t_lo;
   if (t >= a.n_tok) return;
   const int64_t slot = a.slots[t];
   if (slot < 0 || slot >= a.n_slots) return;
   const int64_t page = slot / a.bs;
   const int off = (int)(slot - page * a.bs);
-  const int nh = min(kRopeHeads, a.Hkv - h0);
+  const int nh = min(HEADS, a.Hkv - h0);
   const E* __restrict__ kb = static_cast<const E*>(a.k_new) + t * a.kts + (int64_t)c * X;
   const E* __restrict__ vb = static_cast<const E*>(a.v_new) + t * a.vts + (int64_t)c * X;
   E* __restrict__ kp = static_cast<E*>(a.k_pool);
@@ -87,9 +90,9 @@ __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
     Chunk16 c;
     E e[X];
   };
-  E k[kRopeHeads][X], v[kRopeHeads][X];
+  E k[HEADS][X], v[HEADS][X];
 #pragma unroll
-  for (int u = 0; u < kRopeHeads; ++u) {
+  for (int u = 0; u < HEADS; ++u) {
     if (u < nh) {
       if constexpr (VEC) {  // 16-byte source chunks
         Row rk, rv;
@@ -114,7 +117,7 @@ __global__ __launch_bounds__(256) void append_rope_kernel(AppendRopeArgs a) {
 #pragma unroll
   for (int j = 0; j < X / 2; ++j) pair_angle(s_freq, p, c * (X / 2) + j, a.D, a.theta, cs[j], sn[j]);
 #pragma unroll
-  for (int u = 0; u < kRopeHeads; ++u) {
+  for (int u = 0; u < HEADS; ++u) {
     if (u < nh) {
 #pragma unroll
       for (int j = 0; j < X / 2; ++j) rotate_pair(k[u][2 * j], k[u][2 * j + 1], cs[j], sn[j]);
@@ -220,28 +223,31 @@ extern "C" int ivakv_append_rope(const void* k_new, const void* v_new, int64_t k
   AppendRopeArgs a{k_new, v_new, k_tok_stride, k_head_stride, v_tok_stride, v_head_stride,
                    k_pool, v_pool, slot_mapping, positions, n_tok, num_kv_heads, head_dim,
                    block_size, (int64_t)num_pages * block_size, theta};
-  const int64_t total = (int64_t)cdiv(n_tok, 16) * 16 * cdiv(num_kv_heads, kRopeHeads) * (head_dim / X);
-  const int64_t blocks = (total + 255) / 256;
+  const int64_t lanes = (int64_t)cdiv(n_tok, 16) * 16 * (head_dim / X);  // per head group
+  const bool few = lanes * cdiv(num_kv_heads, kRopeHeads) < kFewRopeThreads;
+  const int64_t total = lanes * (few ? num_kv_heads : cdiv(num_kv_heads, kRopeHeads));
+  const int threads = few ? 64 : 256;
+  const int64_t blocks = (total + threads - 1) / threads;
   if (blocks > kMaxGridR) return fail(IVAKV_E_SHAPE, "%s: too many rows", name);
   // 16-byte K / V chunk accesses when every source row and the pools allow them
   const bool vec = aligned16(k_new) && aligned16(v_new) && aligned16(k_pool) && aligned16(v_pool) &&
                    (k_tok_stride % X == 0) && (k_head_stride % X == 0) &&
                    (v_tok_stride % X == 0) && (v_head_stride % X == 0);
   const unsigned g = (unsigned)blocks;
-  switch (dtype) {
-    case IVAKV_F16:
-      if (vec) append_rope_kernel<_Float16, true><<<g, 256, 0, stream>>>(a);
-      else append_rope_kernel<_Float16, false><<<g, 256, 0, stream>>>(a);
-      break;
-    case IVAKV_BF16:
-      if (vec) append_rope_kernel<__bf16, true><<<g, 256, 0, stream>>>(a);
-      else append_rope_kernel<__bf16, false><<<g, 256, 0, stream>>>(a);
-      break;
-    default:
-      if (vec) append_rope_kernel<float, true><<<g, 256, 0, stream>>>(a);
-      else append_rope_kernel<float, false><<<g, 256, 0, stream>>>(a);
-      break;
+#define IVAKV_APPEND_ROPE(E)                                                                     \
+  if (few) {                                                                                     \
+    if (vec) append_rope_kernel<E, true, 1><<<g, threads, 0, stream>>>(a);                       \
+    else append_rope_kernel<E, false, 1><<<g, threads, 0, stream>>>(a);                          \
+  } else {                                                                                       \
+    if (vec) append_rope_kernel<E, true, kRopeHeads><<<g, threads, 0, stream>>>(a);              \
+    else append_rope_kernel<E, false, kRopeHeads><<<g, threads, 0, stream>>>(a);                 \
   }
+  switch (dtype) {
+    case IVAKV_F16: IVAKV_APPEND_ROPE(_Float16); break;
+    case IVAKV_BF16: IVAKV_APPEND_ROPE(__bf16); break;
+    default: IVAKV_APPEND_ROPE(float); break;
+  }
+#undef IVAKV_APPEND_ROPE
   return launch_status(name);
 }
 
