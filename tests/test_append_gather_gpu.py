@@ -190,6 +190,46 @@ def test_geometries(iva, dev, dtype, d, bs):
     run_case(iva, dev, k_new, v_new, slots, lay, need + 5, hkv, d, bs, dtype, canary=0x1234)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=str)
+@pytest.mark.parametrize("rows", [32, 4080, 4096], ids=lambda n: f"{n}rows")
+def test_launch_shapes_around_the_few_row_switch(iva, dev, dtype, rows):
+    """The appends take one kv head per lane below 1024 waves of eight heads per lane
+    (fp16, 8 kv heads, head_dim 128: below 4096 rows) and eight heads per lane above; a
+    decode step's rows (32 sequences, one row each, at random rows of their pages) and
+    chunk appends on both sides of the switch are bit-exact, plain and with RoPE (the
+    RoPE form against rope_ followed by the plain append)."""
+    gen = torch.Generator().manual_seed(rows)
+    hkv, d = 8, 128
+    if rows == 32:
+        lengths = [int(x) for x in torch.randint(1, 300, (32,), generator=gen)]
+    else:
+        lengths = [rows // 2 + 5, rows - rows // 2 - 5]
+    need = sum(-(-n // 16) for n in lengths)
+    lay = iva.workloads.permuted_layout(lengths, need + 3, gen)
+    if rows == 32:  # the last position of each sequence: one row per page
+        slots = torch.cat([lay.slots(b, torch.tensor([n - 1])) for b, n in enumerate(lengths)])
+    else:
+        slots = torch.cat([lay.slots(b, torch.arange(n)) for b, n in enumerate(lengths)])
+    n_tok = slots.numel()
+    k_new = torch.randn(n_tok, hkv, d, generator=gen).to(dtype)
+    v_new = torch.randn(n_tok, hkv, d, generator=gen).to(dtype)
+    k_pool, v_pool = new_pools(iva, dev, need + 3, hkv, d, 16, dtype, 0x1234)
+    iva.kv_append(k_new.to(dev), v_new.to(dev), k_pool, v_pool, slots.to(dev))
+    ok, ov = oracle_pools(need + 3, hkv, d, 16, dtype, 0x1234)
+    orc.append(ok, ov, bits(k_new), bits(v_new), slots.numpy())
+    assert np.array_equal(bits(k_pool), ok) and np.array_equal(bits(v_pool), ov)
+    pos = torch.randint(0, 1 << 15, (n_tok,), generator=gen).to(torch.int32).to(dev)
+    out = []
+    for fused in (True, False):
+        kp, vp = new_pools(iva, dev, need + 3, hkv, d, 16, dtype, 0x1234)
+        if fused:
+            iva.kv_append(k_new.to(dev), v_new.to(dev), kp, vp, slots.to(dev), rope_positions=pos)
+        else:
+            iva.kv_append(iva.rope_(k_new.to(dev).clone(), pos), v_new.to(dev), kp, vp, slots.to(dev))
+        out.append((bits(kp), bits(vp)))
+    assert np.array_equal(out[0][0], out[1][0]) and np.array_equal(out[0][1], out[1][1])
+
+
 def test_decode_appends_and_prefill_chunk(iva, dev):
     """C5-style traffic: one 512-token prefill chunk and one-token decode appends for 32
     sequences, interleaved, on a fp16 Hkv 8 / D 128 pool."""
