@@ -1053,6 +1053,21 @@ def bench_ops(args, iva, torch, dev):
             out.append(pg[p // 16] * 16 + p % 16)
         return torch.cat(out).int().to(dev)
 
+    # a decode step's append (32 sequences, one row each at a random row of its own page)
+    # and one 512-row chunk: the few-row launch shape (one kv head per lane)
+    for name, nr in (("append_decode_step", 32), ("append_chunk512", 512)):
+        sub = [(r[0][:nr].contiguous(), r[1][:nr].contiguous()) for r in rows]
+        if nr == 32:
+            sl = [(perm[20000 + 64 * i: 20000 + 64 * i + 32] * 16
+                   + torch.randint(0, 16, (32,), generator=cpu_gen)).int().to(dev) for i in range(n_app)]
+        else:
+            sl = [s_[:nr] for s_ in slots]
+        timed(name, lambda i, sub=sub, sl=sl: iva.kv_append(sub[i][0], sub[i][1], k_pool, v_pool, sl[i]),
+              append_bytes(nr, hkv, d, es), n_app,
+              extra={"rows": nr, "slots": "one row per sequence, each on its own page" if nr == 32
+                     else "one page-aligned chunk"})
+        del sub, sl
+
     slots_u = [unaligned_slots(i) for i in range(n_app)]
     timed("append_unaligned", lambda i: iva.kv_append(rows[i][0], rows[i][1], k_pool, v_pool,
                                                       slots_u[i]), app_bytes, n_app,
