@@ -169,8 +169,8 @@ int ivakv_decode_attn_merge(const void* q, const void* k_pool, const void* v_poo
  * attended together with positions < L-1 read from the pools.  Same result as
  * ivakv_append of those rows followed by ivakv_decode_attn, in two launches
  * instead of three: the pool walk skips position L-1 and the merge scores the new
- * token straight from k_new.  When the batch has at least one (sequence, kv head)
- * unit per CU of the device and the table holds at most 64 effective pages per
+ * token straight from k_new.  When the batch has one to four (sequence, kv head)
+ * units per CU of the device and the table holds at most 64 effective pages per
  * sequence (max_blocks, or the window and sinks), one launch: a workgroup per unit
  * walks it, merges its waves in LDS, folds in the new token and stores its rows.
  * Workspace: ivakv_decode_workspace_size with partition_pages <= 0 (enough for

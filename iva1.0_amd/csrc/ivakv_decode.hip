@@ -1271,11 +1271,14 @@ int stream_workgroups(int per_cu) {
   return wgs < kMaxStreamWaves / kStreamWaves ? wgs : kMaxStreamWaves / kStreamWaves;
 }
 
-// Fused calls on short tables whose batch has at least one (sequence, kv head)
-// unit per CU take one partition per sequence: a workgroup per unit walks it,
-// merges its waves in LDS, folds the new token and writes out, with no merge
-// kernel (C3's decode shape: 9.9 against 14.9 us for walk + merge).  Returns
-// the partition size for that, or 0 for the stream walk.
+// Fused calls on short tables whose batch has one to four (sequence, kv head) units
+// per CU take one partition per sequence: a workgroup per unit walks it, merges its
+// waves in LDS, folds the new token and writes out, with no merge kernel (C3's
+// decode shape: 9.9 against 14.9 us for walk + merge; 512 units of 32 / 63 pages
+// 28.4 / 49.1 against 32.4 / 52.9 us).  From four units per CU the stream walk's even
+// shares win (1024 units: 54.6 / 94.9 against 57.2 / 98.7 us; 2048: 102.7 / 182.8
+// against 115.8 / 204.0 us).  Returns the partition size for that, or 0 for the
+// stream walk.
 constexpr int kSinglePartitionMaxPages = 64;
 int single_partition_pages(int batch, int num_kv_heads, int max_blocks, int window, int n_sink) {
   const int max_eff = max_effective_pages(max_blocks, window, n_sink, kBS);
@@ -1284,7 +1287,8 @@ int single_partition_pages(int batch, int num_kv_heads, int max_blocks, int wind
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return 0;
-  return (int64_t)batch * num_kv_heads >= cus ? max_eff : 0;
+  const int64_t units = (int64_t)batch * num_kv_heads;
+  return units >= cus && units < 4 * (int64_t)cus ? max_eff : 0;
 }
 
 int decode_entry(Stage stage, const char* name, const void* q, const void* k_pool,
