@@ -239,9 +239,18 @@ def decode_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head
 # query heads x keys, reaches SPLIT_MIN_WORK (enough work that the persistent grid's
 # longest-first order pays for the plan launch: the ragged prefill chunks of a
 # continuous-batching step take 25 % less time split, and 16 x 512 rows at 2048 keys take
-# the same time either way; shorter prefills are 2-11 us slower split).
+# the same time either way; shorter prefills are 2-11 us slower split), or when a walk
+# may pass SPLIT_FEW_BLOCKS_KEYS keys and the single launch would have fewer than
+# SPLIT_FEW_BLOCKS workgroups of 256 query rows (x query heads of a kv head), half the
+# CUs: then most CUs would idle while a few walk the whole context (one sequence, a
+# 128-row chunk at 4096 keys: 148 against 62 us split; a 16-row chunk at 2048 keys: 58
+# against 40 us; four 128-row chunks at 2048 keys, 64 workgroups: 81 against 61 us).
+# With 128-256 such workgroups the single launch stays ahead (four 512-row chunks at
+# 2048 keys: 99 against 125 us), and so it does at 1024 keys (33 against 38 us).
 SPLIT_MIN_KEYS = 4096
 SPLIT_MIN_WORK = 1 << 28
+SPLIT_FEW_BLOCKS_KEYS = 2048
+SPLIT_FEW_BLOCKS = 128
 SPLIT_MAX_BATCH = 2048
 SPLIT_MAX_KV_HEADS = 32767
 
@@ -251,13 +260,18 @@ def prefill_split_default(batch: int, num_q_heads: int, num_kv_heads: int, n_tok
                           window: int = 0, n_sink: int = 0) -> bool:
     """:func:`paged_prefill_attention`'s default for ``split``: within the split path's
     batch and kv-head limits, when the longest walk the table allows (its width in keys,
-    or window + chunk + sinks) exceeds SPLIT_MIN_KEYS, or when query rows x query heads x
-    those keys reaches SPLIT_MIN_WORK."""
+    or window + chunk + sinks) exceeds SPLIT_MIN_KEYS, when query rows x query heads x
+    those keys reaches SPLIT_MIN_WORK, or when that walk reaches SPLIT_FEW_BLOCKS_KEYS
+    and the single launch would have fewer than SPLIT_FEW_BLOCKS row-block workgroups
+    (256 rows of a kv head's query heads each, counted for chunks of max_query_len)."""
     keys = max_blocks * block_size
     if window and window > 0:
         keys = min(keys, window + max_query_len + max(n_sink, 0))
+    group = max(num_q_heads // max(num_kv_heads, 1), 1)
+    row_blocks = batch * num_kv_heads * (-(-max_query_len * group // 256))
     return batch <= SPLIT_MAX_BATCH and num_kv_heads <= SPLIT_MAX_KV_HEADS and (
-        keys > SPLIT_MIN_KEYS or n_tok * num_q_heads * keys >= SPLIT_MIN_WORK)
+        keys > SPLIT_MIN_KEYS or n_tok * num_q_heads * keys >= SPLIT_MIN_WORK
+        or (keys >= SPLIT_FEW_BLOCKS_KEYS and row_blocks < SPLIT_FEW_BLOCKS))
 
 
 def prefill_split_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int,

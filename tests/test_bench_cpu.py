@@ -95,6 +95,15 @@ def test_prefill_split_default(iva):
     assert split(1, 32, 8, 1, 1, 1024, 16)
     # ... unless a window bounds the walk: 256 + 64 + 4 keys
     assert not split(1, 32, 8, 64, 64, 1024, 16, window=256, n_sink=4)
+    # few row blocks on a long walk (one sequence, 128 rows at 4096 keys; 16 rows at 2048
+    # keys; four sequences of 128 rows at 2048 keys) -> split; at 1024 keys -> single launch
+    assert split(1, 32, 8, 128, 128, 256, 16)
+    assert split(1, 32, 8, 16, 16, 128, 16)
+    assert split(4, 32, 8, 4 * 128, 128, 128, 16)
+    assert not split(1, 32, 8, 16, 16, 64, 16)
+    assert not split(16, 32, 8, 16 * 64, 64, 64, 16)
+    # ... and with 256 row-block workgroups (four 512-row chunks at 2048 keys) -> single
+    assert not split(4, 32, 8, 4 * 512, 512, 128, 16)
     # outside the split path's limits -> single launch
     assert not split(ops.SPLIT_MAX_BATCH + 1, 32, 8, 4096, 512, 1024, 16)
     assert not split(4, 32768, 32768, 4, 1, 1024, 16)
