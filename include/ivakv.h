@@ -266,7 +266,8 @@ int ivakv_decode_attn_fp8(const void* q, const void* k_pool, const void* v_pool,
  * to that append's), attended as their dequantized values, and stored into the slot of
  * position L-1; positions < L-1 come from the pools as in ivakv_decode_attn_fp8.  Same
  * result as ivakv_append_fp8 followed by ivakv_decode_attn_fp8, in two launches
- * instead of three.  Workspace, geometry and alignment as ivakv_decode_attn_fp8.
+ * instead of three (one on the batches where ivakv_decode_append_attn takes one).
+ * Workspace, geometry and alignment as ivakv_decode_attn_fp8.
  * Replaces: the append + score sequence of AttentionTorch.forward with a cache
  * (src/core/attention.py:61-102) on a kv_cache_dtype "fp8" cache
  * (configs/quant_infer.yaml:22,52; scaling rule src/quant/fp8_runtime.py:66-76).

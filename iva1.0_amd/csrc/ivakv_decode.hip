@@ -410,10 +410,15 @@ struct TileOps8 {
 // stops overlapping loads with compute.
 // Block table and context lengths come in as __restrict__ parameters, which
 // keeps their reads on the scalar cache (see decode_stream_kernel).
-template <int DT, int D>
+//
+// kFp8: FP8 pools (the fused step's single launch only): tiles through TileOps8, and the
+// new rows quantized as ivakv_append_fp8 does (per-row factor from a wave reduction of
+// max |x|, codes e4m3(x * sf)), attended as their dequantized values and stored as codes
+// and factors, as decode_fused_merge_kernel does on the stream walk.
+template <int DT, int D, bool kFp8 = false>
 __global__ __launch_bounds__(kThreads, partial_wgs_per_cu(D)) void decode_partial_kernel(
     DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ ctx) {
-  using Ops = TileOps<DT, D>;
+  using Ops = typename std::conditional<kFp8, TileOps8<DT, D>, TileOps<DT, D>>::type;
   using E = typename Ops::E;
   constexpr int NB = Ops::NB;
 
@@ -451,14 +456,18 @@ __global__ __launch_bounds__(kThreads, partial_wgs_per_cu(D)) void decode_partia
   const E* qb = static_cast<const E*>(a.q) + ((int64_t)b * Hq + h * G) * D;
   const E* kn = a.fused ? static_cast<const E*>(a.k_new) + row_nh : qb;
   const E* vn = a.fused ? static_cast<const E*>(a.v_new) + row_nh : qb;
-  float kd[DJ], qd[4][DJ];
+  float kd[DJ], qd[4][DJ], vd[kFp8 ? DJ : 1];
 #pragma unroll
   for (int j = 0; j < DJ; ++j) kd[j] = (float)kn[lane + 64 * j];
+  if constexpr (kFp8) {  // the V row's lane-strided dims, for its factor
+#pragma unroll
+    for (int j = 0; j < DJ; ++j) vd[j] = (float)vn[lane + 64 * j];
+  }
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int j = 0; j < DJ; ++j) qd[t][j] = (float)qb[min(wave + 4 * t, G - 1) * D + lane + 64 * j];
-  const float v_own = (float)vn[threadIdx.x % D];
+  float v_own = (float)vn[threadIdx.x % D];
 
   const int v_begin = part * a.part_pages + wave;
   const int v_end = min(min((part + 1) * a.part_pages, w.n_eff), table_pages(w, a.max_blocks));
@@ -518,8 +527,29 @@ __global__ __launch_bounds__(kThreads, partial_wgs_per_cu(D)) void decode_partia
     }
   }
   // Fused: the new token's scores q_g . k_new from the prefetched operands, one
-  // head per wave in turn, a wave reduction each.
+  // head per wave in turn, a wave reduction each.  FP8: every wave first reduces the
+  // new rows' max |x| (NaN kept) to the factors and rounds its operands to the values
+  // the codes decode to.
+  float sfk = 1.f, sfv = 1.f;
   if (a.fused) {
+    if constexpr (kFp8) {
+      float ka = 0.f, va = 0.f;
+#pragma unroll
+      for (int j = 0; j < DJ; ++j) {
+        ka = nan_max(ka, fabsf(kd[j]));
+        va = nan_max(va, fabsf(vd[j]));
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        ka = nan_max(ka, __shfl_xor(ka, o));
+        va = nan_max(va, __shfl_xor(va, o));
+      }
+      sfk = row_sf(ka);
+      sfv = row_sf(va);
+#pragma unroll
+      for (int j = 0; j < DJ; ++j) kd[j] = e4m3_decode(e4m3_encode(kd[j] * sfk)) / sfk;
+      v_own = e4m3_decode(e4m3_encode(v_own * sfv)) / sfv;
+    }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       if (wave + 4 * t >= G) break;
@@ -568,14 +598,28 @@ __global__ __launch_bounds__(kThreads, partial_wgs_per_cu(D)) void decode_partia
   // Fused: the new rows go to the slot of position L-1 (after every wave's reads
   // of that page, which the barriers above order).
   if (new_ok) {
-    constexpr int X = 16 / (int)sizeof(E);
     const int row = (L_ctx - 1) % kBS;
-    const int64_t tile = (new_page * a.Hkv + h) * (int64_t)D * kBS;
-    E* kp = static_cast<E*>(const_cast<void*>(a.k_pool)) + tile;
-    E* vp = static_cast<E*>(const_cast<void*>(a.v_pool)) + tile;
-    for (int d = threadIdx.x; d < D; d += kThreads) {
-      kp[((d / X) * kBS + row) * X + d % X] = kn[d];
-      vp[d * kBS + row] = vn[d];
+    if constexpr (kFp8) {
+      const int64_t tile = new_page * a.Hkv + h;
+      uint8_t* kp = static_cast<uint8_t*>(const_cast<void*>(a.k_pool)) + tile * D * kBS;
+      uint8_t* vp = static_cast<uint8_t*>(const_cast<void*>(a.v_pool)) + tile * D * kBS;
+      for (int d = threadIdx.x; d < D; d += kThreads) {
+        kp[((d >> 4) * kBS + row) * 16 + (d & 15)] = (uint8_t)e4m3_encode((float)kn[d] * sfk);
+        vp[fp8_v_offset(d, row, D)] = (uint8_t)e4m3_encode((float)vn[d] * sfv);
+      }
+      if (threadIdx.x == 0) {
+        const_cast<float*>(a.k_scale)[tile * kBS + row] = sfk;
+        const_cast<float*>(a.v_scale)[tile * kBS + row] = sfv;
+      }
+    } else {
+      constexpr int X = 16 / (int)sizeof(E);
+      const int64_t tile = (new_page * a.Hkv + h) * (int64_t)D * kBS;
+      E* kp = static_cast<E*>(const_cast<void*>(a.k_pool)) + tile;
+      E* vp = static_cast<E*>(const_cast<void*>(a.v_pool)) + tile;
+      for (int d = threadIdx.x; d < D; d += kThreads) {
+        kp[((d / X) * kBS + row) * X + d % X] = kn[d];
+        vp[d * kBS + row] = vn[d];
+      }
     }
   }
 }
@@ -1196,12 +1240,12 @@ int make_plan(const char* name, Stage stage, int batch, int num_q_heads, int num
   return IVAKV_OK;
 }
 
-template <int DT>
+template <int DT, bool kFp8 = false>
 void launch_partial(int D, dim3 grid, size_t smem, hipStream_t stream, const DecodeArgs& a) {
   switch (D) {
-    case 64: decode_partial_kernel<DT, 64><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
-    case 128: decode_partial_kernel<DT, 128><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
-    default: decode_partial_kernel<DT, 256><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+    case 64: decode_partial_kernel<DT, 64, kFp8><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+    case 128: decode_partial_kernel<DT, 128, kFp8><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
+    default: decode_partial_kernel<DT, 256, kFp8><<<grid, kThreads, smem, stream>>>(a, a.bt, a.ctx); break;
   }
 }
 
@@ -1308,7 +1352,7 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
     if (batch > 0 && (!k_scale || !v_scale || !aligned16(k_scale) || !aligned16(v_scale)))
       return fail(IVAKV_E_ARG, "%s: k_scale / v_scale must be 16-byte aligned device pointers", name);
   }
-  if (stage == kFused && !fp8 && partition_pages <= 0 && block_size == kBS && n_sink >= 0)
+  if (stage == kFused && partition_pages <= 0 && block_size == kBS && n_sink >= 0)
     partition_pages = single_partition_pages(batch, num_kv_heads, max_blocks, window, n_sink);
   Plan plan;
   int st = make_plan(name, stage, batch, num_q_heads, num_kv_heads, head_dim, block_size,
@@ -1384,6 +1428,11 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
     dim3 grid((unsigned)num_kv_heads, (unsigned)batch, (unsigned)plan.n_parts_max);
     const size_t smem =
         sizeof(float) * (2 * kWaves * 16 + 32 + (size_t)kWaves * plan.G * (head_dim + 4) + 16);
+    if (fp8) {  // the fused step's single launch (FP8 pools take no partitions otherwise)
+      if (dtype == IVAKV_F16) launch_partial<IVAKV_F16, true>(head_dim, grid, smem, stream, a);
+      else launch_partial<IVAKV_BF16, true>(head_dim, grid, smem, stream, a);
+      return launch_status(name);
+    }
     switch (dtype) {
       case IVAKV_F16: launch_partial<IVAKV_F16>(head_dim, grid, smem, stream, a); break;
       case IVAKV_BF16: launch_partial<IVAKV_BF16>(head_dim, grid, smem, stream, a); break;

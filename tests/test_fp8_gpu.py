@@ -290,18 +290,22 @@ def test_decode_fp8_vs_oracle(iva, dev, qdt, d, window, sink):
 
 @pytest.mark.parametrize("qdt", [torch.float16, torch.bfloat16], ids=str)
 @pytest.mark.parametrize("d", [64, 128, 256])
-@pytest.mark.parametrize("window,sink,many", [(0, 0, False), (70, 4, False), (0, 0, True)])
+@pytest.mark.parametrize("window,sink,many", [(0, 0, False), (70, 4, False), (0, 0, True),
+                                               (0, 0, "mid"), (70, 4, "mid")])
 def test_decode_append_fp8_fused_vs_oracle(iva, dev, qdt, d, window, sink, many):
     """The fused op on FP8 pages: pools and factors afterwards byte-identical to the
     oracle's append of the new rows (the same quantization as kv_append), output within
     2e-3 of the oracle's decode over the dequantized pages.  An empty sequence (zero
     row, nothing stored), a sequence of one token (the new token alone) and a new token
     whose page id is invalid (neither stored nor attended).  ``many``: 136 sequences x 8
-    kv heads (>= 1024 units: the merge with four output elements per thread)."""
+    kv heads (>= 1024 units: the merge with four output elements per thread); "mid": 40
+    sequences x 8 kv heads on tables of at most 33 pages (one to four units per CU: the
+    single launch, each unit walked and merged by one workgroup)."""
     lengths = [0, 1, 16, 17, 100, 257, 513]
     hq, hkv = 8, 2
     if many:
-        lengths = lengths + torch.randint(2, 60, (129,), generator=torch.Generator().manual_seed(3)).tolist()
+        extra = 129 if many is True else 33
+        lengths = lengths + torch.randint(2, 60, (extra,), generator=torch.Generator().manual_seed(3)).tolist()
         hq, hkv = 32, 8
     c = fp8_case(iva, lengths, hkv, d, torch.float32, seed=31 + d, decades=0)
     offs = np.cumsum([0] + lengths[:-1]).tolist()
