@@ -1352,7 +1352,10 @@ int decode_entry(Stage stage, const char* name, const void* q, const void* k_poo
     if (batch > 0 && (!k_scale || !v_scale || !aligned16(k_scale) || !aligned16(v_scale)))
       return fail(IVAKV_E_ARG, "%s: k_scale / v_scale must be 16-byte aligned device pointers", name);
   }
-  if (stage == kFused && partition_pages <= 0 && block_size == kBS && n_sink >= 0)
+  // The single launch for a full decode too (attention alone, the same kernel with no new
+  // token): 256 units of 32 pages 18.3 -> 14.4 us, C3's layer shape 14.1 -> 9.8 us.
+  if ((stage == kFused || stage == kFull) && partition_pages <= 0 && block_size == kBS &&
+      n_sink >= 0)
     partition_pages = single_partition_pages(batch, num_kv_heads, max_blocks, window, n_sink);
   Plan plan;
   int st = make_plan(name, stage, batch, num_q_heads, num_kv_heads, head_dim, block_size,
