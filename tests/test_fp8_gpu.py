@@ -267,10 +267,17 @@ def test_all_codes_decode_as_torch(iva, dev):
 
 @pytest.mark.parametrize("qdt", [torch.float16, torch.bfloat16], ids=str)
 @pytest.mark.parametrize("d", [64, 128, 256])
-@pytest.mark.parametrize("window,sink", [(0, 0), (70, 4)])
-def test_decode_fp8_vs_oracle(iva, dev, qdt, d, window, sink):
+@pytest.mark.parametrize("window,sink,units", [(0, 0, "few"), (70, 4, "few"), (0, 0, "mid"),
+                                                (70, 4, "mid")])
+def test_decode_fp8_vs_oracle(iva, dev, qdt, d, window, sink, units):
+    """FP8 decode attention against the oracle on the dequantized pages; "mid": 40
+    sequences x 8 kv heads on tables of at most 33 pages (one to four units per CU: one
+    partition per sequence in a single launch), else a few units (the stream walk)."""
     lengths = [1, 16, 17, 100, 257, 513]
     hq, hkv = 8, 2
+    if units == "mid":
+        lengths = lengths + torch.randint(2, 60, (34,), generator=torch.Generator().manual_seed(4)).tolist()
+        hq, hkv = 32, 8
     c = fp8_case(iva, lengths, hkv, d, torch.float32, seed=11 + d, decades=0)
     g, o = append_both(iva, dev, c)
     lay = c["layout"]
