@@ -10,7 +10,8 @@
     the dequantized pages, fp16 and bf16 queries, windows and sinks, invalid page ids,
     garbage (NaN included) codes past the context;
   * the fused append + attend op on FP8 pages: pools and factors byte-identical to
-    the oracle's append of the new rows, output within the same bound;
+    the oracle's append of the new rows (inf, NaN and out-of-range rows included, on
+    each walk), output within the same bound;
   * chunked prefill over FP8 pages vs the oracle's prefill on the dequantized pages.
 """
 from __future__ import annotations
@@ -351,6 +352,68 @@ def test_decode_append_fp8_fused_vs_oracle(iva, dev, qdt, d, window, sink, many)
     bound = 2e-3 + OUT_ULP[qdt] * np.abs(ref)
     assert (err <= bound).all(), f"max err {err.max():.3e}"
     assert not out[0].any()                      # empty sequence
+
+
+@pytest.mark.parametrize("qdt", [torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("walk", ["stream", "many", "single"])
+def test_decode_append_fp8_fused_rows_beyond_the_scaled_range(iva, dev, qdt, walk):
+    """New rows that leave e4m3's range under their factor, through the fused op: an inf
+    and a -inf element, NaN elements, a row times 1e12 (bf16: factor clamped to 1e-8;
+    fp16: the row overflows to inf) and rows times 1e-9, on the last kv head of five
+    sequences.  The codes and factors stored equal the oracle's append of the same rows
+    (the quantization ivakv_append_fp8 applies); every other (sequence, kv head) unit's
+    output stays within 2e-3 of the oracle's decode.  Walks: "stream" (a few units: the
+    stream walk and its fused merge), "many" (>= 1024 units: the four-element merge),
+    "single" (40 sequences x 8 kv heads on short tables: one launch per step)."""
+    lengths = [0, 1, 16, 17, 100, 257, 513]
+    hq, hkv = 8, 2
+    if walk != "stream":
+        extra = 129 if walk == "many" else 33
+        lengths = lengths + torch.randint(2, 60, (extra,), generator=torch.Generator().manual_seed(3)).tolist()
+        hq, hkv = 32, 8
+    c = fp8_case(iva, lengths, hkv, 128, torch.float32, seed=71, decades=0)
+    offs = np.cumsum([0] + lengths[:-1]).tolist()
+    prev = torch.cat([torch.arange(o, o + n - 1) for o, n in zip(offs, lengths) if n > 1])
+    g, o = append_both(iva, dev, dict(c, k_new=c["k_new"][prev], v_new=c["v_new"][prev],
+                                      slots=c["slots"][prev]))
+    lay = c["layout"]
+    bt, ctx = lay.block_tables, lay.context_lens
+    kn = torch.zeros(len(lengths), hkv, 128)
+    vn = torch.zeros(len(lengths), hkv, 128)
+    step_slots = torch.full((len(lengths),), -1, dtype=torch.int32)
+    for b, (off, n) in enumerate(zip(offs, lengths)):
+        if n:
+            kn[b], vn[b] = c["k_new"][off + n - 1], c["v_new"][off + n - 1]
+            step_slots[b] = int(bt[b, (n - 1) // 16]) * 16 + (n - 1) % 16
+    hx = hkv - 1
+    kn[2, hx, 5] = math.inf
+    vn[3, hx, 9] = -math.inf
+    kn[5, hx, 7] = math.nan
+    vn[5, hx, 0] = math.nan
+    kn[6, hx] *= 1e12
+    vn[6, hx, 3] = math.nan
+    kn[1, hx] *= 1e-9
+    vn[4, hx] *= 1e-9
+    kn, vn = kn.to(qdt), vn.to(qdt)
+    q = (torch.randn(len(lengths), hq, 128, generator=torch.Generator().manual_seed(8)) * 128 ** -0.5).to(qdt)
+    out = iva.paged_decode_append_attention(q.to(dev), kn.to(dev), vn.to(dev), g["k_pool"],
+                                            g["v_pool"], bt.to(dev), ctx.to(dev),
+                                            k_scale=g["k_scale"], v_scale=g["v_scale"])
+    orc.append_fp8(o["k_pool"], o["v_pool"], o["k_scale"], o["v_scale"], kn.float().numpy(),
+                   vn.float().numpy(), step_slots.numpy())
+    assert np.array_equal(u8(g["k_pool"]), o["k_pool"]) and np.array_equal(u8(g["v_pool"]), o["v_pool"])
+    assert np.array_equal(g["k_scale"].cpu().numpy(), o["k_scale"])
+    assert np.array_equal(g["v_scale"].cpu().numpy(), o["v_scale"])
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = orc.decode_attention_fp8(q.float().numpy(), o["k_pool"], o["v_pool"], o["k_scale"],
+                                       o["v_scale"], bt.numpy(), ctx.numpy())
+    got = out.float().cpu().numpy()
+    G = hq // hkv
+    checked = np.ones(got.shape[:2], dtype=bool)
+    checked[[2, 3, 5, 6], hx * G:(hx + 1) * G] = False   # units whose new rows are not finite
+    err = np.abs(got - ref)[checked]
+    bound = 2e-3 + OUT_ULP[qdt] * np.abs(ref[checked])
+    assert (err <= bound).all(), f"max err {err.max():.3e}"
 
 
 @pytest.mark.parametrize("qdt", [torch.float16, torch.bfloat16], ids=str)
