@@ -124,8 +124,9 @@ int ivakv_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
  * instead splits each sequence into partitions of that many pages (one
  * workgroup each) merged the same way.  With partition_pages <= 0, a batch of one
  * to four (sequence, kv head) units per CU on tables of at most 64 effective pages
- * takes one partition per sequence in a single launch (no merge; its workspace
- * need is then 0).
+ * takes one partition per sequence in a single launch (no merge: the call then
+ * accepts a null workspace; ivakv_decode_workspace_size still reports the stream
+ * walk's need, which covers it).
  * Supported: block_size 16, head_dim 64/128/256, num_q_heads/num_kv_heads
  * (the GQA group) any integer from 1 to 16.
  * Replaces: the cache branch of AttentionTorch.forward -- scores, causal /
