@@ -1120,7 +1120,24 @@ def bench_ops(args, iva, torch, dev):
     timed("gather", lambda i: iva.kv_gather(gsets[i][0], gsets[i][1], gsets[i][2], gsets[i][3],
                                             out_len=lmax, out=(gsets[i][4], gsets[i][5])),
           2 * sum(lengths) * hkv * d * es + 2 * gsets[0][4].numel() * es, n_ga)
+    # the same batch from FP8 pages (codes and factors of each attended row read,
+    # dequantized into fp16 outputs)
+    f8sets = []
+    for i in range(n_ga):
+        k_p, v_p, bt_, ctx_, kg, vg = gsets[i]
+        f8 = [torch.randint(0, 256, s_, dtype=torch.uint8, generator=gen, device=dev)
+              .view(torch.float8_e4m3fn) for s_ in iva.pool_shapes(k_p.shape[0], hkv, d, 16,
+                                                                   torch.float8_e4m3fn)]
+        sc = [torch.rand(iva.scale_shape(k_p.shape[0], hkv), generator=gen, device=dev) + 0.5
+              for _ in range(2)]
+        f8sets.append((f8[0], f8[1], sc[0], sc[1], bt_, ctx_, kg, vg))
     del gsets
+    timed("gather_fp8", lambda i: iva.kv_gather(
+        f8sets[i][0], f8sets[i][1], f8sets[i][4], f8sets[i][5], out_len=lmax,
+        out=(f8sets[i][6], f8sets[i][7]), k_scale=f8sets[i][2], v_scale=f8sets[i][3]),
+        2 * sum(lengths) * hkv * (d + 4) + 2 * f8sets[0][6].numel() * es, n_ga,
+        extra={"pages": "fp8", "out_dtype": "f16"})
+    del f8sets
     # kv_ops' index kernels on a contiguous cache: gather 1024 positions, scatter 1024
     # rows, through the C ABI on preallocated buffers (kv_ops itself checks the indices
     # on the host, a synchronisation per call, and its scatter copies the whole cache

@@ -230,20 +230,67 @@ def test_append_fp8_from_unaligned_strided_rows(iva, dev, src, rope):
 
 
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16], ids=str)
-def test_gather_fp8_exact(iva, dev, out_dtype):
-    c = fp8_case(iva, [17, 40, 3, 0], 2, 128, torch.float16, seed=3)
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("out_len,outputs", [(48, "aligned"), (45, "aligned"), (48, "offset")])
+def test_gather_fp8_exact(iva, dev, out_dtype, d, out_len, outputs):
+    """Dequantized rows equal the oracle's (code / factor in float32, then the output
+    cast), zero past the context and on an invalid page; out_len 45 ends inside a page.
+    "offset": outputs that are views 4-8 bytes into a buffer (not 16-byte aligned: the
+    element-wise kernel), else the 16-byte chunk kernel."""
+    c = fp8_case(iva, [17, 40, 3, 0], 2, d, torch.float16, seed=3 + d)
     g, o = append_both(iva, dev, c)
     lay = c["layout"]
     bt = lay.block_tables.clone()
     bt[1, 1] = -1
+    out = None
+    if outputs == "offset":
+        shape = (4, 2, out_len, d)
+        n = 4 * 2 * out_len * d
+        bufs = [torch.full((n + 8,), 7.0, dtype=out_dtype, device=dev) for _ in range(2)]
+        out = tuple(b_[2:2 + n].view(shape) for b_ in bufs)
+        assert all(t.data_ptr() % 16 for t in out)
     ko, vo = iva.kv_gather(g["k_pool"], g["v_pool"], bt.to(dev), lay.context_lens.to(dev),
-                           out_len=48, k_scale=g["k_scale"], v_scale=g["v_scale"],
+                           out_len=out_len, out=out, k_scale=g["k_scale"], v_scale=g["v_scale"],
                            out_dtype=out_dtype)
     rk, rv = orc.gather_fp8(o["k_pool"], o["v_pool"], o["k_scale"], o["v_scale"], bt.numpy(),
-                            lay.context_lens.numpy(), out_len=48)
+                            lay.context_lens.numpy(), out_len=out_len)
     exp_k = torch.from_numpy(rk).to(out_dtype)
     exp_v = torch.from_numpy(rv).to(out_dtype)
     assert torch.equal(ko.cpu(), exp_k) and torch.equal(vo.cpu(), exp_v)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16], ids=str)
+def test_gather_fp8_quotients_are_ieee(iva, dev, out_dtype):
+    """Every code over factors spread log-uniformly on [2^-120, 2^120] and at chosen
+    points (powers of two and their float neighbours, negative factors, 1e-8, 1e8):
+    through the 16-byte chunk kernel the gathered values are float32 code / factor
+    rounded once, bit for bit, then cast; NaN codes stay NaN."""
+    pages, d = 96, 256
+    ks, vs = iva.pool_shapes(pages, 1, d, 16, FP8)
+    g = torch.Generator().manual_seed(12)
+    n = pages * 16 * d
+    kb = ((torch.arange(n) * 5 + torch.arange(n) // 4096) % 256).to(torch.uint8).reshape(ks)
+    vb = ((torch.arange(n) * 7 + torch.arange(n) // 4096) % 256).to(torch.uint8).reshape(vs)
+    sf = (2.0 ** (torch.rand(pages, 1, 16, generator=g, dtype=torch.float64) * 240 - 120)).float()
+    edge = np.float32(2.0 ** 100)
+    specials = [2.0 ** -100, np.nextafter(np.float32(2.0 ** -100), np.float32(0)), 2.0 ** 100,
+                np.nextafter(edge, np.float32(np.inf)), -(2.0 ** -100), -3.0, -(2.0 ** 100),
+                1e-8, 1e8, 1.0, 448 / 3.3, 2.0 ** -120, 2.0 ** 120, 0.7, 1.5, 3.0]
+    sf[0, 0, :] = torch.tensor(specials, dtype=torch.float32)
+    vsf = sf.flip(0).contiguous()
+    bt = torch.arange(pages, dtype=torch.int32).reshape(pages, 1)
+    ctx = torch.full((pages,), 16, dtype=torch.int32)
+    ko, vo = iva.kv_gather(kb.view(FP8).to(dev), vb.view(FP8).to(dev), bt.to(dev), ctx.to(dev),
+                           out_len=16, k_scale=sf.to(dev), v_scale=vsf.to(dev),
+                           out_dtype=out_dtype)
+    rk, rv = orc.gather_fp8(kb.numpy(), vb.numpy(), sf.numpy(), vsf.numpy(), bt.numpy(),
+                            ctx.numpy(), out_len=16)
+    bits = torch.int32 if out_dtype == torch.float32 else torch.int16
+    for got, ref in ((ko.cpu(), rk), (vo.cpu(), rv)):
+        exp = torch.from_numpy(ref).to(out_dtype)
+        nan = torch.isnan(exp)
+        assert torch.equal(torch.isnan(got), nan)
+        assert torch.equal(got[~nan].view(bits), exp[~nan].view(bits))
 
 
 def test_all_codes_decode_as_torch(iva, dev):
