@@ -242,7 +242,8 @@ int ivakv_append_fp8(const void* k_new, const void* v_new, int64_t k_tok_stride,
 /*
  * ivakv_gather_fp8: ivakv_gather for FP8 pools, dequantized (code / sf) into outputs of
  * dtype `dtype` (f32 / f16 / bf16, [batch][Hkv][out_len][D] dense); zero past the
- * context or on an invalid page id.
+ * context or on an invalid page id.  16-byte aligned pools and outputs take a kernel
+ * that moves 16-element chunks; any other alignment an element-wise one (same values).
  */
 int ivakv_gather_fp8(const void* k_pool, const void* v_pool, const float* k_scale,
                      const float* v_scale, const int32_t* block_tables,
