@@ -268,36 +268,38 @@ struct alignas(16) Out16 {
   E e[16];
 };
 
-// The same gather on 16-byte aligned pools and outputs: grid (position block of 16, kv
-// head, sequence), D threads.  Thread t takes row t / (D/16) and 16-dim chunk t % (D/16)
-// of the block's K and of its V: the K chunk is one 16-byte load (the K tile order keeps
+// The same gather on 16-byte aligned pools and outputs: grid (position block of 16, group
+// of H kv heads, sequence), H x D threads, D per kv head.  Thread t of a head takes row
+// t / (D/16) and 16-dim chunk t % (D/16) of the block's K and of its V: the K chunk is one 16-byte load (the K tile order keeps
 // a row's chunk contiguous); the V tile (16 x D codes in the FP8 V order) is staged in
 // LDS with one 16-byte load per thread and read back in row order.  All loads of a thread
 // are issued before the barrier.  Codes are decoded and divided by the row's factor in
 // float32, as gather8_kernel does, and each chunk is stored as 16 contiguous outputs
 // (consecutive threads: consecutive chunks of a row, so a wave stores whole rows).
 // Rows past the context or on an invalid page are stored as zeros without loads.
-// (C2's batch into fp16: 279 -> 164 us.  The gather is bound by its zero-padded output:
+// (C2's batch into fp16: 279 -> 154 us.  The gather is bound by its zero-padded output:
 // one reciprocal per row with an FMA correction per element instead of the division
 // measured 159 us, a bare multiply 158 us.)
-template <typename E, int D>
-__global__ __launch_bounds__(256) void gather8_vec_kernel(Gather8Args a) {
+template <typename E, int D, int H>
+__global__ __launch_bounds__(1024) void gather8_vec_kernel(Gather8Args a) {
   constexpr int NC = D / 16;
   constexpr int64_t kTile = 16 * D;
-  __shared__ uint4 s_v[D];  // the V tile: D 16-byte chunks
-  const int blk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  __shared__ uint4 s_v[H][D];  // the V tiles: D 16-byte chunks per kv head
+  const int blk = blockIdx.x, b = blockIdx.z;
+  const int hl = threadIdx.x / D, t = threadIdx.x - hl * D;
+  const int h = blockIdx.y * H + hl;
   const int L = a.ctx[b];
   const int64_t page = blk < a.max_blocks ? (int64_t)a.bt[(int64_t)b * a.max_blocks + blk] : -1;
-  const bool page_ok = page >= 0 && page < a.num_pages;
-  const int64_t tile = (page_ok ? page : 0) * a.Hkv + h;
-  const int rows = min(16, a.out_len - blk * 16);
-  const int live = page_ok ? max(0, min(rows, L - blk * 16)) : 0;  // workgroup-uniform
-  const int t = threadIdx.x, r = t / NC, c = t - r * NC;
+  const bool page_ok = page >= 0 && page < a.num_pages && h < a.Hkv;
+  const int64_t tile = (page_ok ? page * a.Hkv + h : 0);
+  const int rows = h < a.Hkv ? min(16, a.out_len - blk * 16) : 0;
+  const int live = page_ok ? max(0, min(rows, L - blk * 16)) : 0;  // uniform per kv head
+  const int r = t / NC, c = t - r * NC;
   const bool has = r < live;
   uint4 kw = make_uint4(0, 0, 0, 0);
   float ksf = 1.f, vsf = 1.f;
   if (live > 0) {
-    s_v[t] = reinterpret_cast<const uint4*>(a.v_pool + tile * kTile)[t];
+    s_v[hl][t] = reinterpret_cast<const uint4*>(a.v_pool + tile * kTile)[t];
     if (has) {
       kw = *reinterpret_cast<const uint4*>(a.k_pool + tile * kTile + (c * 16 + r) * 16);
       ksf = a.k_scale[tile * 16 + r];
@@ -306,7 +308,7 @@ __global__ __launch_bounds__(256) void gather8_vec_kernel(Gather8Args a) {
   }
   __syncthreads();
   if (r >= rows) return;
-  const uint8_t* sv = reinterpret_cast<const uint8_t*>(s_v);
+  const uint8_t* sv = reinterpret_cast<const uint8_t*>(s_v[hl]);
   const uint8_t* kb = reinterpret_cast<const uint8_t*>(&kw);
   Out16<E> ko, vo;
 #pragma unroll
@@ -325,6 +327,10 @@ __global__ __launch_bounds__(256) void gather8_vec_kernel(Gather8Args a) {
 using namespace ivakv;
 
 namespace {
+
+// kv heads per workgroup of the FP8 gather (C2's batch: 1 / 2 / 4 / 8 heads 165 / 157 /
+// 154 / 166 us)
+constexpr int kGather8Heads = 4;
 
 // Shared checks and launch of the two FP8 appends (positions == nullptr: no RoPE).
 constexpr int kFewAppend8Tokens = 512;
@@ -442,11 +448,13 @@ extern "C" int ivakv_gather_fp8(const void* k_pool, const void* v_pool, const fl
                 num_pages, out_len, k_out, v_out};
   const dim3 grid((unsigned)cdiv(out_len, 16), (unsigned)num_kv_heads, (unsigned)batch);
   if (aligned16(k_pool) && aligned16(v_pool) && aligned16(k_out) && aligned16(v_out)) {
+    constexpr int kH = kGather8Heads;
+    const dim3 vgrid((unsigned)cdiv(out_len, 16), (unsigned)cdiv(num_kv_heads, kH), (unsigned)batch);
 #define IVAKV_GATHER8_VEC(E)                                                                \
   switch (head_dim) {                                                                       \
-    case 64: gather8_vec_kernel<E, 64><<<grid, 64, 0, stream>>>(a); break;                  \
-    case 128: gather8_vec_kernel<E, 128><<<grid, 128, 0, stream>>>(a); break;               \
-    default: gather8_vec_kernel<E, 256><<<grid, 256, 0, stream>>>(a); break;                \
+    case 64: gather8_vec_kernel<E, 64, kH><<<vgrid, 64 * kH, 0, stream>>>(a); break;        \
+    case 128: gather8_vec_kernel<E, 128, kH><<<vgrid, 128 * kH, 0, stream>>>(a); break;     \
+    default: gather8_vec_kernel<E, 256, kH><<<vgrid, 256 * kH, 0, stream>>>(a); break;      \
   }
     switch (dtype) {
       case IVAKV_F16: IVAKV_GATHER8_VEC(_Float16); break;

@@ -234,10 +234,12 @@ def test_append_fp8_from_unaligned_strided_rows(iva, dev, src, rope):
 @pytest.mark.parametrize("out_len,outputs", [(48, "aligned"), (45, "aligned"), (48, "offset")])
 def test_gather_fp8_exact(iva, dev, out_dtype, d, out_len, outputs):
     """Dequantized rows equal the oracle's (code / factor in float32, then the output
-    cast), zero past the context and on an invalid page; out_len 45 ends inside a page.
+    cast), zero past the context and on an invalid page; out_len 45 ends inside a page
+    (on 5 kv heads: a group of four and a group of one in the chunk kernel's workgroups).
     "offset": outputs that are views 4-8 bytes into a buffer (not 16-byte aligned: the
     element-wise kernel), else the 16-byte chunk kernel."""
-    c = fp8_case(iva, [17, 40, 3, 0], 2, d, torch.float16, seed=3 + d)
+    hkv = 5 if out_len == 45 else 2
+    c = fp8_case(iva, [17, 40, 3, 0], hkv, d, torch.float16, seed=3 + d)
     g, o = append_both(iva, dev, c)
     lay = c["layout"]
     bt = lay.block_tables.clone()
