@@ -988,7 +988,8 @@ def bench_ops(args, iva, torch, dev):
     """The hot path's data-movement kernels at realistic sizes (fp16, 8 kv heads, D 128),
     each as average time over back-to-back launches captured in one HIP graph: the append of
     16 x 512-token chunks (8192 rows; plain and with RoPE fused, into 16-bit and into FP8
-    pages), the gather of the C2 batch into contiguous K/V, the kv_ops index gather /
+    pages), the gather of the C2 batch into contiguous K/V (from 16-bit and from FP8
+    pages), the kv_ops index gather /
     scatter kernels on a [32, 8, 4096, 128] cache, and the compaction's page moves (4096
     pages).  Every kernel's launches cycle through independent input and output sets
     (>= 512 MiB of distinct source bytes in all), so the 256 MiB MALL cannot serve a
