@@ -174,7 +174,8 @@ def bits_t(t: torch.Tensor) -> torch.Tensor:
 
 
 @pytest.mark.parametrize("dtype,d,bs", [(torch.float16, 8, 16), (torch.float16, 128, 16),
-                                        (torch.float16, 256, 16), (torch.float32, 4, 8),
+                                        (torch.float16, 256, 16), (torch.bfloat16, 64, 16),
+                                        (torch.float32, 4, 8),
                                         (torch.bfloat16, 64, 32), (torch.float32, 128, 1),
                                         (torch.float16, 72, 5)])
 def test_geometries(iva, dev, dtype, d, bs):
